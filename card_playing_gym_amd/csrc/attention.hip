@@ -1,0 +1,366 @@
+// Ragged GQA decode attention read straight from the KV pool.
+//
+// Replaces the gather + masked-softmax path of DecoderBlock.forward_ragged
+// (cardgym/nn/trunk.py:216-256) and the fp16 / span<=64 CUDA op
+// (cardgym/nn/cuda_decode.py:46-151).  Semantics: query t of sequence b, head hd, sees
+// keys k < min(key_lengths[b] + t, span) of cache row rows[b], KV head hd / G; scores are
+// q.k * scale, softmax in fp32, output sum_k p_k v_k.
+//
+// Layout of the work (gfx950, wave64):
+//   * one workgroup per (sequence, KV head): the group's G query heads and all of the
+//     sequence's new tokens share every K/V byte the workgroup reads, so the pool is read
+//     once per (sequence, KV head) whatever G and T are;
+//   * WAVES waves split the key range in 64-key blocks (wave w takes blocks w, w+WAVES..);
+//   * inside a wave, lane = 4 * slot + e: slot (16 of them) owns keys 16 r + slot of each
+//     block (r = 0..3), e owns head_dim / 4 consecutive dims.  A wave-wide load of one r
+//     reads 16 consecutive keys = one contiguous 16 x head_dim segment of the row;
+//   * each lane keeps its own running max / sum / accumulator per query (no cross-lane
+//     traffic in the key loop except the 2-step quad reduction of the dot products); the
+//     16 slots and the waves are merged once at the end (log-sum-exp merge);
+//   * softmax in base 2 with log2(e) folded into the query scale.
+#include "attention.h"
+#include "common.h"
+
+namespace cg {
+namespace {
+
+// DPP quad permutations: lane i of each group of 4 reads lane i^1 / i^2.
+__device__ __forceinline__ float quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
+// Loads N consecutive elements of T as wide vectors and widens them to fp32.
+template <typename T, int N>
+__device__ __forceinline__ void load_widen(const T *__restrict__ p, float (&out)[N]) {
+  constexpr int BYTES = N * int(sizeof(T));
+  T tmp[N];
+  if constexpr (BYTES % 16 == 0) {
+    uint4 raw[BYTES / 16];
+#pragma unroll
+    for (int i = 0; i < BYTES / 16; ++i) raw[i] = reinterpret_cast<const uint4 *>(p)[i];
+    __builtin_memcpy(tmp, raw, BYTES);
+  } else if constexpr (BYTES % 8 == 0) {
+    uint2 raw[BYTES / 8];
+#pragma unroll
+    for (int i = 0; i < BYTES / 8; ++i) raw[i] = reinterpret_cast<const uint2 *>(p)[i];
+    __builtin_memcpy(tmp, raw, BYTES);
+  } else if constexpr (BYTES % 4 == 0) {
+    uint32_t raw[BYTES / 4];
+#pragma unroll
+    for (int i = 0; i < BYTES / 4; ++i) raw[i] = reinterpret_cast<const uint32_t *>(p)[i];
+    __builtin_memcpy(tmp, raw, BYTES);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) tmp[i] = p[i];
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(tmp[i]);
+}
+
+__device__ __forceinline__ float load_any(const void *p, int dtype, int64_t i) {
+  switch (dtype) {
+    case CG_BF16:
+      return to_f32(static_cast<const bf16 *>(p)[i]);
+    case CG_F16:
+      return to_f32(static_cast<const f16 *>(p)[i]);
+    default:
+      return static_cast<const float *>(p)[i];
+  }
+}
+
+__device__ __forceinline__ void store_any(void *p, int dtype, int64_t i, float v) {
+  switch (dtype) {
+    case CG_BF16:
+      static_cast<bf16 *>(p)[i] = from_f32<bf16>(v);
+      break;
+    case CG_F16:
+      static_cast<f16 *>(p)[i] = from_f32<f16>(v);
+      break;
+    default:
+      static_cast<float *>(p)[i] = v;
+  }
+}
+
+constexpr int KEYS_PER_BLOCK = 64;
+constexpr int QB = 4;  // queries per pass over the keys
+constexpr float NEG_BIG = -1.0e30f;
+
+template <typename TKV, int D, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(AttnArgs a) {
+  constexpr int DPL = D / 4;
+  __shared__ float merge_m[WAVES][QB], merge_l[WAVES][QB];
+  __shared__ float merge_acc[WAVES][QB][D];
+
+  const int unit = blockIdx.x;
+  const int b = unit / a.kv_heads, h = unit % a.kv_heads;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = lane >> 2, e = lane & 3;
+  const int G = a.n_heads / a.kv_heads;
+
+  const int64_t row = a.rows ? a.rows[b] : int64_t(b);
+  int64_t tok0 = 0, count = a.T;
+  if (a.seq_start) {
+    // Packed descriptors come from the caller: clamp the range to the packed tokens.
+    int64_t lo = a.seq_start[b], hi = a.seq_start[b + 1];
+    lo = lo < 0 ? 0 : (lo > a.n_tokens ? a.n_tokens : lo);
+    hi = hi < lo ? lo : (hi > a.n_tokens ? a.n_tokens : hi);
+    tok0 = lo;
+    count = hi - lo;
+  }
+  const int64_t q_base = a.seq_start ? tok0 * a.q_st : int64_t(b) * a.q_sb;
+  const int64_t o_base = a.seq_start ? tok0 * a.o_st : int64_t(b) * a.o_sb;
+  const int64_t kl = a.key_lengths[b] + a.kl_add;
+  const bool row_ok = row >= 0 && row < a.capacity;
+
+  const int64_t head_off = (row * a.kv_heads + h) * int64_t(a.max_len) * D + e * DPL;
+  const TKV *__restrict__ kbase = static_cast<const TKV *>(a.k) + head_off;
+  const TKV *__restrict__ vbase = static_cast<const TKV *>(a.v) + head_off;
+
+  const int nq = int(count) * G;
+  for (int qb = 0; qb < nq; qb += QB) {
+    float q[QB][DPL];
+    int lim[QB];
+    int maxlim = 0;
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      const int m = qb + j;
+      if (m < nq) {
+        const int t = m / G, g = m % G;
+        const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st + e * DPL;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) q[j][i] = load_any(a.q, a.q_dtype, qo + i) * a.scale_log2;
+        int64_t l = kl + t;
+        if (l > a.span) l = a.span;
+        if (!row_ok || l < 0) l = 0;
+        lim[j] = int(l);
+      } else {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) q[j][i] = 0.f;
+        lim[j] = 0;
+      }
+      maxlim = lim[j] > maxlim ? lim[j] : maxlim;
+    }
+
+    float mx[QB], sum[QB], acc[QB][DPL];
+#pragma unroll
+    for (int j = 0; j < QB; ++j) {
+      mx[j] = NEG_BIG;
+      sum[j] = 0.f;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) acc[j][i] = 0.f;
+    }
+
+    for (int kb = wave * KEYS_PER_BLOCK; kb < maxlim; kb += WAVES * KEYS_PER_BLOCK) {
+      float kf[4][DPL], vf[4][DPL];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + 16 * r + slot;
+        if (key < maxlim) {
+          load_widen<TKV, DPL>(kbase + int64_t(key) * D, kf[r]);
+          load_widen<TKV, DPL>(vbase + int64_t(key) * D, vf[r]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) kf[r][i] = vf[r][i] = 0.f;
+        }
+      }
+      float s[4][QB];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+          float p = 0.f;
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) p = fmaf(q[j][i], kf[r][i], p);
+          p += quad_xor1(p);
+          p += quad_xor2(p);
+          const int key = kb + 16 * r + slot;
+          s[r][j] = key < lim[j] ? p : -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < QB; ++j) {
+        const float blk = fmaxf(fmaxf(s[0][j], s[1][j]), fmaxf(s[2][j], s[3][j]));
+        const float mnew = fmaxf(mx[j], blk);
+        const float corr = exp2f(mx[j] - mnew);
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = exp2f(s[r][j] - mnew);
+        sum[j] = sum[j] * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+          float v = acc[j][i] * corr;
+          v = fmaf(p[0], vf[0][i], v);
+          v = fmaf(p[1], vf[1][i], v);
+          v = fmaf(p[2], vf[2][i], v);
+          v = fmaf(p[3], vf[3][i], v);
+          acc[j][i] = v;
+        }
+        mx[j] = mnew;
+      }
+    }
+
+    // Merge the 16 slots of the wave (lanes differing in bits 2..5).
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+#pragma unroll
+      for (int j = 0; j < QB; ++j) {
+        const float mo = __shfl_xor(mx[j], off, 64);
+        const float so = __shfl_xor(sum[j], off, 64);
+        const float mnew = fmaxf(mx[j], mo);
+        const float c1 = exp2f(mx[j] - mnew), c2 = exp2f(mo - mnew);
+        sum[j] = sum[j] * c1 + so * c2;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+          const float ao = __shfl_xor(acc[j][i], off, 64);
+          acc[j][i] = acc[j][i] * c1 + ao * c2;
+        }
+        mx[j] = mnew;
+      }
+    }
+
+    if constexpr (WAVES > 1) {
+      if (slot == 0) {
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+          if (e == 0) {
+            merge_m[wave][j] = mx[j];
+            merge_l[wave][j] = sum[j];
+          }
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) merge_acc[wave][j][e * DPL + i] = acc[j][i];
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+          float m = merge_m[0][j];
+#pragma unroll
+          for (int w = 1; w < WAVES; ++w) m = fmaxf(m, merge_m[w][j]);
+          float l = 0.f, o[DPL];
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+#pragma unroll
+          for (int w = 0; w < WAVES; ++w) {
+            const float c = exp2f(merge_m[w][j] - m);
+            l += merge_l[w][j] * c;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) o[i] += merge_acc[w][j][e * DPL + i] * c;
+          }
+          sum[j] = l;
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) acc[j][i] = o[i];
+        }
+      }
+      __syncthreads();
+    }
+
+    if (wave == 0 && slot == 0) {
+#pragma unroll
+      for (int j = 0; j < QB; ++j) {
+        const int m = qb + j;
+        if (m < nq) {
+          const int t = m / G, g = m % G;
+          const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st + e * DPL;
+          const float inv = sum[j] > 0.f ? 1.0f / sum[j] : 0.f;
+#pragma unroll
+          for (int i = 0; i < DPL; ++i) store_any(a.out, a.out_dtype, oo + i, acc[j][i] * inv);
+        }
+      }
+    }
+  }
+}
+
+template <typename TKV, int D>
+void launch_d(const AttnArgs &a, hipStream_t s) {
+  constexpr int WAVES = 4;
+  decode_attention_kernel<TKV, D, WAVES><<<a.n_seqs * a.kv_heads, 64 * WAVES, 0, s>>>(a);
+  CG_LAUNCHED();
+}
+
+template <typename TKV>
+void launch_kv(const AttnArgs &a, hipStream_t s) {
+  switch (a.head_dim) {
+    case 8:
+      return launch_d<TKV, 8>(a, s);
+    case 16:
+      return launch_d<TKV, 16>(a, s);
+    case 24:
+      return launch_d<TKV, 24>(a, s);
+    case 32:
+      return launch_d<TKV, 32>(a, s);
+    case 64:
+      return launch_d<TKV, 64>(a, s);
+  }
+  throw Error(CG_ERR_UNSUPPORTED,
+              "decode attention is built for head_dim 8, 16, 24, 32 and 64, not " +
+                  std::to_string(a.head_dim));
+}
+
+}  // namespace
+
+void launch_decode_attention(const AttnArgs &a, hipStream_t s) {
+  CG_REQUIRE(a.n_heads > 0 && a.kv_heads > 0 && a.n_heads % a.kv_heads == 0, CG_ERR_INVALID,
+             "n_heads must be a positive multiple of kv_heads");
+  CG_REQUIRE(a.n_seqs >= 0, CG_ERR_INVALID, "negative batch");
+  if (a.n_seqs == 0) return;
+  switch (a.kv_dtype) {
+    case CG_F32:
+      return launch_kv<float>(a, s);
+    case CG_BF16:
+      return launch_kv<bf16>(a, s);
+    case CG_F16:
+      return launch_kv<f16>(a, s);
+  }
+  throw Error(CG_ERR_INVALID, "unknown cache dtype");
+}
+
+}  // namespace cg
+
+using namespace cg;
+
+extern "C" int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_sh,
+                                   int64_t q_st, const cg_kv_layer *layer, const int64_t *rows,
+                                   const int64_t *key_lengths, int32_t B, int32_t n_heads,
+                                   int32_t T, int32_t span, float scale, void *out,
+                                   int32_t out_dtype, void *stream) {
+  return guarded([&] {
+    check_layer(layer);
+    CG_REQUIRE(q && out && key_lengths, CG_ERR_INVALID, "q, out and key_lengths are required");
+    dtype_size(q_dtype);
+    dtype_size(out_dtype);
+    CG_REQUIRE(B >= 0 && T >= 0, CG_ERR_INVALID, "B and T must be non-negative");
+    AttnArgs a{};
+    a.q = q;
+    a.q_dtype = q_dtype;
+    a.q_sb = q_sb;
+    a.q_sh = q_sh;
+    a.q_st = q_st;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.o_st = layer->head_dim;
+    a.o_sh = int64_t(T) * layer->head_dim;
+    a.o_sb = int64_t(n_heads) * T * layer->head_dim;
+    a.k = layer->k;
+    a.v = layer->v;
+    a.kv_dtype = layer->dtype;
+    a.rows = rows;
+    a.key_lengths = key_lengths;
+    a.kl_add = 0;
+    a.seq_start = nullptr;
+    a.n_seqs = B;
+    a.n_heads = n_heads;
+    a.kv_heads = layer->kv_heads;
+    a.head_dim = layer->head_dim;
+    a.T = T;
+    a.max_len = layer->max_len;
+    a.capacity = layer->capacity;
+    a.span = (span <= 0 || span > layer->max_len) ? layer->max_len : span;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    if (T == 0) return;
+    launch_decode_attention(a, as_stream(stream));
+  });
+}

@@ -1,0 +1,65 @@
+"""Builds libcardgym_hip.so for gfx950 with hipcc (objects in parallel, then one link).
+
+Run as ``python -m card_playing_gym_amd.csrc.build`` or through ``__graft_entry__.build()``.
+Objects go to ``_build/`` at the repository root; the shared library lands next to the
+package (``card_playing_gym_amd/libcardgym_hip.so``) so it travels with the tree.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PACKAGE = CSRC.parent
+ROOT = PACKAGE.parent
+LIBRARY = PACKAGE / "libcardgym_hip.so"
+SOURCES = ("kv_ops.hip", "attention.hip", "gemm.hip", "trunk.hip")
+ARCH = os.environ.get("CARDGYM_HIP_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Packed fp32 VALU forms are kept out of every kernel (see the build notes in DESIGN).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def _compile(source: Path, obj: Path) -> None:
+    cmd = [HIPCC, *FLAGS, "-c", str(source), "-o", str(obj)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    stderr = "\n".join(line for line in result.stderr.splitlines() if noise not in line)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {source.name}:\n{stderr}")
+    if stderr.strip():
+        print(stderr, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    out_dir = ROOT / "_build"
+    out_dir.mkdir(exist_ok=True)
+    objects = [out_dir / (Path(name).stem + ".o") for name in SOURCES]
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as pool:
+        list(pool.map(lambda pair: _compile(CSRC / pair[0], pair[1]), zip(SOURCES, objects)))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *map(str, objects)]
+    result = subprocess.run(link, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"link failed:\n{result.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY}")
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build(verbose=True)

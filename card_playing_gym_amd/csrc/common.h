@@ -1,0 +1,165 @@
+// Shared device helpers and host-side error plumbing for libcardgym_hip.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "../../include/cardgym_hip.h"
+
+namespace cg {
+
+// ---- element conversion ---------------------------------------------------------
+// bf16 and fp16 values travel as raw 16-bit patterns; conversions are explicit so the
+// rounding is the one Tensor.to uses: round to nearest even, NaN -> 0x7FC0 for bf16.
+
+struct bf16 {
+  uint16_t bits;
+};
+struct f16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return __uint_as_float(uint32_t(v.bits) << 16); }
+__device__ __forceinline__ float to_f32(f16 v) {
+  _Float16 h;
+  __builtin_memcpy(&h, &v.bits, 2);
+  return float(h);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float v) {
+  uint32_t u = __float_as_uint(v);
+  bf16 r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.bits = 0x7fc0;
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.bits = uint16_t(u >> 16);
+  }
+  return r;
+}
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float v) {
+  // v_cvt_f16_f32 rounds to nearest even in the default mode and keeps denormals.
+  _Float16 h = _Float16(v);
+  f16 r;
+  __builtin_memcpy(&r.bits, &h, 2);
+  return r;
+}
+
+// Bit-preserving conversion between storage types (same type: copy).
+template <typename TO, typename TI>
+__device__ __forceinline__ TO convert(TI v) {
+  return from_f32<TO>(to_f32(v));
+}
+template <>
+__device__ __forceinline__ float convert<float, float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ bf16 convert<bf16, bf16>(bf16 v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ f16 convert<f16, f16>(f16 v) {
+  return v;
+}
+
+// ---- wave helpers ----------------------------------------------------------------
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+
+// Exact-erf GELU (torch.nn.GELU default): 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+// ---- host error plumbing ------------------------------------------------------------
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const std::string &message);
+
+#define CG_REQUIRE(cond, code, msg)                                   \
+  do {                                                                \
+    if (!(cond)) throw ::cg::Error((code), std::string(msg));         \
+  } while (0)
+
+#define CG_HIP(call)                                                                   \
+  do {                                                                                 \
+    hipError_t _e = (call);                                                            \
+    if (_e != hipSuccess)                                                              \
+      throw ::cg::Error(CG_ERR_HIP, std::string(#call) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+#define CG_LAUNCHED()                                                                     \
+  do {                                                                                    \
+    hipError_t _e = hipGetLastError();                                                    \
+    if (_e != hipSuccess)                                                                 \
+      throw ::cg::Error(CG_ERR_HIP, std::string("kernel launch: ") + hipGetErrorString(_e)); \
+  } while (0)
+
+// Runs `body` and converts any exception into a status code + thread-local message.
+template <typename F>
+int guarded(F &&body) {
+  try {
+    body();
+    return CG_OK;
+  } catch (const Error &e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::exception &e) {
+    set_last_error(e.what());
+    return CG_ERR_HIP;
+  } catch (...) {
+    set_last_error("unknown error");
+    return CG_ERR_HIP;
+  }
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int dtype_size(int32_t dtype) {
+  switch (dtype) {
+    case CG_F32:
+      return 4;
+    case CG_BF16:
+    case CG_F16:
+      return 2;
+    default:
+      throw Error(CG_ERR_INVALID, "unknown dtype " + std::to_string(dtype));
+  }
+}
+
+inline void check_layer(const cg_kv_layer *layer) {
+  CG_REQUIRE(layer != nullptr, CG_ERR_INVALID, "cache layer is NULL");
+  CG_REQUIRE(layer->k != nullptr && layer->v != nullptr, CG_ERR_INVALID, "cache k/v is NULL");
+  CG_REQUIRE(layer->capacity > 0 && layer->kv_heads > 0 && layer->max_len > 0 && layer->head_dim > 0,
+             CG_ERR_INVALID, "cache dimensions must be positive");
+  dtype_size(layer->dtype);
+}
+
+}  // namespace cg

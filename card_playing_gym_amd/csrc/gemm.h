@@ -1,0 +1,65 @@
+// Internal interface of the MFMA projection kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cg {
+
+// How the A operand [M, K] is produced.
+enum AMode : int {
+  A_LN = 0,    // fp32 rows normalised on the fly by LayerNorm(ln_w, ln_b, eps)
+  A_F32 = 1,   // fp32 storage
+  A_BF16 = 2,  // bf16 storage
+};
+
+// What happens to the fp32 accumulator C[M, N] = A . W^T.
+enum EpiMode : int {
+  EPI_STORE = 0,      // out = C + bias                      (out_dtype)
+  EPI_GELU = 1,       // out = gelu(C + bias)                (out_dtype)
+  EPI_RESID = 2,      // resid += C + bias + ple_scale * ple[m, ple_off + n % ple_dim]
+  EPI_QKV = 3,        // q | k | v split; k, v (+ value embedding) appended to the KV pool
+  EPI_SCALE_ADD = 4,  // out = (C + addend) * scale           (out_dtype)
+};
+
+struct GemmArgs {
+  int32_t M, N, K;
+  int32_t compute;  // CG_F32 or CG_BF16: operand type of the MFMA
+  // A operand.
+  int32_t a_mode;
+  const void *A;
+  int64_t lda;
+  const float *ln_w, *ln_b;
+  float eps;
+  // W operand [N, K] row-major, storage CG_F32 or CG_BF16.
+  const void *W;
+  int32_t w_dtype;
+  const float *bias;
+  // Epilogue.
+  int32_t epi;
+  void *out;
+  int32_t out_dtype;
+  int64_t ldo;
+  float *resid;
+  int64_t ldr;
+  const float *ple;
+  int64_t ld_ple;
+  int32_t ple_off, ple_dim;
+  float ple_scale;
+  const float *addend;
+  int64_t ld_add;
+  float scale;
+  // EPI_QKV: columns [0, q_cols) -> q (fp32, ld ldo); then kv_heads * head_dim columns of
+  // K and as many of V, appended at (tok_row[m], head, tok_pos[m]).
+  int32_t q_cols;
+  void *kc, *vc;
+  int32_t kv_dtype, kv_heads, head_dim, max_len;
+  const int32_t *tok_row, *tok_pos;
+  const float *vemb;
+  int64_t ld_vemb;
+  int32_t vemb_off;  // < 0: no value embedding
+};
+
+void launch_gemm(const GemmArgs &g, hipStream_t stream);
+
+}  // namespace cg

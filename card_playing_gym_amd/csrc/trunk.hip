@@ -1,0 +1,501 @@
+// The fused trunk: conditioning norms, the per-layer launch sequence of a ragged decode
+// step, and the final LayerNorm at the readout tokens.
+//
+// One step = plan -> (per layer) [LN + QKV GEMM + KV append] -> [decode attention]
+//   -> [out_proj GEMM + residual] -> [LN + up GEMM + GELU] -> [down GEMM + residual (+PLE)]
+//   -> readout LayerNorm.
+// This is DecoderBlock.forward_ragged / Trunk.forward_ragged (cardgym/nn/trunk.py:183-223,
+// 391-429) with the gather copy and the masked full-span attention replaced by in-place
+// attention over each row's own prefix.
+#include <string>
+#include <vector>
+
+#include "attention.h"
+#include "common.h"
+#include "gemm.h"
+
+struct cg_trunk {
+  cg_trunk_config cfg;
+  int32_t head_dim;
+  int32_t compute;
+  std::vector<cg_layer_params> layers;
+  const float *final_w;
+  const float *final_b;
+  // bf16 copies of the projection weights (compute == CG_BF16), one allocation.
+  void *wbuf = nullptr;
+  size_t wbuf_bytes = 0;
+  std::vector<const void *> qkv_w, out_w, up_w, down_w;
+};
+
+namespace cg {
+namespace {
+
+constexpr size_t ALIGN = 256;
+inline size_t align_up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
+
+struct Workspace {
+  float *x;
+  float *q;
+  void *attn;
+  void *h1;
+  int32_t *tok_row;
+  int32_t *tok_pos;
+  int32_t *readout_tok;
+  size_t bytes;
+};
+
+Workspace carve(const cg_trunk &t, int32_t n_tokens, int32_t n_seqs, char *base) {
+  const int d = t.cfg.d_model, hd = t.cfg.n_heads * t.head_dim, ff = t.cfg.d_ff;
+  const size_t act = t.compute == CG_BF16 ? 2 : 4;
+  Workspace w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char *p = base ? base + off : nullptr;
+    off += align_up(bytes);
+    return p;
+  };
+  w.x = reinterpret_cast<float *>(take(size_t(n_tokens) * d * 4));
+  w.q = reinterpret_cast<float *>(take(size_t(n_tokens) * hd * 4));
+  w.attn = take(size_t(n_tokens) * hd * act);
+  w.h1 = take(size_t(n_tokens) * ff * act);
+  w.tok_row = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
+  w.tok_pos = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
+  w.readout_tok = reinterpret_cast<int32_t *>(take(size_t(n_seqs > 0 ? n_seqs : 1) * 4));
+  w.bytes = off;
+  return w;
+}
+
+// Per-token cache slot (row, clamped write position) and per-sequence readout token.
+// Padded mode (seq_start NULL): token i belongs to sequence i / T.
+__global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t *__restrict__ positions,
+                            const int64_t *__restrict__ rows, const int64_t *__restrict__ readout,
+                            int32_t n_seqs, int32_t n_tokens, int32_t T, int32_t max_len,
+                            int32_t capacity, int32_t *__restrict__ tok_row,
+                            int32_t *__restrict__ tok_pos, int32_t *__restrict__ readout_tok) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n_tokens) {
+    int b, t;
+    if (seq_start) {
+      int lo = 0, hi = n_seqs - 1;  // last b with seq_start[b] <= i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (seq_start[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      b = lo;
+      t = int(i - seq_start[b]);
+    } else {
+      b = i / T;
+      t = i % T;
+    }
+    const int64_t row = rows ? rows[b] : int64_t(b);
+    int64_t pos = positions[b] + t;
+    if (pos > max_len - 1) pos = max_len - 1;
+    const bool ok = row >= 0 && row < capacity && pos >= 0;
+    tok_row[i] = ok ? int32_t(row) : -1;
+    tok_pos[i] = ok ? int32_t(pos) : 0;
+  }
+  if (readout && i < n_seqs) {
+    const int64_t start = seq_start ? seq_start[i] : int64_t(i) * T;
+    const int64_t stop = seq_start ? seq_start[i + 1] : start + T;
+    int64_t r = start + readout[i];
+    if (r < start || r >= stop) r = -1;
+    readout_tok[i] = int32_t(r);
+  }
+}
+
+// One wave per row: y = LayerNorm(x[src]) with fp32 two-pass statistics.
+__global__ void layernorm_rows_kernel(const float *__restrict__ x, const int32_t *__restrict__ index,
+                                      const float *__restrict__ w, const float *__restrict__ b,
+                                      float eps, float *__restrict__ y, int32_t n, int32_t d) {
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;
+  const int src = index ? index[row] : row;
+  float *out = y + int64_t(row) * d;
+  if (src < 0) {
+    for (int k = lane; k < d; k += 64) out[k] = 0.f;
+    return;
+  }
+  const float *in = x + int64_t(src) * d;
+  float s = 0.f;
+  for (int k = lane; k < d; k += 64) s += in[k];
+  const float mean = wave_sum(s) / float(d);
+  float v = 0.f;
+  for (int k = lane; k < d; k += 64) {
+    const float t = in[k] - mean;
+    v = fmaf(t, t, v);
+  }
+  const float rstd = rsqrtf(wave_sum(v) / float(d) + eps);
+  for (int k = lane; k < d; k += 64) out[k] = fmaf((in[k] - mean) * rstd, w[k], b[k]);
+}
+
+// One wave per row: y = rms_norm(src row) * gain; src row = table[ids[row]] or x[row].
+__global__ void rmsnorm_rows_kernel(const float *__restrict__ x, const float *__restrict__ table,
+                                    int32_t vocab, const int64_t *__restrict__ ids,
+                                    const float *__restrict__ gain, float eps, float *__restrict__ y,
+                                    int32_t n, int32_t d, int32_t *__restrict__ flag) {
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;
+  float *out = y + int64_t(row) * d;
+  const float *in;
+  if (ids) {
+    const int64_t id = ids[row];
+    if (id < 0 || id >= vocab) {
+      for (int k = lane; k < d; k += 64) out[k] = 0.f;
+      if (flag && lane == 0) flag[0] = 1;
+      return;
+    }
+    in = table + id * d;
+  } else {
+    in = x + int64_t(row) * d;
+  }
+  float s = 0.f;
+  for (int k = lane; k < d; k += 64) s = fmaf(in[k], in[k], s);
+  const float r = rsqrtf(wave_sum(s) / float(d) + eps);
+  for (int k = lane; k < d; k += 64) out[k] = in[k] * r * gain[k];
+}
+
+// fp32 -> bf16 (round to nearest even) weight copies.
+__global__ void to_bf16_kernel(const float *__restrict__ src, bf16 *__restrict__ dst, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x)
+    dst[i] = from_f32<bf16>(src[i]);
+}
+
+unsigned rows_grid(int32_t n, int waves_per_block) {
+  return unsigned((n + waves_per_block - 1) / waves_per_block);
+}
+
+void convert_weights(cg_trunk &t, hipStream_t s) {
+  if (t.compute != CG_BF16) return;
+  const int d = t.cfg.d_model, hd = t.cfg.n_heads * t.head_dim, ff = t.cfg.d_ff;
+  const int qkv_rows = (t.cfg.n_heads + 2 * t.cfg.n_kv_heads) * t.head_dim;
+  char *p = static_cast<char *>(t.wbuf);
+  size_t off = 0;
+  auto conv = [&](const float *src, int64_t n) {
+    bf16 *dst = reinterpret_cast<bf16 *>(p + off);
+    off += align_up(size_t(n) * 2);
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    to_bf16_kernel<<<unsigned(blocks), 256, 0, s>>>(src, dst, n);
+    CG_LAUNCHED();
+    return static_cast<const void *>(dst);
+  };
+  for (int l = 0; l < t.cfg.n_layers; ++l) {
+    const cg_layer_params &L = t.layers[l];
+    t.qkv_w[l] = conv(L.qkv_w, int64_t(qkv_rows) * d);
+    t.out_w[l] = conv(L.out_w, int64_t(d) * hd);
+    t.up_w[l] = conv(L.mlp_up_w, int64_t(ff) * d);
+    t.down_w[l] = conv(L.mlp_down_w, int64_t(d) * ff);
+  }
+}
+
+}  // namespace
+}  // namespace cg
+
+using namespace cg;
+
+extern "C" {
+
+int cg_trunk_create(const cg_trunk_config *config, const cg_layer_params *layers,
+                    const float *final_ln_w, const float *final_ln_b, int32_t compute_dtype,
+                    cg_trunk **out) {
+  cg_trunk *t = nullptr;
+  int status = guarded([&] {
+    CG_REQUIRE(config && layers && out && final_ln_w && final_ln_b, CG_ERR_INVALID,
+               "config, layers, final norm and out are required");
+    const cg_trunk_config &c = *config;
+    CG_REQUIRE(c.d_model > 0 && c.n_layers > 0 && c.n_heads > 0 && c.n_kv_heads > 0 && c.d_ff > 0,
+               CG_ERR_INVALID, "trunk dimensions must be positive");
+    CG_REQUIRE(c.d_model % c.n_heads == 0, CG_ERR_INVALID, "d_model must be divisible by n_heads");
+    CG_REQUIRE(c.n_heads % c.n_kv_heads == 0, CG_ERR_INVALID, "n_kv_heads must divide n_heads");
+    CG_REQUIRE(c.per_layer_dim >= 0 && c.value_width >= 0, CG_ERR_INVALID,
+               "per_layer_dim and value_width must be non-negative");
+    CG_REQUIRE(compute_dtype == CG_F32 || compute_dtype == CG_BF16, CG_ERR_INVALID,
+               "compute dtype must be CG_F32 or CG_BF16");
+    const int hd = c.d_model / c.n_heads;
+    CG_REQUIRE(c.d_model % 8 == 0 && c.d_ff % 8 == 0, CG_ERR_UNSUPPORTED,
+               "d_model and d_ff must be multiples of 8");
+    CG_REQUIRE(hd == 8 || hd == 16 || hd == 24 || hd == 32 || hd == 64, CG_ERR_UNSUPPORTED,
+               "head_dim must be 8, 16, 24, 32 or 64");
+    t = new cg_trunk();
+    t->cfg = c;
+    t->head_dim = hd;
+    t->compute = compute_dtype;
+    t->layers.assign(layers, layers + c.n_layers);
+    for (const cg_layer_params &L : t->layers) {
+      CG_REQUIRE(L.ln_attn_w && L.ln_attn_b && L.qkv_w && L.out_w && L.ln_mlp_w && L.ln_mlp_b &&
+                     L.mlp_up_w && L.mlp_up_b && L.mlp_down_w && L.mlp_down_b,
+                 CG_ERR_INVALID, "a layer parameter is NULL");
+      CG_REQUIRE(L.value_index < 0 || (L.value_index + 1) * c.n_kv_heads * hd <= c.value_width,
+                 CG_ERR_INVALID, "value_index outside the value-embedding stream");
+    }
+    t->final_w = final_ln_w;
+    t->final_b = final_ln_b;
+    const int n = c.n_layers;
+    t->qkv_w.resize(n);
+    t->out_w.resize(n);
+    t->up_w.resize(n);
+    t->down_w.resize(n);
+    for (int l = 0; l < n; ++l) {
+      t->qkv_w[l] = t->layers[l].qkv_w;
+      t->out_w[l] = t->layers[l].out_w;
+      t->up_w[l] = t->layers[l].mlp_up_w;
+      t->down_w[l] = t->layers[l].mlp_down_w;
+    }
+    if (compute_dtype == CG_BF16) {
+      const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * hd;
+      const size_t per_layer = align_up(size_t(qkv_rows) * c.d_model * 2) +
+                               align_up(size_t(c.d_model) * c.n_heads * hd * 2) +
+                               align_up(size_t(c.d_ff) * c.d_model * 2) +
+                               align_up(size_t(c.d_model) * c.d_ff * 2);
+      t->wbuf_bytes = per_layer * n;
+      CG_HIP(hipMalloc(&t->wbuf, t->wbuf_bytes));
+      convert_weights(*t, nullptr);
+      CG_HIP(hipStreamSynchronize(nullptr));
+    }
+    *out = t;
+  });
+  if (status != CG_OK && t) {
+    if (t->wbuf) (void)hipFree(t->wbuf);
+    delete t;
+  }
+  return status;
+}
+
+int cg_trunk_refresh(cg_trunk *trunk, void *stream) {
+  return guarded([&] {
+    CG_REQUIRE(trunk != nullptr, CG_ERR_INVALID, "trunk is NULL");
+    convert_weights(*trunk, as_stream(stream));
+  });
+}
+
+int cg_trunk_destroy(cg_trunk *trunk) {
+  return guarded([&] {
+    if (!trunk) return;
+    if (trunk->wbuf) CG_HIP(hipFree(trunk->wbuf));
+    delete trunk;
+  });
+}
+
+size_t cg_trunk_workspace_size(const cg_trunk *trunk, int32_t n_tokens, int32_t n_seqs) {
+  if (!trunk || n_tokens < 0 || n_seqs < 0) return 0;
+  return carve(*trunk, n_tokens, n_seqs, nullptr).bytes;
+}
+
+int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
+                     const float *ple, const float *values, const cg_ragged *step, float *hidden,
+                     void *workspace, size_t workspace_size, void *stream) {
+  return guarded([&] {
+    CG_REQUIRE(trunk && cache && x && step && hidden, CG_ERR_INVALID,
+               "trunk, cache, x, step and hidden are required");
+    const cg_trunk &t = *trunk;
+    const cg_trunk_config &c = t.cfg;
+    const cg_ragged &r = *step;
+    CG_REQUIRE(r.n_seqs >= 0 && r.n_tokens >= 0, CG_ERR_INVALID, "negative step size");
+    CG_REQUIRE(r.positions != nullptr, CG_ERR_INVALID, "positions is NULL");
+    CG_REQUIRE(r.seq_start || int64_t(r.n_seqs) * r.T == r.n_tokens, CG_ERR_INVALID,
+               "padded step: n_tokens must equal n_seqs * T");
+    CG_REQUIRE(c.per_layer_dim == 0 || ple, CG_ERR_INVALID,
+               "This trunk expects a per-layer embedding lookup.");
+    CG_REQUIRE(c.value_width == 0 || values, CG_ERR_INVALID,
+               "This trunk expects a value-embedding lookup.");
+    for (int l = 0; l < c.n_layers; ++l) {
+      const cg_kv_layer &L = cache[l];
+      check_layer(&L);
+      CG_REQUIRE(L.kv_heads == c.n_kv_heads && L.head_dim == t.head_dim, CG_ERR_INVALID,
+                 "cache layout does not match the trunk");
+      CG_REQUIRE(L.max_len == cache[0].max_len && L.capacity == cache[0].capacity &&
+                     L.dtype == cache[0].dtype,
+                 CG_ERR_INVALID, "cache layers differ in shape");
+    }
+    CG_REQUIRE(r.rows || r.n_seqs <= cache[0].capacity, CG_ERR_RANGE,
+               "dense rows: more sequences than cache rows");
+    if (r.n_tokens == 0 || r.n_seqs == 0) return;
+    Workspace w = carve(t, r.n_tokens, r.n_seqs, static_cast<char *>(workspace));
+    CG_REQUIRE(workspace && workspace_size >= w.bytes, CG_ERR_INVALID,
+               "workspace too small: need " + std::to_string(w.bytes) + " bytes");
+    hipStream_t s = as_stream(stream);
+    const int d = c.d_model, H = c.n_heads, KVH = c.n_kv_heads, D = t.head_dim;
+    const int N = r.n_tokens;
+    const int max_len = cache[0].max_len;
+    const int span = (r.span <= 0 || r.span > max_len) ? max_len : r.span;
+    const int act_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
+    const int w_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
+
+    {
+      const int n = N > r.n_seqs ? N : r.n_seqs;
+      plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout,
+                                                  r.n_seqs, N, r.T, max_len, cache[0].capacity,
+                                                  w.tok_row, w.tok_pos, w.readout_tok);
+      CG_LAUNCHED();
+    }
+    CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
+
+    const float ple_scale = [&] {
+      if (c.per_layer_dim == 0 || c.per_layer_dim == d) return 1.0f;
+      const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
+      return 1.0f / sqrtf(float(repeats));
+    }();
+
+    for (int l = 0; l < c.n_layers; ++l) {
+      const cg_layer_params &P = t.layers[l];
+      const cg_kv_layer &L = cache[l];
+      {  // LN1 + QKV + append
+        GemmArgs g{};
+        g.M = N;
+        g.N = (H + 2 * KVH) * D;
+        g.K = d;
+        g.compute = t.compute;
+        g.a_mode = A_LN;
+        g.A = w.x;
+        g.lda = d;
+        g.ln_w = P.ln_attn_w;
+        g.ln_b = P.ln_attn_b;
+        g.eps = c.eps;
+        g.W = t.qkv_w[l];
+        g.w_dtype = w_dtype;
+        g.epi = EPI_QKV;
+        g.out = w.q;
+        g.ldo = H * D;
+        g.q_cols = H * D;
+        g.kc = L.k;
+        g.vc = L.v;
+        g.kv_dtype = L.dtype;
+        g.kv_heads = KVH;
+        g.head_dim = D;
+        g.max_len = max_len;
+        g.tok_row = w.tok_row;
+        g.tok_pos = w.tok_pos;
+        g.vemb = values;
+        g.ld_vemb = c.value_width;
+        g.vemb_off = (values && P.value_index >= 0) ? P.value_index * KVH * D : -1;
+        launch_gemm(g, s);
+      }
+      {  // attention
+        AttnArgs a{};
+        a.q = w.q;
+        a.q_dtype = CG_F32;
+        a.q_st = int64_t(H) * D;
+        a.q_sh = D;
+        a.q_sb = int64_t(r.T) * H * D;
+        a.out = w.attn;
+        a.out_dtype = act_dtype;
+        a.o_st = int64_t(H) * D;
+        a.o_sh = D;
+        a.o_sb = int64_t(r.T) * H * D;
+        a.k = L.k;
+        a.v = L.v;
+        a.kv_dtype = L.dtype;
+        a.rows = r.rows;
+        a.key_lengths = r.positions;
+        a.kl_add = 1;
+        a.seq_start = r.seq_start;
+        a.n_tokens = N;
+        a.n_seqs = r.n_seqs;
+        a.n_heads = H;
+        a.kv_heads = KVH;
+        a.head_dim = D;
+        a.T = r.T;
+        a.max_len = max_len;
+        a.capacity = L.capacity;
+        a.span = span;
+        a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
+        launch_decode_attention(a, s);
+      }
+      {  // out_proj + residual
+        GemmArgs g{};
+        g.M = N;
+        g.N = d;
+        g.K = H * D;
+        g.compute = t.compute;
+        g.a_mode = act_dtype == CG_BF16 ? A_BF16 : A_F32;
+        g.A = w.attn;
+        g.lda = H * D;
+        g.W = t.out_w[l];
+        g.w_dtype = w_dtype;
+        g.epi = EPI_RESID;
+        g.resid = w.x;
+        g.ldr = d;
+        launch_gemm(g, s);
+      }
+      {  // LN2 + up + GELU
+        GemmArgs g{};
+        g.M = N;
+        g.N = c.d_ff;
+        g.K = d;
+        g.compute = t.compute;
+        g.a_mode = A_LN;
+        g.A = w.x;
+        g.lda = d;
+        g.ln_w = P.ln_mlp_w;
+        g.ln_b = P.ln_mlp_b;
+        g.eps = c.eps;
+        g.W = t.up_w[l];
+        g.w_dtype = w_dtype;
+        g.bias = P.mlp_up_b;
+        g.epi = EPI_GELU;
+        g.out = w.h1;
+        g.out_dtype = act_dtype;
+        g.ldo = c.d_ff;
+        launch_gemm(g, s);
+      }
+      {  // down + residual (+ PLE)
+        GemmArgs g{};
+        g.M = N;
+        g.N = d;
+        g.K = c.d_ff;
+        g.compute = t.compute;
+        g.a_mode = act_dtype == CG_BF16 ? A_BF16 : A_F32;
+        g.A = w.h1;
+        g.lda = c.d_ff;
+        g.W = t.down_w[l];
+        g.w_dtype = w_dtype;
+        g.bias = P.mlp_down_b;
+        g.epi = EPI_RESID;
+        g.resid = w.x;
+        g.ldr = d;
+        if (ple && c.per_layer_dim > 0) {
+          g.ple = ple;
+          g.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
+          g.ple_off = l * c.per_layer_dim;
+          g.ple_dim = c.per_layer_dim;
+          g.ple_scale = ple_scale;
+        }
+        launch_gemm(g, s);
+      }
+    }
+    const int rows_out = r.readout ? r.n_seqs : N;
+    layernorm_rows_kernel<<<rows_grid(rows_out, 4), 256, 0, s>>>(
+        w.x, r.readout ? w.readout_tok : nullptr, t.final_w, t.final_b, c.eps, hidden, rows_out, d);
+    CG_LAUNCHED();
+  });
+}
+
+int cg_rmsnorm(const float *x, const float *gain, float eps, float *y, int32_t n, int32_t d,
+               void *stream) {
+  return guarded([&] {
+    CG_REQUIRE(x && gain && y, CG_ERR_INVALID, "x, gain and y are required");
+    CG_REQUIRE(n >= 0 && d > 0, CG_ERR_INVALID, "bad sizes");
+    if (n == 0) return;
+    rmsnorm_rows_kernel<<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
+        x, nullptr, 0, nullptr, gain, eps, y, n, d, nullptr);
+    CG_LAUNCHED();
+  });
+}
+
+int cg_embed_rmsnorm(const float *table, int32_t vocab, const int64_t *ids, const float *gain,
+                     float eps, float *y, int32_t n, int32_t d, int32_t *flag, void *stream) {
+  return guarded([&] {
+    CG_REQUIRE(table && ids && gain && y, CG_ERR_INVALID, "table, ids, gain and y are required");
+    CG_REQUIRE(n >= 0 && d > 0 && vocab > 0, CG_ERR_INVALID, "bad sizes");
+    if (n == 0) return;
+    rmsnorm_rows_kernel<<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
+        nullptr, table, vocab, ids, gain, eps, y, n, d, flag);
+    CG_LAUNCHED();
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,94 @@
+"""Ragged GQA decode attention straight from the KV pool (API of cardgym.nn.cuda_decode).
+
+``decode_attention(q, k_cache, v_cache, rows, key_lengths, span, scale)`` keeps the
+signature and meaning of cardgym/nn/cuda_decode.py:188-202 -- query t of row b sees keys
+below ``key_lengths[b] + t`` of cache row ``rows[b]`` -- and is registered as the custom
+op ``cardgym_hip::decode_attention`` with a fake implementation, as the reference
+registers ``cardgym::decode_attention`` (cuda_decode.py:172-181), so graph capture and
+torch.compile treat it as opaque.  Unlike the reference kernel it takes any span,
+head_dim 8 / 16 / 24 / 32 / 64 and fp32 / bf16 / fp16 caches; scores, softmax and
+accumulation are fp32.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _native as nat
+from .kv_cache import dtype_code, require_device, stream_handle
+
+HEAD_DIMS = (8, 16, 24, 32, 64)
+
+
+def supported(head_dim: int, span: int, queries: int) -> bool:
+    """Shapes the kernel is built for (any span and query count)."""
+
+    return head_dim in HEAD_DIMS
+
+
+def _layer(k: torch.Tensor, v: torch.Tensor) -> nat.KVLayer:
+    if k.shape != v.shape or k.dtype != v.dtype:
+        raise ValueError("k and v caches must match in shape and dtype")
+    if not (k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("k and v caches must be contiguous [capacity, kv_heads, max_len, head_dim]")
+    capacity, kv_heads, max_len, head_dim = k.shape
+    return nat.KVLayer(k.data_ptr(), v.data_ptr(), capacity, kv_heads, max_len, head_dim, dtype_code(k.dtype))
+
+
+def attention_into(
+    out: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    rows: torch.Tensor | None,
+    key_lengths: torch.Tensor,
+    span: int,
+    scale: float,
+) -> None:
+    """Writes attention of q [B, H, T, D] (any strides, unit last stride) into out
+    [B, H, T, D] (contiguous)."""
+
+    import ctypes
+
+    require_device(q, k, v, out)
+    if q.stride(3) != 1:
+        q = q.contiguous()
+    if rows is not None and (rows.dtype != torch.int64 or not rows.is_contiguous()):
+        rows = rows.to(torch.int64).contiguous()
+    lengths = key_lengths.to(torch.int64).contiguous()
+    batch, heads, steps, _ = q.shape
+    layer = _layer(k, v)
+    nat.call(
+        "cg_decode_attention", q.data_ptr(), dtype_code(q.dtype), q.stride(0), q.stride(1), q.stride(2),
+        ctypes.byref(layer), None if rows is None else rows.data_ptr(), lengths.data_ptr(), batch, heads,
+        steps, int(span), float(scale), out.data_ptr(), dtype_code(out.dtype), stream_handle(q.device),
+    )
+
+
+@torch.library.custom_op("cardgym_hip::decode_attention", mutates_args=())
+def _decode_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rows: torch.Tensor, lengths: torch.Tensor, span: int, scale: float
+) -> torch.Tensor:
+    out = torch.empty(q.shape, dtype=k.dtype, device=q.device)
+    attention_into(out, q, k, v, rows, lengths, span, scale)
+    return out
+
+
+@_decode_attention.register_fake
+def _(q, k, v, rows, lengths, span, scale):
+    return torch.empty(q.shape, dtype=k.dtype, device=q.device)
+
+
+def decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    rows: torch.Tensor,
+    key_lengths: torch.Tensor,
+    span: int,
+    scale: float,
+) -> torch.Tensor:
+    """q [B, H, T, D] against cache rows ``rows`` [B] of k/v [R, KVH, L, D]; returns
+    [B, H, T, D] in the cache's dtype."""
+
+    return _decode_attention(q, k_cache, v_cache, rows, key_lengths, span, scale)

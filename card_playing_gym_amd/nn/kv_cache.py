@@ -1,0 +1,265 @@
+"""Preallocated key/value pool for the ragged decode step (API of cardgym.nn.kv_cache).
+
+Mirrors ``KVCache`` (cardgym/nn/kv_cache.py:19-138): the same constructor, attributes
+(``k[layer]`` / ``v[layer]`` views of shape ``[capacity, kv_heads, max_len, head_dim]``,
+``stacked``, ``capacity``, ``max_len``, ``dtype``) and methods, with every data movement
+done by the HIP kernels of libcardgym_hip.so.  Storage stays in the reference's layout,
+so each (row, KV head) prefix is one contiguous segment that the attention kernel reads
+with full-width coalesced loads.
+
+The pool must live on a ROCm device; the methods raise on CPU tensors (there is no CPU
+path).  Kernels skip out-of-range rows and positions instead of faulting; set
+``CARDGYM_HIP_CHECK=1`` to have every write validate its indices on the device and raise
+``IndexError`` (this reads a flag back, so it synchronises).
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .. import _native as nat
+
+# Elements, not bytes: the reference keeps one stacked tensor only below this count
+# (cardgym/nn/kv_cache.py:15-16); the same rule is kept so ``stacked`` means the same.
+MAX_TENSOR_ELEMENTS = 2**31 - 1
+
+DTYPE_CODES = {torch.float32: nat.CG_F32, torch.bfloat16: nat.CG_BF16, torch.float16: nat.CG_F16}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"Unsupported dtype {dtype}; use float32, bfloat16 or float16.") from None
+
+
+def require_device(*tensors: torch.Tensor | None) -> None:
+    for tensor in tensors:
+        if tensor is not None and tensor.device.type != "cuda":
+            raise RuntimeError(
+                "card_playing_gym_amd runs on a ROCm GPU only; got a tensor on "
+                f"{tensor.device} (there is no CPU fallback)."
+            )
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def index_tensor(values, device: torch.device) -> torch.Tensor:
+    """int64 contiguous device tensor (host arrays are uploaded)."""
+
+    tensor = torch.as_tensor(values)
+    if tensor.dtype != torch.int64:
+        tensor = tensor.to(torch.int64)
+    return tensor.to(device, non_blocking=True).contiguous()
+
+
+def _check_enabled() -> bool:
+    return os.environ.get("CARDGYM_HIP_CHECK", "0") not in ("", "0")
+
+
+class KVCache:
+    # Cap on the gathered temporary one ``copy_rows`` chunk may hold (kv_cache.py:20-21).
+    COPY_CHUNK_BYTES = 256 * 1024 * 1024
+
+    def __init__(
+        self,
+        *,
+        n_layers: int,
+        kv_heads: int,
+        head_dim: int,
+        capacity: int,
+        max_len: int,
+        device: torch.device | str,
+        dtype: torch.dtype = torch.float32,
+    ) -> None:
+        if min(n_layers, kv_heads, head_dim, capacity, max_len) <= 0:
+            raise ValueError("KVCache dimensions must be positive.")
+        dtype_code(dtype)
+        self.n_layers = n_layers
+        self.kv_heads = kv_heads
+        self.head_dim = head_dim
+        self.capacity = capacity
+        self.max_len = max_len
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self._row_shape = (kv_heads, max_len, head_dim)
+        elements = n_layers * capacity * kv_heads * max_len * head_dim
+        self.stacked = elements <= MAX_TENSOR_ELEMENTS
+        # Zero-filled: a reset row is only re-lengthed, never cleared, and stale keys
+        # past a row's length are masked; zeros keep 0 * value finite.
+        if self.stacked:
+            self._base_k = torch.zeros((n_layers, capacity, *self._row_shape), device=self.device, dtype=dtype)
+            self._base_v = torch.zeros_like(self._base_k)
+            self.k = list(self._base_k.unbind(0))
+            self.v = list(self._base_v.unbind(0))
+        else:
+            self._base_k = self._base_v = None
+            self.k = [torch.zeros((capacity, *self._row_shape), device=self.device, dtype=dtype) for _ in range(n_layers)]
+            self.v = [torch.zeros_like(k) for k in self.k]
+        self._layers: list[nat.KVLayer] | None = None
+
+    @staticmethod
+    def bytes_per_row(n_layers: int, kv_heads: int, head_dim: int, max_len: int, dtype: torch.dtype) -> int:
+        return n_layers * kv_heads * max_len * head_dim * 2 * dtype.itemsize
+
+    # -- native views --------------------------------------------------------
+
+    def layer_struct(self, layer: int) -> nat.KVLayer:
+        return self.layer_array()[layer]
+
+    def layer_array(self):
+        """ctypes array of every layer's ``cg_kv_layer`` (pointers into this pool)."""
+
+        if self._layers is None:
+            array = (nat.KVLayer * self.n_layers)()
+            for index in range(self.n_layers):
+                array[index] = nat.KVLayer(
+                    self.k[index].data_ptr(),
+                    self.v[index].data_ptr(),
+                    self.capacity,
+                    self.kv_heads,
+                    self.max_len,
+                    self.head_dim,
+                    dtype_code(self.dtype),
+                )
+            self._layers = array
+        return self._layers
+
+    def _stream(self) -> int:
+        return stream_handle(self.device)
+
+    def _validate(self, layer: int, rows: torch.Tensor | None, positions: torch.Tensor | None) -> None:
+        if not _check_enabled():
+            return
+        flag = torch.zeros(1, dtype=torch.int32, device=self.device)
+        nat.call(
+            "cg_kv_check_indices",
+            ctypes_ref(self.layer_struct(layer)),
+            _ptr(rows),
+            0 if rows is None else rows.numel(),
+            _ptr(positions),
+            0 if positions is None else positions.numel(),
+            flag.data_ptr(),
+            self._stream(),
+        )
+        if int(flag.item()):
+            raise IndexError("cache rows or positions out of range")
+
+    @staticmethod
+    def _source(tensor: torch.Tensor) -> tuple[nat.KVSource, torch.Tensor]:
+        """[B, kv_heads, T, head_dim] view -> strided source (head_dim stride 1)."""
+
+        if tensor.dim() != 4:
+            raise ValueError("new keys/values must be [B, kv_heads, T, head_dim]")
+        if tensor.stride(3) != 1:
+            tensor = tensor.contiguous()
+        return (
+            nat.KVSource(tensor.data_ptr(), dtype_code(tensor.dtype), tensor.stride(0), tensor.stride(1), tensor.stride(2)),
+            tensor,
+        )
+
+    # -- reference API -------------------------------------------------------
+
+    def write_range(self, layer: int, rows, start: int, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """Write [B, kv_heads, T, head_dim] at a shared offset; ``rows=None`` is 0..B-1."""
+
+        require_device(self.k[layer], k_new, v_new)
+        batch, _, length, _ = k_new.shape
+        if start < 0 or start + length > self.max_len:
+            raise IndexError("write_range past the pool's max_len")
+        rows_t = None if rows is None else index_tensor(rows, self.device)
+        if rows_t is None and batch > self.capacity:
+            raise IndexError("dense write past the pool's capacity")
+        self._validate(layer, rows_t, None)
+        ks, keep_k = self._source(k_new)
+        vs, keep_v = self._source(v_new.to(k_new.dtype) if v_new.dtype != k_new.dtype else v_new)
+        nat.call(
+            "cg_kv_write_range", ctypes_ref(self.layer_struct(layer)), _ptr(rows_t), int(start),
+            ctypes_ref(ks), ctypes_ref(vs), batch, length, self._stream(),
+        )
+        del keep_k, keep_v
+
+    def write_step(self, layer: int, rows, positions, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
+        """Write K/V at a per-row offset: ``positions`` is [B] or [B, T]."""
+
+        require_device(self.k[layer], k_new, v_new)
+        length = k_new.shape[2]
+        positions = torch.as_tensor(positions)
+        if positions.dim() == 1:
+            if length != 1:
+                raise ValueError("A [B] position vector writes exactly one position per row.")
+        elif positions.shape[1] != length:
+            raise ValueError("positions must carry one offset per written step.")
+        batch = k_new.shape[0]
+        rows_t = index_tensor(rows, self.device)
+        pos_t = index_tensor(positions, self.device).reshape(-1)
+        if pos_t.numel() != batch * length or rows_t.numel() != batch:
+            raise ValueError("rows / positions do not match the new keys")
+        self._validate(layer, rows_t, pos_t)
+        ks, keep_k = self._source(k_new)
+        vs, keep_v = self._source(v_new.to(k_new.dtype) if v_new.dtype != k_new.dtype else v_new)
+        nat.call(
+            "cg_kv_write_step", ctypes_ref(self.layer_struct(layer)), rows_t.data_ptr(), pos_t.data_ptr(),
+            ctypes_ref(ks), ctypes_ref(vs), batch, length, self._stream(),
+        )
+        del keep_k, keep_v
+
+    def read(self, layer: int, rows, length: int, count: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Cached K/V [B, kv_heads, length, head_dim]; ``rows=None`` is a zero-copy 0..count-1 view."""
+
+        if rows is None:
+            if count is None:
+                raise ValueError("A dense read requires an explicit row count.")
+            return self.k[layer][:count, :, :length], self.v[layer][:count, :, :length]
+        require_device(self.k[layer])
+        if length < 0 or length > self.max_len:
+            raise IndexError("read length past max_len")
+        rows_t = index_tensor(rows, self.device)
+        shape = (rows_t.numel(), self.kv_heads, length, self.head_dim)
+        k_out = torch.empty(shape, device=self.device, dtype=self.dtype)
+        v_out = torch.empty_like(k_out)
+        self._validate(layer, rows_t, None)
+        nat.call(
+            "cg_kv_read", ctypes_ref(self.layer_struct(layer)), rows_t.data_ptr(), rows_t.numel(), length,
+            k_out.data_ptr(), v_out.data_ptr(), self._stream(),
+        )
+        return k_out, v_out
+
+    def copy_rows(self, sources, targets, length: int) -> None:
+        """Copy the first ``length`` positions of ``sources`` rows onto ``targets``.
+
+        Like the reference, each chunk is gathered before it is written, so sources and
+        targets may overlap (compaction moves rows down onto rows that are themselves
+        sources).
+        """
+
+        require_device(self.k[0])
+        if length < 0 or length > self.max_len:
+            raise IndexError("copy length past max_len")
+        src = index_tensor(sources, self.device)
+        dst = index_tensor(targets, self.device)
+        if src.numel() != dst.numel():
+            raise ValueError("sources and targets differ in length")
+        if length == 0 or src.numel() == 0:
+            return
+        row_bytes = max(self.kv_heads * length * self.head_dim * self.dtype.itemsize, 1)
+        chunk = max(self.COPY_CHUNK_BYTES // row_bytes, 1)
+        for start in range(0, src.numel(), chunk):
+            s, t = src[start : start + chunk], dst[start : start + chunk]
+            for layer in range(self.n_layers):
+                k_tmp, v_tmp = self.read(layer, s, length)
+                self.write_range(layer, t, 0, k_tmp, v_tmp)
+
+
+def _ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def ctypes_ref(struct):
+    import ctypes
+
+    return ctypes.byref(struct)

@@ -1,0 +1,450 @@
+"""GQA decoder trunk with a KV-cached ragged step on MI355X (API of cardgym.nn.trunk).
+
+The module tree and parameter names are those of the reference trunk
+(cardgym/nn/trunk.py:124-281): ``input_norm``, ``ple_context``, ``blocks[i].ln_attn``,
+``.qkv_proj``, ``.out_proj``, ``.ln_mlp``, ``.mlp[0|2]``, ``final_norm``, so a reference
+state dict loads unchanged and the collectors' calls keep their meaning.  Every forward
+runs on the HIP kernels of libcardgym_hip.so through one ``cg_trunk_forward`` call per
+step (all layers, append + attention + projections); there is no PyTorch compute path.
+
+Precision follows the caller's autocast state, as the reference's collectors set it
+(cardgym/core/devices.py:32-43): under ``torch.autocast("cuda", dtype=torch.bfloat16)``
+the projections run as bf16 x bf16 MFMA with fp32 accumulation, otherwise in fp32.
+The KV storage dtype is the cache's own.  Norms, softmax and the residual stream are
+always fp32.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+from torch import nn
+
+from .. import _native as nat
+from .kv_cache import KVCache, index_tensor, require_device, stream_handle
+
+ValueEmbeddingMode = Literal["off", "alternating", "all"]
+
+
+@dataclass(frozen=True)
+class TrunkConfig:
+    """Fields and derived sizes of cardgym.nn.trunk.TrunkConfig (trunk.py:39-91)."""
+
+    d_model: int = 256
+    n_layers: int = 6
+    n_heads: int = 8
+    n_kv_heads: int = 2
+    d_ff: int = 768
+    per_layer_dim: int = 0
+    value_embeddings: ValueEmbeddingMode = "off"
+    input_norm: bool = True
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.n_heads
+
+    @property
+    def kv_width(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    @property
+    def value_layers(self) -> tuple[int, ...]:
+        """Blocks whose V receives a value embedding: none, all, or the last block and
+        every other block before it."""
+
+        if self.value_embeddings == "off":
+            return ()
+        if self.value_embeddings == "all":
+            return tuple(range(self.n_layers))
+        last_parity = (self.n_layers - 1) % 2
+        return tuple(layer for layer in range(self.n_layers) if layer % 2 == last_parity)
+
+    @property
+    def ple_width(self) -> int:
+        return self.n_layers * self.per_layer_dim
+
+    @property
+    def value_width(self) -> int:
+        return len(self.value_layers) * self.kv_width
+
+    def validate(self) -> None:
+        if self.d_model % self.n_heads:
+            raise ValueError("d_model must be divisible by n_heads.")
+        if self.n_kv_heads > self.n_heads or self.n_heads % self.n_kv_heads:
+            raise ValueError("n_kv_heads must divide n_heads.")
+        if self.per_layer_dim < 0:
+            raise ValueError("per_layer_dim must be non-negative.")
+        if self.value_embeddings not in ("off", "alternating", "all"):
+            raise ValueError(f"Unknown value_embeddings mode {self.value_embeddings!r}.")
+
+
+def init_weights(module: nn.Module) -> None:
+    """N(0, 0.02) Linear / Embedding weights and zero biases (trunk.py:93-101)."""
+
+    if isinstance(module, nn.Linear):
+        nn.init.normal_(module.weight, mean=0.0, std=0.02)
+        if module.bias is not None:
+            nn.init.zeros_(module.bias)
+    elif isinstance(module, nn.Embedding):
+        nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+
+class RMSNorm(nn.Module):
+    """Gain-only RMSNorm (trunk.py:104-115); evaluated by the ``cg_rmsnorm`` kernel."""
+
+    def __init__(self, d: int, eps: float = 1e-5) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        require_device(x)
+        flat = x.reshape(-1, x.shape[-1]).float().contiguous()
+        out = torch.empty_like(flat)
+        nat.call(
+            "cg_rmsnorm", flat.data_ptr(), _param(self.weight).data_ptr(), float(self.eps), out.data_ptr(),
+            flat.shape[0], flat.shape[1], stream_handle(x.device),
+        )
+        return out.view(x.shape)
+
+
+class DecoderBlock(nn.Module):
+    """Parameters of one pre-LN GQA block (trunk.py:124-139).
+
+    The block's computation is fused into the trunk-level kernels; it is not callable
+    on its own (run ``Trunk.forward_ragged`` / ``forward_prefill`` / ``forward``).
+    """
+
+    def __init__(self, config: TrunkConfig) -> None:
+        super().__init__()
+        d = config.d_model
+        self.n_heads = config.n_heads
+        self.kv_heads = config.n_kv_heads
+        self.head_dim = config.head_dim
+        self.head_group = config.n_heads // config.n_kv_heads
+        self.scale = 1.0 / math.sqrt(config.head_dim)
+        self.ln_attn = nn.LayerNorm(d)
+        self.qkv_proj = nn.Linear(d, (self.n_heads + 2 * self.kv_heads) * self.head_dim, bias=False)
+        self.out_proj = nn.Linear(self.n_heads * self.head_dim, d, bias=False)
+        self.ln_mlp = nn.LayerNorm(d)
+        self.mlp = nn.Sequential(nn.Linear(d, config.d_ff), nn.GELU(), nn.Linear(config.d_ff, d))
+
+    def forward(self, *args, **kwargs):  # pragma: no cover - guidance only
+        raise NotImplementedError("Blocks run fused inside Trunk.forward_ragged / forward_prefill / forward.")
+
+
+def _param(tensor: torch.Tensor) -> torch.Tensor:
+    if tensor.dtype != torch.float32 or not tensor.is_contiguous():
+        raise ValueError("trunk parameters must be contiguous float32 tensors")
+    return tensor
+
+
+def compute_dtype_code(device: torch.device) -> int:
+    """bf16 projections under bf16 autocast on the device, fp32 otherwise."""
+
+    if torch.is_autocast_enabled(device.type) and torch.get_autocast_dtype(device.type) == torch.bfloat16:
+        return nat.CG_BF16
+    return nat.CG_F32
+
+
+class _NativeTrunk:
+    """A ``cg_trunk`` handle over the module's parameters for one compute dtype."""
+
+    def __init__(self, trunk: "Trunk", compute: int) -> None:
+        self.compute = compute
+        self.params = list(_trunk_tensors(trunk))
+        self.signature = _signature(self.params)
+        config = trunk.config
+        cfg = nat.TrunkConfig(
+            config.d_model, config.n_layers, config.n_heads, config.n_kv_heads, config.d_ff,
+            config.per_layer_dim, config.value_width, float(trunk.final_norm.eps),
+        )
+        layers = (nat.LayerParams * config.n_layers)()
+        for index, block in enumerate(trunk.blocks):
+            layers[index] = nat.LayerParams(
+                _param(block.ln_attn.weight).data_ptr(), _param(block.ln_attn.bias).data_ptr(),
+                _param(block.qkv_proj.weight).data_ptr(), _param(block.out_proj.weight).data_ptr(),
+                _param(block.ln_mlp.weight).data_ptr(), _param(block.ln_mlp.bias).data_ptr(),
+                _param(block.mlp[0].weight).data_ptr(), _param(block.mlp[0].bias).data_ptr(),
+                _param(block.mlp[2].weight).data_ptr(), _param(block.mlp[2].bias).data_ptr(),
+                trunk._value_index.get(index, -1),
+            )
+        self.layers = layers
+        handle = ctypes.c_void_p()
+        nat.call(
+            "cg_trunk_create", ctypes.byref(cfg), layers, _param(trunk.final_norm.weight).data_ptr(),
+            _param(trunk.final_norm.bias).data_ptr(), compute, ctypes.byref(handle),
+        )
+        self.handle = handle
+        self.versions = _versions(self.params)
+
+    def sync(self, trunk: "Trunk", stream: int) -> bool:
+        """False when the parameters moved (rebuild); re-derives weight copies after edits."""
+
+        if _signature(self.params) != self.signature or len(self.params) != len(list(_trunk_tensors(trunk))):
+            return False
+        if any(a is not b for a, b in zip(self.params, _trunk_tensors(trunk))):
+            return False
+        versions = _versions(self.params)
+        if versions != self.versions:
+            nat.call("cg_trunk_refresh", self.handle, stream)
+            self.versions = versions
+        return True
+
+    def close(self) -> None:
+        if self.handle:
+            try:
+                nat.lib().cg_trunk_destroy(self.handle)
+            finally:
+                self.handle = ctypes.c_void_p()
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _trunk_tensors(trunk: "Trunk"):
+    for block in trunk.blocks:
+        yield from (
+            block.ln_attn.weight, block.ln_attn.bias, block.qkv_proj.weight, block.out_proj.weight,
+            block.ln_mlp.weight, block.ln_mlp.bias, block.mlp[0].weight, block.mlp[0].bias,
+            block.mlp[2].weight, block.mlp[2].bias,
+        )
+    yield trunk.final_norm.weight
+    yield trunk.final_norm.bias
+
+
+def _signature(params) -> tuple[int, ...]:
+    return tuple(p.data_ptr() for p in params)
+
+
+def _versions(params) -> tuple[int, ...]:
+    return tuple(p._version for p in params)
+
+
+class Trunk(nn.Module):
+    def __init__(self, config: TrunkConfig) -> None:
+        super().__init__()
+        config.validate()
+        self.config = config
+        d = config.d_model
+        self.input_norm = RMSNorm(d) if config.input_norm else None
+        self.ple_context = nn.Linear(d, config.ple_width, bias=False) if config.per_layer_dim else None
+        self.blocks = nn.ModuleList(DecoderBlock(config) for _ in range(config.n_layers))
+        self.final_norm = nn.LayerNorm(d)
+        self._value_index = {layer: index for index, layer in enumerate(config.value_layers)}
+        self.blocks.apply(init_weights)
+        # GPT-2 residual scaling of the two projections that write the stream (trunk.py:276-279).
+        residual_scale = 1.0 / math.sqrt(2 * config.n_layers)
+        for block in self.blocks:
+            block.out_proj.weight.data.mul_(residual_scale)
+            block.mlp[2].weight.data.mul_(residual_scale)
+        if self.ple_context is not None:
+            nn.init.zeros_(self.ple_context.weight)
+        self._native_cache: dict[tuple[int, int], _NativeTrunk] = {}
+
+    # -- native handle ---------------------------------------------------------
+
+    def native(self, device: torch.device) -> _NativeTrunk:
+        compute = compute_dtype_code(device)
+        key = (device.index if device.index is not None else torch.cuda.current_device(), compute)
+        entry = self._native_cache.get(key)
+        if entry is not None and entry.sync(self, stream_handle(device)):
+            return entry
+        if entry is not None:
+            entry.close()
+        entry = _NativeTrunk(self, compute)
+        self._native_cache[key] = entry
+        return entry
+
+    def _apply(self, fn, *args, **kwargs):
+        # Moving or casting parameters invalidates every handle (they hold raw pointers).
+        for entry in getattr(self, "_native_cache", {}).values():
+            entry.close()
+        self._native_cache = {}
+        return super()._apply(fn, *args, **kwargs)
+
+    # -- conditioning ----------------------------------------------------------
+
+    def condition(self, x: torch.Tensor, ple_lookup: torch.Tensor | None, value_lookup: torch.Tensor | None):
+        """Normalise the embedding sum and shape the per-layer streams (trunk.py:285-312)."""
+
+        require_device(x)
+        if self.input_norm is not None:
+            x = self.input_norm(x)
+        else:
+            x = x.float()
+        lead = x.shape[:-1]
+        ple = None
+        if self.ple_context is not None:
+            if ple_lookup is None:
+                raise ValueError("This trunk expects a per-layer embedding lookup.")
+            flat = x.reshape(-1, x.shape[-1]).contiguous()
+            lookup = ple_lookup.reshape(flat.shape[0], -1).float().contiguous()
+            out = torch.empty_like(lookup)
+            nat.call(
+                "cg_linear_add_scale", flat.data_ptr(), _param(self.ple_context.weight).data_ptr(),
+                lookup.data_ptr(), out.data_ptr(), flat.shape[0], lookup.shape[1], flat.shape[1],
+                1.0 / math.sqrt(2.0), compute_dtype_code(x.device), stream_handle(x.device),
+            )
+            ple = out.view(*lead, self.config.n_layers, self.config.per_layer_dim)
+        values = None
+        if self._value_index:
+            if value_lookup is None:
+                raise ValueError("This trunk expects a value-embedding lookup.")
+            values = value_lookup.view(*lead, len(self._value_index), self.config.kv_width)
+        return x, ple, values
+
+    # -- execution paths -------------------------------------------------------
+
+    def _run(
+        self,
+        x: torch.Tensor,
+        ple: torch.Tensor | None,
+        values: torch.Tensor | None,
+        cache: KVCache,
+        *,
+        n_seqs: int,
+        T: int,
+        seq_start: torch.Tensor | None,
+        positions: torch.Tensor,
+        rows: torch.Tensor | None,
+        readout: torch.Tensor | None,
+        span: int | None,
+    ) -> torch.Tensor:
+        require_device(x, cache.k[0])
+        config = self.config
+        if cache.n_layers != config.n_layers or cache.kv_heads != config.n_kv_heads or cache.head_dim != config.head_dim:
+            raise ValueError("cache layout does not match the trunk")
+        device = x.device
+        n_tokens = x.numel() // config.d_model
+        flat = x.reshape(n_tokens, config.d_model).float().contiguous()
+        ple_flat = None if ple is None else ple.reshape(n_tokens, -1).float().contiguous()
+        values_flat = None if values is None else values.reshape(n_tokens, -1).float().contiguous()
+        if config.per_layer_dim and ple_flat is None:
+            raise ValueError("This trunk expects a per-layer embedding lookup.")
+        if self._value_index and values_flat is None:
+            raise ValueError("This trunk expects a value-embedding lookup.")
+        native = self.native(device)
+        stream = stream_handle(device)
+        rows_out = n_seqs if readout is not None else n_tokens
+        hidden = torch.empty((rows_out, config.d_model), device=device, dtype=torch.float32)
+        size = nat.lib().cg_trunk_workspace_size(native.handle, n_tokens, n_seqs)
+        workspace = torch.empty(max(size, 1), device=device, dtype=torch.uint8)
+        step = nat.Ragged(
+            n_seqs, n_tokens, T, 0 if span is None else int(span),
+            None if seq_start is None else seq_start.data_ptr(), positions.data_ptr(),
+            None if rows is None else rows.data_ptr(), None if readout is None else readout.data_ptr(),
+        )
+        nat.call(
+            "cg_trunk_forward", native.handle, cache.layer_array(), flat.data_ptr(),
+            None if ple_flat is None else ple_flat.data_ptr(),
+            None if values_flat is None else values_flat.data_ptr(),
+            ctypes.byref(step), hidden.data_ptr(), workspace.data_ptr(), size, stream,
+        )
+        return hidden
+
+    def forward_ragged(
+        self,
+        x: torch.Tensor,
+        ple: torch.Tensor | None,
+        values: torch.Tensor | None,
+        cache: KVCache,
+        positions: torch.Tensor,
+        readout_offsets: torch.Tensor,
+        span: int | None = None,
+        rows: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Append a padded run of T tokens to rows 0..B-1 (or ``rows``) at their own lengths.
+
+        Same contract as trunk.py:391-429: ``positions[b]`` is row b's length, token t is
+        written at ``min(positions[b] + t, max_len - 1)``, query t sees keys below
+        ``positions[b] + 1 + t`` (capped by ``span``).  Returns the final-norm hidden
+        state of token ``readout_offsets[b]`` of each row, [B, d].  ``span`` is only a cap:
+        nothing is read back from the device when it is None.
+        """
+
+        batch, length = x.shape[0], x.shape[1]
+        device = x.device
+        return self._run(
+            x, ple, values, cache, n_seqs=batch, T=length, seq_start=None,
+            positions=index_tensor(positions, device), rows=None if rows is None else index_tensor(rows, device),
+            readout=index_tensor(readout_offsets, device), span=span,
+        )
+
+    def forward_packed(
+        self,
+        x: torch.Tensor,
+        ple: torch.Tensor | None,
+        values: torch.Tensor | None,
+        cache: KVCache,
+        positions: torch.Tensor,
+        seq_start: torch.Tensor,
+        readout_offsets: torch.Tensor | None,
+        rows: torch.Tensor | None = None,
+        span: int | None = None,
+    ) -> torch.Tensor:
+        """Packed variable-length chunks (no padding): sequence b owns packed tokens
+        ``seq_start[b] .. seq_start[b+1]-1`` of ``x`` [N, d] (the ``[start, end)`` bounds
+        convention of cardgym/nn/packing.py:36-40).  Causal inside each chunk, full
+        attention to the cached prefix.  ``readout_offsets=None`` returns every token."""
+
+        device = x.device
+        starts = index_tensor(seq_start, device)
+        return self._run(
+            x, ple, values, cache, n_seqs=starts.numel() - 1, T=0, seq_start=starts,
+            positions=index_tensor(positions, device), rows=None if rows is None else index_tensor(rows, device),
+            readout=None if readout_offsets is None else index_tensor(readout_offsets, device), span=span,
+        )
+
+    def forward_prefill(
+        self,
+        x: torch.Tensor,
+        ple: torch.Tensor | None,
+        values: torch.Tensor | None,
+        cache: KVCache,
+        rows: torch.Tensor | None,
+    ) -> torch.Tensor:
+        """Encode fresh prefixes into cache ``rows`` at positions 0..T-1; last hidden [B, d]
+        (trunk.py:376-389)."""
+
+        batch, length = x.shape[0], x.shape[1]
+        if length > cache.max_len:
+            raise IndexError("prefill longer than the pool's max_len")
+        device = x.device
+        positions = torch.zeros(batch, dtype=torch.int64, device=device)
+        readout = torch.full((batch,), length - 1, dtype=torch.int64, device=device)
+        return self._run(
+            x, ple, values, cache, n_seqs=batch, T=length, seq_start=None, positions=positions,
+            rows=None if rows is None else index_tensor(rows, device), readout=readout, span=None,
+        )
+
+    def forward(
+        self,
+        x: torch.Tensor,
+        ple: torch.Tensor | None,
+        values: torch.Tensor | None,
+        bounds: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Full causal forward over [B, T, d]; final-norm hidden states [B, T, d]
+        (trunk.py:348-374), run as a prefill into a scratch pool."""
+
+        if bounds is not None:
+            raise ValueError("Packed full forwards take forward_packed with a cache.")
+        batch, length = x.shape[0], x.shape[1]
+        cache = KVCache(
+            n_layers=self.config.n_layers, kv_heads=self.config.n_kv_heads, head_dim=self.config.head_dim,
+            capacity=batch, max_len=length, device=x.device, dtype=torch.float32,
+        )
+        positions = torch.zeros(batch, dtype=torch.int64, device=x.device)
+        hidden = self._run(
+            x, ple, values, cache, n_seqs=batch, T=length, seq_start=None, positions=positions,
+            rows=None, readout=None, span=None,
+        )
+        return hidden.view(batch, length, self.config.d_model)

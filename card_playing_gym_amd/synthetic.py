@@ -1,0 +1,261 @@
+"""The synthetic self-play model and workloads the benchmark configurations are quoted on.
+
+Model: a single-field token embedder (``Embedding(vocab, d_model)``, N(0, 0.02)) in front
+of the trunk, with the two heads a rollout wave evaluates at each readout row: policy
+logits ``Linear(d_model, vocab)`` and the per-seat value MLP ``value_mlp(d_model, 2)``
+(cardgym/nn/model.py:12-17; the graphed wave computes every head at every readout,
+cardgym/rl/graphs.py:88-104).  Weights are random-init from ``torch.manual_seed(seed)``.
+
+Workloads: the five configurations of the benchmark (KV-cached decode of many concurrent
+games).  ``Workload.plan`` produces the per-step host descriptors deterministically from
+``numpy.random.default_rng(seed)``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+from torch import nn
+
+from . import _native as nat
+from .nn.kv_cache import require_device, stream_handle
+from .nn.model import SequenceModel, value_mlp
+from .nn.trunk import TrunkConfig, _param, compute_dtype_code, init_weights
+
+VOCAB = 512
+
+
+class SyntheticModel(SequenceModel):
+    """Embedding -> trunk -> (policy logits, seat values)."""
+
+    graphable_heads = True
+    policy_heads = ("policy",)
+
+    def __init__(self, trunk_config: TrunkConfig, vocab: int = VOCAB, seats: int = 2) -> None:
+        super().__init__(trunk_config)
+        d = trunk_config.d_model
+        self.vocab = vocab
+        self.embedding = nn.Embedding(vocab, d)
+        init_weights(self.embedding)
+        self.policy_head = nn.Linear(d, vocab)
+        init_weights(self.policy_head)
+        self.value_head = value_mlp(d, seats)
+
+    def embed(self, tokens: torch.Tensor):
+        return self.embedding(tokens[..., 0]), None, None
+
+    def prepare(self, tokens: torch.Tensor):
+        """Embedding lookup fused with the trunk's input RMSNorm (one kernel)."""
+
+        trunk = self.trunk
+        if trunk.input_norm is None:
+            return super().prepare(tokens)
+        require_device(tokens)
+        ids = tokens[..., 0].reshape(-1).to(torch.int64).contiguous()
+        d = self.trunk_config.d_model
+        out = torch.empty((ids.numel(), d), device=tokens.device, dtype=torch.float32)
+        nat.call(
+            "cg_embed_rmsnorm", _param(self.embedding.weight).data_ptr(), self.vocab, ids.data_ptr(),
+            _param(trunk.input_norm.weight).data_ptr(), float(trunk.input_norm.eps), out.data_ptr(),
+            ids.numel(), d, None, stream_handle(tokens.device),
+        )
+        return out.view(*tokens.shape[:-1], d), None, None
+
+    def heads(self, hidden: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Policy logits [B, vocab] and seat values [B, seats], fp32."""
+
+        require_device(hidden)
+        device = hidden.device
+        compute = compute_dtype_code(device)
+        stream = stream_handle(device)
+        h = hidden.float().contiguous()
+        m, d = h.shape
+        logits = torch.empty((m, self.vocab), device=device, dtype=torch.float32)
+        nat.call(
+            "cg_linear", h.data_ptr(), _param(self.policy_head.weight).data_ptr(),
+            _param(self.policy_head.bias).data_ptr(), logits.data_ptr(), m, self.vocab, d,
+            nat.CG_ACT_NONE, compute, stream,
+        )
+        first, last = self.value_head[0], self.value_head[2]
+        mid = torch.empty((m, first.out_features), device=device, dtype=torch.float32)
+        nat.call(
+            "cg_linear", h.data_ptr(), _param(first.weight).data_ptr(), _param(first.bias).data_ptr(),
+            mid.data_ptr(), m, first.out_features, d, nat.CG_ACT_GELU, compute, stream,
+        )
+        values = torch.empty((m, last.out_features), device=device, dtype=torch.float32)
+        nat.call(
+            "cg_linear", mid.data_ptr(), _param(last.weight).data_ptr(), _param(last.bias).data_ptr(),
+            values.data_ptr(), m, last.out_features, first.out_features, nat.CG_ACT_NONE, compute, stream,
+        )
+        return logits, values
+
+
+def build_model(config: TrunkConfig, seed: int = 0, device: str | torch.device = "cpu") -> SyntheticModel:
+    """Random-init synthetic model from ``torch.manual_seed(seed)`` (CPU init, then moved)."""
+
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        model = SyntheticModel(config)
+    return model.to(device).eval()
+
+
+def trunk_config(n_layers: int) -> TrunkConfig:
+    """The benchmark trunk: d 256, 8 / 2 heads (head_dim 32), MLP 4x, input RMSNorm."""
+
+    return TrunkConfig(d_model=256, n_layers=n_layers, n_heads=8, n_kv_heads=2, d_ff=1024)
+
+
+@dataclass(frozen=True)
+class Workload:
+    """One benchmark configuration.
+
+    ``mode``: "grow" (every game appends one token per step), "continuous" (slots reset
+    when their game ends, rows gathered through a fresh permutation each step) or
+    "chunks" (every game appends a causal chunk of 1..max_chunk tokens, packed).
+    """
+
+    name: str
+    n_layers: int
+    games: int
+    kv_dtype: torch.dtype
+    precision: str  # "fp32" or "bf16" (autocast of the projections)
+    mode: str
+    length_low: int
+    length_high: int  # inclusive
+    max_len_cap: int = 0  # 0: derived from the lengths and the step count
+    end_probability: float = 0.0
+    max_chunk: int = 1
+    description: str = ""
+    extra: dict = field(default_factory=dict, compare=False)
+
+    def trunk_config(self) -> TrunkConfig:
+        return trunk_config(self.n_layers)
+
+    def max_len(self, steps: int) -> int:
+        if self.max_len_cap:
+            return self.max_len_cap
+        return self.length_high + steps * self.max_chunk + 1
+
+    def capacity(self) -> int:
+        return self.games
+
+    def tokens_per_step_mean(self) -> float:
+        return self.games * (1 + self.max_chunk) / 2 if self.mode == "chunks" else float(self.games)
+
+
+WORKLOADS = {
+    "cfg1": Workload(
+        "cfg1", 8, 64, torch.float32, "fp32", "grow", 0, 0,
+        description="8 layers, fp32, 64 games decoding 1 token per step from length 0 to 128",
+    ),
+    "cfg2": Workload(
+        "cfg2", 8, 1024, torch.float32, "fp32", "grow", 1, 256,
+        description="8 layers, fp32, 1024 games, lengths U[1,256], 1 token per game per step",
+    ),
+    "cfg3": Workload(
+        "cfg3", 16, 4096, torch.bfloat16, "bf16", "grow", 1, 512,
+        description="16 layers, bf16 KV + bf16 projections with fp32 accumulation, 4096 games, "
+        "lengths U[1,512], context grows one token per step",
+    ),
+    "cfg4": Workload(
+        "cfg4", 16, 8192, torch.bfloat16, "bf16", "continuous", 0, 0, max_len_cap=2048,
+        end_probability=1.0 / 200.0,
+        description="8192 slots, 16 layers, bf16; games end with p=1/200 and their slot restarts at "
+        "length 0; rows through a fresh random slot permutation each step; max_len 2048",
+    ),
+    "cfg5": Workload(
+        "cfg5", 16, 4096, torch.bfloat16, "bf16", "chunks", 0, 480, max_chunk=16,
+        description="4096 games appending causal chunks of U{1..16} tokens onto lengths U[0,480], "
+        "packed varlen rows, 16 layers, bf16",
+    ),
+}
+
+
+@dataclass
+class StepPlan:
+    """Host descriptors of one step (numpy int64)."""
+
+    tokens: np.ndarray  # [n_tokens] token ids (packed)
+    positions: np.ndarray  # [n_seqs] cache length before the step
+    rows: np.ndarray  # [n_seqs] cache rows
+    seq_start: np.ndarray  # [n_seqs + 1]
+    readout: np.ndarray  # [n_seqs] offset of the last token of each chunk
+
+    @property
+    def n_tokens(self) -> int:
+        return int(self.seq_start[-1])
+
+    @property
+    def T(self) -> int:
+        """Tokens per sequence when every chunk has the same length, else 0."""
+
+        counts = np.diff(self.seq_start)
+        return int(counts[0]) if counts.size and (counts == counts[0]).all() else 0
+
+
+class Driver:
+    """Deterministic host-side generator of a workload's steps (seeded numpy)."""
+
+    def __init__(self, workload: Workload, seed: int = 0, max_len: int | None = None) -> None:
+        self.workload = workload
+        self.rng = np.random.default_rng(seed)
+        w = workload
+        self.max_len = max_len
+        if w.mode == "continuous":
+            # Stationary Geometric(p) ages of games in flight, capped below max_len.
+            cap = (max_len or w.max_len_cap) - 2
+            ages = self.rng.geometric(w.end_probability, size=w.games) - 1
+            self.lengths = np.minimum(ages, cap).astype(np.int64)
+            self.ended = 0
+        else:
+            self.lengths = self.rng.integers(w.length_low, w.length_high + 1, size=w.games).astype(np.int64)
+
+    def step(self) -> StepPlan:
+        w = self.workload
+        games = w.games
+        if w.mode == "chunks":
+            counts = self.rng.integers(1, w.max_chunk + 1, size=games).astype(np.int64)
+        else:
+            counts = np.ones(games, dtype=np.int64)
+        seq_start = np.zeros(games + 1, dtype=np.int64)
+        np.cumsum(counts, out=seq_start[1:])
+        tokens = self.rng.integers(0, VOCAB, size=int(seq_start[-1])).astype(np.int64)
+        if w.mode == "continuous":
+            rows = self.rng.permutation(games).astype(np.int64)
+            positions = self.lengths[rows].copy()
+        else:
+            rows = np.arange(games, dtype=np.int64)
+            positions = self.lengths.copy()
+        plan = StepPlan(tokens, positions, rows, seq_start, counts - 1)
+        # Advance the host state.
+        if w.mode == "continuous":
+            self.lengths += 1
+            cap = (self.max_len or w.max_len_cap) - 2
+            ended = (self.rng.random(games) < w.end_probability) | (self.lengths >= cap)
+            self.ended += int(ended.sum())
+            self.lengths[ended] = 0
+        else:
+            self.lengths += counts
+        return plan
+
+
+def kv_bytes(plan: StepPlan, n_layers: int, kv_heads: int, head_dim: int, itemsize: int) -> int:
+    """Algorithmic K+V bytes one step's attention reads: each (game, KV head) prefix,
+    new tokens included, read once for all of its queries."""
+
+    counts = np.diff(plan.seq_start)
+    keys = int((plan.positions + counts).sum())
+    return keys * kv_heads * head_dim * 2 * itemsize * n_layers
+
+
+def projection_flops(config: TrunkConfig, n_tokens: int) -> int:
+    d, h, kv = config.d_model, config.n_heads * config.head_dim, config.kv_width
+    per_token = 2 * d * (h + 2 * kv) + 2 * h * d + 2 * d * config.d_ff * 2
+    return per_token * n_tokens * config.n_layers
+
+
+def round_up(value: int, multiple: int) -> int:
+    return int(math.ceil(value / multiple) * multiple)

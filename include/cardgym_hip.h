@@ -1,0 +1,241 @@
+/*
+ * cardgym_hip.h -- C ABI of libcardgym_hip.so, the gfx950 (MI355X) kernels behind the
+ * KV-cached ragged decode step of the cardgym GQA trunk.
+ *
+ * Conventions shared by every entry point:
+ *   - Plain pointers and sizes only.  Every tensor pointer is a device pointer unless the
+ *     comment says "host".  Tensors are dense row-major unless strides are passed.
+ *   - Each call enqueues work on `stream` (a hipStream_t passed as void*; NULL = the
+ *     null stream) and returns at once.  Nothing is read back to the host and nothing is
+ *     allocated per call, so every call may be captured into a hipGraph.  The only calls
+ *     that allocate are cg_trunk_create / cg_trunk_destroy.
+ *   - The return value is a status (CG_OK = 0).  On failure, cg_last_error() returns the
+ *     message for the calling thread.  No C++ exception crosses this boundary.
+ *   - Integer index arrays that mirror PyTorch int64 tensors (rows, positions, offsets)
+ *     are int64_t.
+ *
+ * Each declaration cites the reference interface it replaces (paths are into the
+ * maxrlinder/card_playing_gym source tree).
+ */
+#ifndef CARDGYM_HIP_H
+#define CARDGYM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------------- */
+#define CG_OK 0
+#define CG_ERR_INVALID 1     /* bad argument: shape, dtype, null pointer      -> ValueError   */
+#define CG_ERR_UNSUPPORTED 2 /* valid but not built (e.g. head_dim 40)        -> ValueError   */
+#define CG_ERR_RANGE 3       /* index or size out of range                    -> IndexError   */
+#define CG_ERR_HIP 4         /* the HIP runtime reported an error             -> RuntimeError */
+
+/* ---- element types ------------------------------------------------------------- */
+#define CG_F32 0
+#define CG_BF16 1
+#define CG_F16 2
+
+/* ---- activations for cg_linear ----------------------------------------------- */
+#define CG_ACT_NONE 0
+#define CG_ACT_GELU 1 /* exact erf GELU, torch.nn.GELU() */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int cg_version(void);
+
+/* Copies the calling thread's last error message into buf (always NUL-terminated);
+ * returns the message length. */
+size_t cg_last_error(char *buf, size_t size);
+
+/* One layer of a KV pool: k and v are each [capacity, kv_heads, max_len, head_dim]
+ * contiguous, element type `dtype`.  Mirrors KVCache.k[layer] / KVCache.v[layer]
+ * (cardgym/nn/kv_cache.py:45-59). */
+typedef struct cg_kv_layer {
+  void *k;
+  void *v;
+  int32_t capacity;
+  int32_t kv_heads;
+  int32_t max_len;
+  int32_t head_dim;
+  int32_t dtype; /* CG_F32, CG_BF16 or CG_F16 */
+} cg_kv_layer;
+
+/* Strided source of new keys or values, logically [B, kv_heads, T, head_dim]; the
+ * head_dim stride must be 1.  The reference passes transposed views of the QKV split
+ * (cardgym/nn/trunk.py:147-152), hence the explicit strides. */
+typedef struct cg_kv_source {
+  const void *data;
+  int32_t dtype;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_t;
+} cg_kv_source;
+
+/* KVCache.write_step (cardgym/nn/kv_cache.py:84-105): for every b < B, t < T and head,
+ * cache[rows[b], head, positions[b*T + t], :] = new[b, head, t, :] cast to the cache
+ * dtype (round to nearest even, NaN -> canonical quiet NaN, as Tensor.to).  rows may be
+ * NULL for 0..B-1.  positions is int64 [B, T] (for T = 1 the reference's [B] form).
+ * Positions must lie in [0, max_len); rows in [0, capacity): out-of-range entries are
+ * skipped on the device and reported by cg_kv_check_indices. */
+int cg_kv_write_step(const cg_kv_layer *layer, const int64_t *rows, const int64_t *positions,
+                     const cg_kv_source *k_new, const cg_kv_source *v_new, int32_t B, int32_t T,
+                     void *stream);
+
+/* KVCache.write_range (cardgym/nn/kv_cache.py:65-82): positions start..start+T-1 of
+ * rows (NULL = 0..B-1). */
+int cg_kv_write_range(const cg_kv_layer *layer, const int64_t *rows, int32_t start,
+                      const cg_kv_source *k_new, const cg_kv_source *v_new, int32_t B, int32_t T,
+                      void *stream);
+
+/* KVCache.read with explicit rows (cardgym/nn/kv_cache.py:107-120): gathers
+ * [B, kv_heads, length, head_dim] copies of the first `length` positions of rows[b]
+ * into k_out / v_out (cache dtype, contiguous).  rows NULL = 0..B-1. */
+int cg_kv_read(const cg_kv_layer *layer, const int64_t *rows, int32_t B, int32_t length,
+               void *k_out, void *v_out, void *stream);
+
+/* KVCache.copy_rows (cardgym/nn/kv_cache.py:122-138) for one layer: the first `length`
+ * positions of rows sources[i] are copied onto targets[i].  Sources and targets must not
+ * overlap (the reference copies through a gathered temporary). */
+int cg_kv_copy_rows(const cg_kv_layer *layer, const int64_t *sources, const int64_t *targets,
+                    int32_t n, int32_t length, void *stream);
+
+/* Validates row and position indices on the device (no host read-back): flag[0] is set
+ * to 1 if any rows[b] is outside [0, capacity) or positions[i] outside [0, max_len).
+ * flag must be zeroed by the caller.  n_pos is the length of positions. */
+int cg_kv_check_indices(const cg_kv_layer *layer, const int64_t *rows, int32_t B,
+                        const int64_t *positions, int32_t n_pos, int32_t *flag, void *stream);
+
+/* Ragged GQA decode attention straight from the pool: the custom op
+ * cardgym::decode_attention (cardgym/nn/cuda_decode.py:172-202) and the gather + masked
+ * softmax fallback it replaces (cardgym/nn/trunk.py:216-256), without their
+ * head_dim 32 / span 64 / fp16 limits.
+ *   q       [B, n_heads, T, head_dim] with strides (q_sb, q_sh, q_st), type q_dtype
+ *   rows    int64 [B] cache rows (NULL = 0..B-1)
+ *   key_lengths int64 [B]: query t of row b sees keys < min(key_lengths[b] + t, span)
+ *   out     [B, n_heads, T, head_dim] contiguous, type out_dtype
+ * Scores, softmax and accumulation are fp32 whatever the storage types. */
+int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                        const cg_kv_layer *layer, const int64_t *rows, const int64_t *key_lengths,
+                        int32_t B, int32_t n_heads, int32_t T, int32_t span, float scale, void *out,
+                        int32_t out_dtype, void *stream);
+
+/* ---- fused trunk ------------------------------------------------------------------ */
+
+/* TrunkConfig (cardgym/nn/trunk.py:39-91). */
+typedef struct cg_trunk_config {
+  int32_t d_model;
+  int32_t n_layers;
+  int32_t n_heads;
+  int32_t n_kv_heads;
+  int32_t d_ff;
+  int32_t per_layer_dim;  /* PLE width per layer, 0 = off */
+  int32_t value_width;    /* columns of the value-embedding stream (n_value_layers * kv_width) */
+  float eps;              /* LayerNorm epsilon (nn.LayerNorm default 1e-5) */
+} cg_trunk_config;
+
+/* One DecoderBlock's parameters (cardgym/nn/trunk.py:124-139), fp32 device tensors in
+ * torch nn.Linear layout ([out, in] row-major).  value_index is the block's slot in the
+ * value-embedding stream, or -1 (Trunk._value, trunk.py:314-316). */
+typedef struct cg_layer_params {
+  const float *ln_attn_w;
+  const float *ln_attn_b;
+  const float *qkv_w;      /* [(n_heads + 2 kv_heads) * head_dim, d_model] */
+  const float *out_w;      /* [d_model, n_heads * head_dim] */
+  const float *ln_mlp_w;
+  const float *ln_mlp_b;
+  const float *mlp_up_w;   /* [d_ff, d_model] */
+  const float *mlp_up_b;   /* [d_ff] */
+  const float *mlp_down_w; /* [d_model, d_ff] */
+  const float *mlp_down_b; /* [d_model] */
+  int32_t value_index;
+} cg_layer_params;
+
+typedef struct cg_trunk cg_trunk; /* opaque */
+
+/* Builds a trunk over caller-owned fp32 parameters.  compute_dtype CG_F32 runs every
+ * projection in fp32; CG_BF16 runs them as bf16 x bf16 with fp32 accumulation (the
+ * projections of torch.autocast(bfloat16), trunk.py:143/156-157 under
+ * cardgym/core/devices.py:32-43) from bf16 weight copies the handle owns.  layers is a
+ * host array of n_layers entries; the pointers are kept, not copied.  Allocates. */
+int cg_trunk_create(const cg_trunk_config *config, const cg_layer_params *layers,
+                    const float *final_ln_w, const float *final_ln_b, int32_t compute_dtype,
+                    cg_trunk **out);
+
+/* Re-derives the handle's weight copies from the fp32 parameters (after the caller has
+ * changed them, e.g. load_state_dict). */
+int cg_trunk_refresh(cg_trunk *trunk, void *stream);
+
+int cg_trunk_destroy(cg_trunk *trunk);
+
+/* One ragged step (or prefill) over packed tokens.  Mirrors the metadata of
+ * Trunk.forward_ragged (cardgym/nn/trunk.py:391-429) with packed-row descriptors
+ * (cardgym/nn/packing.py:36-40):
+ *   n_seqs sequences; sequence b owns tokens seq_start[b] .. seq_start[b+1]-1 of the
+ *   packed [n_tokens, d_model] input (seq_start NULL = padded: T tokens each, n_tokens =
+ *   n_seqs * T); positions[b] is its cache length before the step, rows[b] its cache row
+ *   (NULL = b); token t of sequence b is written at min(positions[b] + t, max_len - 1)
+ *   and its query sees keys < min(positions[b] + 1 + t, span).
+ *   readout[b] (NULL = every token) is the offset within sequence b whose final-norm
+ *   hidden state is returned. */
+typedef struct cg_ragged {
+  int32_t n_seqs;
+  int32_t n_tokens;
+  int32_t T;                 /* tokens per sequence when seq_start is NULL */
+  int32_t span;              /* key cap; <= 0 means max_len */
+  const int64_t *seq_start;  /* int64 [n_seqs + 1] or NULL */
+  const int64_t *positions;  /* int64 [n_seqs] */
+  const int64_t *rows;       /* int64 [n_seqs] or NULL */
+  const int64_t *readout;    /* int64 [n_seqs] or NULL */
+} cg_ragged;
+
+/* Workspace bytes cg_trunk_forward needs for n_tokens tokens and n_seqs sequences. */
+size_t cg_trunk_workspace_size(const cg_trunk *trunk, int32_t n_tokens, int32_t n_seqs);
+
+/* Trunk.forward_ragged / Trunk.forward_prefill (cardgym/nn/trunk.py:376-429): every
+ * block of the trunk over the packed tokens, appending their K/V to `cache` (an array of
+ * n_layers cg_kv_layer, host), then the final LayerNorm at the readout tokens.
+ *   x       fp32 [n_tokens, d_model], already conditioned (Trunk.condition); not modified
+ *   ple     fp32 [n_tokens, n_layers * per_layer_dim] or NULL (Trunk._add_ple)
+ *   values  fp32 [n_tokens, value_width] or NULL (value embeddings, added to V)
+ *   hidden  fp32 [n_seqs, d_model] (readout given) or [n_tokens, d_model] (readout NULL) */
+int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
+                     const float *ple, const float *values, const cg_ragged *step, float *hidden,
+                     void *workspace, size_t workspace_size, void *stream);
+
+/* ---- conditioning, embedding and heads ------------------------------------------ */
+
+/* RMSNorm (cardgym/nn/trunk.py:104-115): y = rms_norm(x, eps) * gain, rows of width d. */
+int cg_rmsnorm(const float *x, const float *gain, float eps, float *y, int32_t n, int32_t d,
+               void *stream);
+
+/* Embedding lookup then RMSNorm: y[i] = rms_norm(table[ids[i]]) * gain, the synthetic
+ * single-field embedder followed by Trunk.condition's input norm
+ * (cardgym/nn/model.py:45-48, cardgym/nn/trunk.py:297-298).  Ids outside [0, vocab)
+ * produce zero rows and set flag[0] = 1 when flag is not NULL. */
+int cg_embed_rmsnorm(const float *table, int32_t vocab, const int64_t *ids, const float *gain,
+                     float eps, float *y, int32_t n, int32_t d, int32_t *flag, void *stream);
+
+/* y = act(x @ w^T + bias) for fp32 x [m, k], w [n, k], bias [n] or NULL: the nn.Linear
+ * layers of the heads evaluated at readout rows (cardgym/rl/graphs.py:88-104,
+ * cardgym/nn/model.py:12-17).  compute_dtype CG_BF16 rounds x and w to bf16 (autocast). */
+int cg_linear(const float *x, const float *w, const float *bias, float *y, int32_t m, int32_t n,
+              int32_t k, int32_t act, int32_t compute_dtype, void *stream);
+
+/* y = (x @ w^T + addend) * scale for fp32 x [m, k], w [n, k], addend [m, n]: the per-layer
+ * embedding stream of Trunk.condition, ple = (ple_lookup + ple_context(x)) / sqrt(2)
+ * (cardgym/nn/trunk.py:301-306). */
+int cg_linear_add_scale(const float *x, const float *w, const float *addend, float *y, int32_t m,
+                        int32_t n, int32_t k, float scale, int32_t compute_dtype, void *stream);
+
+/* Adds `delta` to every entry of the int64 array a (n entries): the synthetic driver's
+ * "every game appended one token" position update, kept on the device. */
+int cg_advance_positions(int64_t *positions, int32_t n, int64_t delta, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CARDGYM_HIP_H */

@@ -1,0 +1,352 @@
+"""Pins the oracle (oracle/reference_path.py) before it is trusted as the checker.
+
+Each oracle function is checked against something that does not retype its formula:
+
+  RefCache.write_step / write_range / read   per-element Python loops on tiny pools; the
+                                             bf16 / fp16 casts against an independent
+                                             bit-level round-to-nearest-even
+  RefCache.copy_rows                         the reference's known answer
+                                             (tests/nn/test_trunk.py:81-88)
+  RefTrunk.grouped_attention                 float64 brute-force softmax loops; closed-form
+                                             special cases (one key -> v0, equal keys -> mean
+                                             of V, one dominant logit -> that V)
+  RefTrunk.forward_full                      a float64 NumPy transformer written per element
+                                             (LayerNorm, erf GELU, causal GQA, PLE, VE)
+  RefTrunk.forward_ragged / forward_prefill  the reference's invariant: cached ragged decode
+                                             equals the full causal forward to 1e-5
+                                             (tests/nn/test_trunk.py:38-78), with gathered
+                                             rows, PLE and value embeddings switched on
+  conditioning                               zero PLE / VE tables leave the function
+                                             unchanged (tests/nn/test_trunk.py:91-104)
+  bf16 rounding policy                       golden vectors written by the reference's own
+                                             trunk (tests/golden/), when present
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from card_playing_gym_amd.nn.trunk import Trunk, TrunkConfig
+from oracle.reference_path import RefCache, RefConfig, RefTrunk, ref_config_of
+
+
+# ---- helpers -------------------------------------------------------------------------
+
+
+def bf16_rne_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit pattern, round to nearest even, written on the bit level."""
+
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    rounded[nan] = 0x7FC0
+    return rounded
+
+
+def random_trunk(config: TrunkConfig, seed: int = 0, scale: float = 0.05) -> dict[str, torch.Tensor]:
+    """A trunk state dict with every parameter perturbed (so zero-initialised PLE / VE
+    tables and biases carry signal), like the reference's ``randomize`` fixture."""
+
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        trunk = Trunk(config)
+        gen = torch.Generator().manual_seed(seed + 1)
+        with torch.no_grad():
+            for p in trunk.parameters():
+                p.add_(scale * torch.randn(p.shape, generator=gen))
+    return {f"trunk.{k}": v.detach().clone() for k, v in trunk.state_dict().items()}
+
+
+# ---- KV pool -------------------------------------------------------------------------
+
+
+def test_write_step_matches_element_loops():
+    gen = torch.Generator().manual_seed(0)
+    cache = RefCache(1, 2, 4, capacity=5, max_len=6, dtype=torch.float32)
+    rows = torch.tensor([3, 0, 4])
+    positions = torch.tensor([[1, 2], [0, 1], [4, 5]])
+    k = torch.randn(3, 2, 2, 4, generator=gen)
+    v = torch.randn(3, 2, 2, 4, generator=gen)
+    cache.write_step(0, rows, positions, k, v)
+    expect_k = np.zeros((5, 2, 6, 4), dtype=np.float32)
+    expect_v = np.zeros((5, 2, 6, 4), dtype=np.float32)
+    for b in range(3):
+        for h in range(2):
+            for t in range(2):
+                for d in range(4):
+                    expect_k[rows[b], h, positions[b, t], d] = k[b, h, t, d]
+                    expect_v[rows[b], h, positions[b, t], d] = v[b, h, t, d]
+    assert np.array_equal(cache.k[0].numpy(), expect_k) and np.array_equal(cache.v[0].numpy(), expect_v)
+    # The [B] form writes one position per row.
+    cache.write_step(0, torch.tensor([2]), torch.tensor([3]), k[:1, :, :1], v[:1, :, :1])
+    assert torch.equal(cache.k[0][2, :, 3], k[0, :, 0])
+    with pytest.raises(ValueError):
+        cache.write_step(0, torch.tensor([2]), torch.tensor([3]), k[:1], v[:1])
+
+
+def test_cache_casts_are_round_to_nearest_even():
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(4096, generator=gen) * 10
+    x[:4] = torch.from_numpy(np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x7F7FFFFF], dtype=np.uint32).view(np.float32))
+    cache = RefCache(1, 1, 4096, capacity=1, max_len=1, dtype=torch.bfloat16)
+    cache.write_range(0, None, 0, x.view(1, 1, 1, -1), x.view(1, 1, 1, -1))
+    got = cache.k[0].view(-1).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, bf16_rne_bits(x.numpy()))
+    half = RefCache(1, 1, 4096, capacity=1, max_len=1, dtype=torch.float16)
+    half.write_range(0, None, 0, x.view(1, 1, 1, -1), x.view(1, 1, 1, -1))
+    with np.errstate(over="ignore"):
+        assert np.array_equal(half.k[0].view(-1).numpy(), x.numpy().astype(np.float16))
+
+
+def test_write_range_and_read_match_loops():
+    gen = torch.Generator().manual_seed(2)
+    cache = RefCache(2, 2, 3, capacity=4, max_len=7, dtype=torch.float32)
+    k = torch.randn(2, 2, 3, 3, generator=gen)
+    cache.write_range(1, torch.tensor([3, 1]), 2, k, -k)
+    for b, row in enumerate([3, 1]):
+        for t in range(3):
+            assert torch.equal(cache.k[1][row, :, 2 + t], k[b, :, t])
+            assert torch.equal(cache.v[1][row, :, 2 + t], -k[b, :, t])
+    kr, vr = cache.read(1, torch.tensor([1, 1, 3]), 5)
+    for i, row in enumerate([1, 1, 3]):
+        assert torch.equal(kr[i], cache.k[1][row, :, :5]) and torch.equal(vr[i], cache.v[1][row, :, :5])
+    dense, _ = cache.read(1, None, 4, count=2)
+    assert dense.data_ptr() == cache.k[1].data_ptr() and dense.shape == (2, 2, 4, 3)
+
+
+def test_copy_rows_known_answer():
+    """tests/nn/test_trunk.py:81-88 of the reference."""
+
+    cache = RefCache(2, 1, 2, capacity=4, max_len=5)
+    for layer in range(2):
+        cache.k[layer][:] = torch.arange(4, dtype=torch.float32).view(4, 1, 1, 1)
+        cache.v[layer][:] = -torch.arange(4, dtype=torch.float32).view(4, 1, 1, 1)
+    cache.copy_rows(torch.tensor([2, 3]), torch.tensor([1, 2]), length=3)
+    assert cache.k[1][:, 0, 0, 0].tolist() == [0.0, 2.0, 3.0, 3.0]
+    assert cache.v[0][1, 0, 3, 0].item() == -1.0
+
+
+# ---- attention -----------------------------------------------------------------------
+
+
+def brute_attention(q, k, v, key_lengths, group):
+    """float64 loops: q [B, H, T, D], k/v [B, KVH, S, D]."""
+
+    B, H, T, D = q.shape
+    out = np.zeros((B, H, T, D))
+    scale = 1.0 / math.sqrt(D)
+    for b in range(B):
+        for h in range(H):
+            kv = h // group
+            for t in range(T):
+                limit = min(int(key_lengths[b]) + t, k.shape[2])
+                scores = [sum(q[b, h, t, d] * k[b, kv, s, d] for d in range(D)) * scale for s in range(limit)]
+                m = max(scores)
+                w = [math.exp(x - m) for x in scores]
+                total = sum(w)
+                for d in range(D):
+                    out[b, h, t, d] = sum(w[s] * v[b, kv, s, d] for s in range(limit)) / total
+    return out
+
+
+def _trunk_for_attention(n_heads=4, kv_heads=2, head_dim=4):
+    config = RefConfig(d_model=n_heads * head_dim, n_layers=1, n_heads=n_heads, n_kv_heads=kv_heads, d_ff=8)
+    return RefTrunk({}, config)
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_grouped_attention_matches_float64_loops(T):
+    gen = torch.Generator().manual_seed(3)
+    trunk = _trunk_for_attention()
+    B, S = 3, 9
+    q = torch.randn(B, 4, T, 4, generator=gen, dtype=torch.float64)
+    k = torch.randn(B, 2, S, 4, generator=gen, dtype=torch.float64)
+    v = torch.randn(B, 2, S, 4, generator=gen, dtype=torch.float64)
+    key_lengths = torch.tensor([1, 4, S - T + 1])
+    got = trunk.grouped_attention(q, k, v, key_lengths).numpy()
+    want = brute_attention(q.numpy(), k.numpy(), v.numpy(), key_lengths.numpy(), group=2)
+    # Softmax runs in fp32 whatever the input dtype (trunk.py:255), hence 1e-6 on float64 data.
+    assert np.abs(got - want).max() < 1e-6
+
+
+def test_grouped_attention_special_cases():
+    trunk = _trunk_for_attention()
+    gen = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 4, 1, 4, generator=gen, dtype=torch.float64)
+    v = torch.randn(1, 2, 6, 4, generator=gen, dtype=torch.float64)
+    k = torch.randn(1, 2, 6, 4, generator=gen, dtype=torch.float64)
+    # One visible key: the output is that key's value, whatever the scores.
+    out = trunk.grouped_attention(q, k, v, torch.tensor([1]))
+    assert torch.allclose(out[0, :2, 0], v[0, 0, 0].expand(2, 4)) and torch.allclose(out[0, 2:, 0], v[0, 1, 0].expand(2, 4))
+    # Identical keys: uniform weights, the mean of the visible values.
+    same = k[:, :, :1].expand_as(k).contiguous()
+    out = trunk.grouped_attention(q, same, v, torch.tensor([5]))
+    assert torch.allclose(out[0, 0, 0], v[0, 0, :5].mean(0)) and torch.allclose(out[0, 3, 0], v[0, 1, :5].mean(0))
+    # One dominant logit selects its value.
+    big = k.clone()
+    big[0, 0, 3] = 1e3 * q[0, 0, 0]
+    out = trunk.grouped_attention(q, big, v, torch.tensor([6]))
+    assert torch.allclose(out[0, 0, 0], v[0, 0, 3])
+
+
+# ---- full forward against a float64 transformer ------------------------------------------
+
+
+def np_layer_norm(x, w, b, eps=1e-5):
+    mean = x.mean(-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(-1, keepdims=True)
+    return (x - mean) / np.sqrt(var + eps) * w + b
+
+
+def np_gelu(x):
+    return 0.5 * x * (1.0 + np.vectorize(math.erf)(x / math.sqrt(2.0)))
+
+
+def np_full_forward(state, c: RefConfig, x, ple, values):
+    """Per-element float64 statement of the trunk's full causal forward."""
+
+    s = {k: v.double().numpy() for k, v in state.items()}
+    B, T, d = x.shape
+    G, D = c.n_heads // c.n_kv_heads, c.head_dim
+    x = x / np.sqrt((x**2).mean(-1, keepdims=True) + 1e-5) * s["trunk.input_norm.weight"]
+    if c.per_layer_dim:
+        ple = ((ple + x @ s["trunk.ple_context.weight"].T) / math.sqrt(2.0)).reshape(B, T, c.n_layers, c.per_layer_dim)
+    value_index = {layer: i for i, layer in enumerate(c.value_layers)}
+    for layer in range(c.n_layers):
+        p = lambda n: s[f"trunk.blocks.{layer}.{n}"]  # noqa: E731
+        h = np_layer_norm(x, p("ln_attn.weight"), p("ln_attn.bias"))
+        qkv = h @ p("qkv_proj.weight").T
+        q = qkv[..., : c.n_heads * D].reshape(B, T, c.n_heads, D)
+        k = qkv[..., c.n_heads * D : c.n_heads * D + c.kv_width].reshape(B, T, c.n_kv_heads, D)
+        v = qkv[..., c.n_heads * D + c.kv_width :].reshape(B, T, c.n_kv_heads, D)
+        if layer in value_index:
+            v = v + values.reshape(B, T, -1, c.kv_width)[:, :, value_index[layer]].reshape(B, T, c.n_kv_heads, D)
+        attn = np.zeros((B, T, c.n_heads, D))
+        for b in range(B):
+            for hd in range(c.n_heads):
+                for t in range(T):
+                    sc = np.array([q[b, t, hd] @ k[b, u, hd // G] for u in range(t + 1)]) / math.sqrt(D)
+                    w = np.exp(sc - sc.max())
+                    attn[b, t, hd] = (w[:, None] * v[b, : t + 1, hd // G]).sum(0) / w.sum()
+        x = x + attn.reshape(B, T, -1) @ p("out_proj.weight").T
+        m = np_layer_norm(x, p("ln_mlp.weight"), p("ln_mlp.bias"))
+        m = np_gelu(m @ p("mlp.0.weight").T + p("mlp.0.bias")) @ p("mlp.2.weight").T + p("mlp.2.bias")
+        x = x + m
+        if c.per_layer_dim:
+            upd = ple[:, :, layer]
+            reps = math.ceil(d / c.per_layer_dim)
+            x = x + np.tile(upd, (1, 1, reps))[..., :d] * (1.0 if c.per_layer_dim == d else 1.0 / math.sqrt(reps))
+    return np_layer_norm(x, s["trunk.final_norm.weight"], s["trunk.final_norm.bias"])
+
+
+@pytest.mark.parametrize("ple_dim,ve", [(0, "off"), (4, "alternating"), (6, "all")])
+def test_full_forward_matches_float64_transformer(ple_dim, ve):
+    config = TrunkConfig(d_model=16, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=24, per_layer_dim=ple_dim, value_embeddings=ve)
+    state = random_trunk(config)
+    rc = ref_config_of(config)
+    ref = RefTrunk(state, rc)
+    gen = torch.Generator().manual_seed(5)
+    B, T = 2, 5
+    x = torch.randn(B, T, 16, generator=gen)
+    ple_lookup = torch.randn(B, T, config.ple_width, generator=gen) if ple_dim else None
+    value_lookup = torch.randn(B, T, config.value_width, generator=gen) if ve != "off" else None
+    got = ref.forward_full(*ref.condition(x, ple_lookup, value_lookup))
+    want = np_full_forward(state, rc, x.double().numpy(), None if ple_lookup is None else ple_lookup.double().numpy(),
+                           None if value_lookup is None else value_lookup.double().numpy())
+    assert np.abs(got.double().numpy() - want).max() < 2e-5
+
+
+# ---- the reference's invariants --------------------------------------------------------
+
+
+@pytest.mark.parametrize("ple_dim,ve,gathered", [(0, "off", False), (8, "all", True), (12, "alternating", True)])
+def test_ragged_decode_matches_full_forward(ple_dim, ve, gathered):
+    """tests/nn/test_trunk.py:38-78 of the reference, on the oracle: prefill 4 tokens, then
+    ragged waves of 0-3 tokens per row (zero padding for rows that get none, repeat-last
+    padding for the rest) reproduce the full causal forward at rtol = atol = 1e-5."""
+
+    config = TrunkConfig(d_model=32, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=64, per_layer_dim=ple_dim, value_embeddings=ve)
+    state = random_trunk(config)
+    ref = RefTrunk(state, ref_config_of(config))
+    rng = np.random.default_rng(0)
+    B = 6
+    lengths = [int(n) for n in rng.integers(6, 16, size=B)]
+    L = max(lengths)
+    gen = torch.Generator().manual_seed(6)
+    emb = torch.randn(B, L, 32, generator=gen)
+    ple_lookup = torch.randn(B, L, config.ple_width, generator=gen) if ple_dim else None
+    value_lookup = torch.randn(B, L, config.value_width, generator=gen) if ve != "off" else None
+
+    def cond(sl):
+        return ref.condition(emb[sl], None if ple_lookup is None else ple_lookup[sl],
+                             None if value_lookup is None else value_lookup[sl])
+
+    full = ref.forward_full(*cond((slice(None), slice(None))))
+    rows = torch.from_numpy(rng.permutation(B + 2)[:B]) if gathered else None
+    cache = RefCache(2, 2, 8, B + 2 if gathered else B, L + 1)
+    hidden = ref.forward_prefill(*cond((slice(None), slice(0, 4))), cache, rows)
+    torch.testing.assert_close(hidden, full[:, 3], rtol=1e-5, atol=1e-5)
+    cursor = [4] * B
+    while any(c < n for c, n in zip(cursor, lengths)):
+        counts = [min(int(rng.integers(0, 4)), n - c) for c, n in zip(cursor, lengths)]
+        if not any(counts):
+            continue
+        run = max(counts)
+        index = torch.zeros(B, run, dtype=torch.long)
+        offsets = torch.zeros(B, dtype=torch.long)
+        zero = torch.zeros(B, dtype=torch.bool)
+        for row, (start, count) in enumerate(zip(cursor, counts)):
+            if not count:
+                zero[row] = True
+                continue
+            index[row, :count] = torch.arange(start, start + count)
+            index[row, count:] = start + count - 1
+            offsets[row] = count - 1
+        picked = [t[torch.arange(B)[:, None], index] if t is not None else None for t in (emb, ple_lookup, value_lookup)]
+        for t in picked:
+            if t is not None:
+                t[zero] = 0.0
+        x, ple, values = ref.condition(*picked)
+        out = ref.forward_ragged(x, ple, values, cache, torch.tensor(cursor), offsets, rows=rows)
+        for row, (start, count) in enumerate(zip(cursor, counts)):
+            if count:
+                torch.testing.assert_close(out[row], full[row, start + count - 1], rtol=1e-5, atol=1e-5)
+        cursor = [c + n for c, n in zip(cursor, counts)]
+
+
+def test_zero_conditioning_leaves_the_function_unchanged():
+    """tests/nn/test_trunk.py:91-104: PLE and value embeddings start switched off."""
+
+    with_cond = TrunkConfig(d_model=32, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=64, per_layer_dim=8, value_embeddings="all")
+    plain = TrunkConfig(d_model=32, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=64)
+    state = random_trunk(with_cond)
+    state["trunk.ple_context.weight"].zero_()
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(2, 7, 32, generator=gen)
+    a = RefTrunk(state, ref_config_of(with_cond))
+    b = RefTrunk(state, ref_config_of(plain))
+    got = a.forward_full(*a.condition(x, torch.zeros(2, 7, 16), torch.zeros(2, 7, 2 * 16)))
+    torch.testing.assert_close(got, b.forward_full(*b.condition(x, None, None)))
+
+
+def test_bf16_policy_rounds_at_the_reference_points():
+    """Under the bf16 policy every projection output is a bf16 value and the residual
+    stream stays fp32; the result stays near the fp32 path."""
+
+    config = TrunkConfig(d_model=32, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=64)
+    state = random_trunk(config)
+    ref16 = RefTrunk(state, ref_config_of(config), "bf16")
+    ref32 = RefTrunk(state, ref_config_of(config), "fp32")
+    x = torch.randn(2, 6, 32, generator=torch.Generator().manual_seed(8))
+    y = ref16.lin(x, state["trunk.blocks.0.qkv_proj.weight"])
+    assert y.dtype == torch.bfloat16
+    want = (x.bfloat16().double() @ state["trunk.blocks.0.qkv_proj.weight"].bfloat16().double().T)
+    assert (y.double() - want).abs().max() <= 2 ** -7 * want.abs().max()
+    out16 = ref16.forward_full(*ref16.condition(x))
+    out32 = ref32.forward_full(*ref32.condition(x))
+    assert out16.dtype == torch.float32
+    assert 0 < (out16 - out32).abs().max() < 5e-2
