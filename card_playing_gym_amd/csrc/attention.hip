@@ -18,6 +18,8 @@
 //     traffic in the key loop except the 2-step quad reduction of the dot products); the
 //     16 slots and the waves are merged once at the end (log-sum-exp merge);
 //   * softmax in base 2 with log2(e) folded into the query scale.
+#include <type_traits>
+
 #include "attention.h"
 #include "common.h"
 
@@ -274,6 +276,320 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(AttnArgs a
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Matrix-core path (head_dim 32 / 64): one wave per (sequence, KV head), four independent
+// waves per workgroup.  For each tile of KT keys:
+//   S^T[key, query] = K . Q^T on MFMA: the A operand is 16 keys x 32 dims straight from the
+//     pool (lane l reads 16 bytes of key l % 16 at dims 8 (l / 16): one coalesced load of
+//     a contiguous 1 KB segment per 16 keys); the B operand is the group's queries
+//     (G heads x the sequence's new tokens, 16 per column tile), pre-scaled by
+//     scale * log2(e) and rounded to the cache type as the reference rounds q
+//     (trunk.py:222).
+//   Online softmax on the MFMA output layout: lane l holds keys 4 (l / 16) + i of query
+//     column l % 16; the running max is shared by the four lanes of a column.
+//   O^T[dim, query] += V^T . P^T on MFMA: P^T is the lane's own probabilities (the k
+//     ordering of the product is chosen to match where the scores already are, so P never
+//     moves between lanes); V^T is read from a padded per-wave LDS copy of the V tile.
+// Query t of the sequence sees keys < min(key_lengths + t, span): per-column masks.
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(8))) float f32x8;
+
+template <typename TKV>
+struct Mfma16;  // 16-bit operand helpers
+
+template <>
+struct Mfma16<bf16> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ vec from(const f32x8 &f) { return __builtin_convertvector(f, bf16x8); }
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<f16> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ vec from(const f32x8 &f) { return __builtin_convertvector(f, f16x8); }
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <typename TKV, int D, int NQT>
+__global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) {
+  constexpr int ES = int(sizeof(TKV));
+  constexpr bool F32 = ES == 4;
+  constexpr int KT = F32 ? 32 : 64;   // keys per tile
+  constexpr int NJ = KT / 16;         // 16-key score tiles per key tile
+  constexpr int DK = D / 32;          // 32-dim slices of a key (S^T k-steps)
+  constexpr int DH = D / 16;          // 16-dim slices of the output (O^T row tiles)
+  constexpr int ROW = D * ES + 8;     // padded LDS row of V (bytes): conflict-free transposed reads
+  __shared__ __align__(16) unsigned char vtile[4][KT * ROW];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int unit = blockIdx.x * 4 + wave;
+  if (unit >= a.n_seqs * a.kv_heads) return;  // the whole wave leaves; no block barriers below
+  const int b = unit / a.kv_heads, h = unit % a.kv_heads;
+  const int li = lane & 15, lg = lane >> 4;
+  const int G = a.n_heads / a.kv_heads;
+  unsigned char *vt = vtile[wave];
+
+  const int64_t row = a.rows ? a.rows[b] : int64_t(b);
+  int64_t tok0 = 0, count = a.T;
+  if (a.seq_start) {
+    int64_t lo = a.seq_start[b], hi = a.seq_start[b + 1];
+    lo = lo < 0 ? 0 : (lo > a.n_tokens ? a.n_tokens : lo);
+    hi = hi < lo ? lo : (hi > a.n_tokens ? a.n_tokens : hi);
+    tok0 = lo;
+    count = hi - lo;
+  }
+  const int64_t q_base = a.seq_start ? tok0 * a.q_st : int64_t(b) * a.q_sb;
+  const int64_t o_base = a.seq_start ? tok0 * a.o_st : int64_t(b) * a.o_sb;
+  const int64_t kl = a.key_lengths[b] + a.kl_add;
+  const bool row_ok = row >= 0 && row < a.capacity;
+  const int64_t head_off = (row * a.kv_heads + h) * int64_t(a.max_len) * D;
+  const TKV *__restrict__ kbase = static_cast<const TKV *>(a.k) + head_off;
+  const TKV *__restrict__ vbase = static_cast<const TKV *>(a.v) + head_off;
+
+  const int nq = int(count) * G;
+  for (int qg = 0; qg < nq; qg += NQT * 16) {
+    // ---- queries of this group: column li of tile qt is query qg + 16 qt + li ----------
+    int lim[NQT];
+    float qf[NQT][DK][8];
+    int kend = 0;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const int m = qg + 16 * qt + li;
+      int l = 0;
+      if (m < nq) {
+        const int t = m / G, g = m % G;
+        const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st;
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qf[qt][dk][e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e) * a.scale_log2;
+        int64_t lim64 = kl + t;
+        if (lim64 > a.span) lim64 = a.span;
+        l = (row_ok && lim64 > 0) ? int(lim64) : 0;
+      } else {
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qf[qt][dk][e] = 0.f;
+      }
+      lim[qt] = l;
+      kend = l > kend ? l : kend;
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int other = __shfl_xor(kend, o, 64);
+      kend = other > kend ? other : kend;
+    }
+
+    f32x4 acc[NQT][DH];
+    float mrun[NQT], lsum[NQT];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      mrun[qt] = NEG_BIG;
+      lsum[qt] = 0.f;
+#pragma unroll
+      for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // B operands of S^T (16-bit paths): the queries in the cache's type.
+    typename std::conditional<F32, float, typename Mfma16<typename std::conditional<F32, bf16, TKV>::type>::vec>::type
+        qv[NQT][DK];
+    if constexpr (!F32) {
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          f32x8 f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = qf[qt][dk][e];
+          qv[qt][dk] = Mfma16<TKV>::from(f);
+        }
+    }
+
+    // Global -> register staging of one tile: lane l holds 8 consecutive elements of key
+    // 16 j + l % 16 at dims 32 dk + 8 (l / 16), for both K and V.
+    constexpr int VEC = 8 * ES / 16;  // 16-byte vectors per 8 elements
+    uint4 kr[NJ][DK][VEC], vr[NJ][DK][VEC];
+    auto fetch = [&](int kb) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int key = kb + 16 * j + li;
+        const bool ok = key < kend;
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          const int64_t off = int64_t(key) * D + 32 * dk + 8 * lg;
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) {
+            kr[j][dk][c] = ok ? reinterpret_cast<const uint4 *>(kbase + off)[c] : uint4{0u, 0u, 0u, 0u};
+            vr[j][dk][c] = ok ? reinterpret_cast<const uint4 *>(vbase + off)[c] : uint4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+    };
+
+    if (kend > 0) fetch(0);
+    for (int kb = 0; kb < kend; kb += KT) {
+      // V tile into LDS (row = key within the tile), K kept in registers.
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) {
+            unsigned char *dst = vt + (16 * j + li) * ROW + (32 * dk + 8 * lg) * ES + 16 * c;
+            const uint4 v = vr[j][dk][c];
+            reinterpret_cast<uint2 *>(dst)[0] = uint2{v.x, v.y};
+            reinterpret_cast<uint2 *>(dst)[1] = uint2{v.z, v.w};
+          }
+      uint4 kcur[NJ][DK][VEC];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) kcur[j][dk][c] = kr[j][dk][c];
+      if (kb + KT < kend) fetch(kb + KT);  // next tile in flight during this one
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // ---- scores -------------------------------------------------------------------
+      f32x4 sc[NQT][NJ];
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int dk = 0; dk < DK; ++dk) {
+            if constexpr (F32) {
+              float kf[8];
+              __builtin_memcpy(kf, &kcur[j][dk][0], 32);
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                s4 = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[qt][dk][e], s4, 0, 0, 0);
+            } else {
+              typename Mfma16<TKV>::vec kvec;
+              __builtin_memcpy(&kvec, &kcur[j][dk][0], 16);
+              s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
+            }
+          }
+          sc[qt][j] = s4;
+        }
+
+      // ---- online softmax per query column --------------------------------------------
+      float p[NQT][NJ][4];
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        float tmax = NEG_BIG;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb + 16 * j + 4 * lg + i;
+            const float v = key < lim[qt] ? sc[qt][j][i] : -INFINITY;
+            sc[qt][j][i] = v;
+            tmax = fmaxf(tmax, v);
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(mrun[qt], tmax);
+        const float corr = fast_exp2(mrun[qt] - mnew);
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p[qt][j][i] = fast_exp2(sc[qt][j][i] - mnew);
+            psum += p[qt][j][i];
+          }
+        lsum[qt] = lsum[qt] * corr + psum;
+        mrun[qt] = mnew;
+#pragma unroll
+        for (int dh = 0; dh < DH; ++dh) acc[qt][dh] *= corr;
+      }
+
+      // ---- O^T += V^T . P^T --------------------------------------------------------------
+      if constexpr (F32) {
+#pragma unroll
+        for (int dh = 0; dh < DH; ++dh)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float v = *reinterpret_cast<const float *>(vt + (16 * j + 4 * lg + i) * ROW + (16 * dh + li) * 4);
+#pragma unroll
+              for (int qt = 0; qt < NQT; ++qt)
+                acc[qt][dh] = __builtin_amdgcn_mfma_f32_16x16x4f32(v, p[qt][j][i], acc[qt][dh], 0, 0, 0);
+            }
+      } else {
+        // k slot 8 (l / 16) + e of a 32-key chunk c is key 32 c + 16 (e / 4) + 4 (l / 16) + e % 4.
+#pragma unroll
+        for (int c = 0; c < KT / 32; ++c) {
+          typename Mfma16<TKV>::vec pv[NQT];
+#pragma unroll
+          for (int qt = 0; qt < NQT; ++qt) {
+            f32x8 f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = p[qt][2 * c + (e >> 2)][e & 3];
+            pv[qt] = Mfma16<TKV>::from(f);
+          }
+#pragma unroll
+          for (int dh = 0; dh < DH; ++dh) {
+            unsigned short raw[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int key = 32 * c + 16 * (e >> 2) + 4 * lg + (e & 3);
+              raw[e] = *reinterpret_cast<const unsigned short *>(vt + key * ROW + (16 * dh + li) * 2);
+            }
+            typename Mfma16<TKV>::vec vv;
+            __builtin_memcpy(&vv, raw, 16);
+#pragma unroll
+            for (int qt = 0; qt < NQT; ++qt) acc[qt][dh] = Mfma16<TKV>::mma(vv, pv[qt], acc[qt][dh]);
+          }
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      float total = lsum[qt];
+      total += __shfl_xor(total, 16, 64);
+      total += __shfl_xor(total, 32, 64);
+      const int m = qg + 16 * qt + li;
+      if (m >= nq) continue;
+      const int t = m / G, g = m % G;
+      const float inv = total > 0.f ? 1.0f / total : 0.f;
+      const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st;
+#pragma unroll
+      for (int dh = 0; dh < DH; ++dh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[qt][dh][i] * inv);
+    }
+  }
+}
+
+template <typename TKV, int D>
+void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
+  const unsigned grid = unsigned((int64_t(a.n_seqs) * a.kv_heads + 3) / 4);
+  if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
+  else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);
+  else decode_attention_mfma_kernel<TKV, D, 4><<<grid, 256, 0, s>>>(a);
+  CG_LAUNCHED();
+}
+
 template <typename TKV, int D>
 void launch_d(const AttnArgs &a, hipStream_t s) {
   constexpr int WAVES = 4;
@@ -283,6 +599,10 @@ void launch_d(const AttnArgs &a, hipStream_t s) {
 
 template <typename TKV>
 void launch_kv(const AttnArgs &a, hipStream_t s) {
+  // Queries per (sequence, KV head): G heads x tokens (packed chunks: up to 16 tokens).
+  const int queries = (a.n_heads / a.kv_heads) * (a.seq_start ? 16 : a.T);
+  if (a.head_dim == 32) return launch_mfma<TKV, 32>(a, queries, s);
+  if (a.head_dim == 64) return launch_mfma<TKV, 64>(a, queries, s);
   switch (a.head_dim) {
     case 8:
       return launch_d<TKV, 8>(a, s);
@@ -329,10 +649,11 @@ extern "C" int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb,
                                    int32_t out_dtype, void *stream) {
   return guarded([&] {
     check_layer(layer);
-    CG_REQUIRE(q && out && key_lengths, CG_ERR_INVALID, "q, out and key_lengths are required");
     dtype_size(q_dtype);
     dtype_size(out_dtype);
     CG_REQUIRE(B >= 0 && T >= 0, CG_ERR_INVALID, "B and T must be non-negative");
+    if (B == 0 || T == 0) return;  // empty tensors may carry NULL data pointers
+    CG_REQUIRE(q && out && key_lengths, CG_ERR_INVALID, "q, out and key_lengths are required");
     AttnArgs a{};
     a.q = q;
     a.q_dtype = q_dtype;
@@ -360,7 +681,6 @@ extern "C" int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb,
     a.capacity = layer->capacity;
     a.span = (span <= 0 || span > layer->max_len) ? layer->max_len : span;
     a.scale_log2 = scale * 1.4426950408889634f;
-    if (T == 0) return;
     launch_decode_attention(a, as_stream(stream));
   });
 }

@@ -6,34 +6,22 @@
 
 namespace cg {
 
-// How the A operand [M, K] is produced.
-enum AMode : int {
-  A_LN = 0,    // fp32 rows normalised on the fly by LayerNorm(ln_w, ln_b, eps)
-  A_F32 = 1,   // fp32 storage
-  A_BF16 = 2,  // bf16 storage
-};
-
 // What happens to the fp32 accumulator C[M, N] = A . W^T.
 enum EpiMode : int {
-  EPI_STORE = 0,      // out = C + bias                      (out_dtype)
-  EPI_GELU = 1,       // out = gelu(C + bias)                (out_dtype)
+  EPI_STORE = 0,      // out = C + bias                                  (out_dtype)
+  EPI_GELU = 1,       // out = gelu(C + bias)                            (out_dtype)
   EPI_RESID = 2,      // resid += C + bias + ple_scale * ple[m, ple_off + n % ple_dim]
   EPI_QKV = 3,        // q | k | v split; k, v (+ value embedding) appended to the KV pool
-  EPI_SCALE_ADD = 4,  // out = (C + addend) * scale           (out_dtype)
+  EPI_SCALE_ADD = 4,  // out = (C + addend) * scale                      (out_dtype)
+  EPI_RESID_LN = 5,   // EPI_RESID, then out = LayerNorm(resid row)      (out_dtype); N <= 256
 };
 
 struct GemmArgs {
   int32_t M, N, K;
-  int32_t compute;  // CG_F32 or CG_BF16: operand type of the MFMA
-  // A operand.
-  int32_t a_mode;
-  const void *A;
+  int32_t compute;  // CG_F32 or CG_BF16: storage type of A and W and operand type of the MFMA
+  const void *A;    // [M, K] row-major, type `compute`
   int64_t lda;
-  const float *ln_w, *ln_b;
-  float eps;
-  // W operand [N, K] row-major, storage CG_F32 or CG_BF16.
-  const void *W;
-  int32_t w_dtype;
+  const void *W;    // [N, K] row-major, type `compute`
   const float *bias;
   // Epilogue.
   int32_t epi;
@@ -49,6 +37,8 @@ struct GemmArgs {
   const float *addend;
   int64_t ld_add;
   float scale;
+  const float *ln_w, *ln_b;  // EPI_RESID_LN
+  float eps;
   // EPI_QKV: columns [0, q_cols) -> q (fp32, ld ldo); then kv_heads * head_dim columns of
   // K and as many of V, appended at (tok_row[m], head, tok_pos[m]).
   int32_t q_cols;
@@ -61,5 +51,13 @@ struct GemmArgs {
 };
 
 void launch_gemm(const GemmArgs &g, hipStream_t stream);
+
+// y[i] = LayerNorm(x[index ? index[i] : i]) (fp32 statistics), stored as y_dtype.
+void launch_layernorm_rows(const float *x, const int32_t *index, const float *w, const float *b,
+                           float eps, void *y, int32_t y_dtype, int32_t n, int32_t d,
+                           hipStream_t stream);
+
+// y = x (fp32) rounded to `dtype` (CG_BF16) or copied (CG_F32), n elements.
+void launch_convert(const float *x, void *y, int32_t dtype, int64_t n, hipStream_t stream);
 
 }  // namespace cg

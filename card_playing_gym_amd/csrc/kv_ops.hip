@@ -146,10 +146,12 @@ void write_common(const cg_kv_layer *layer, const int64_t *rows, const int64_t *
                   int32_t start, const cg_kv_source *k, const cg_kv_source *v, int32_t B, int32_t T,
                   void *stream) {
   check_layer(layer);
-  CG_REQUIRE(k && v && k->data && v->data, CG_ERR_INVALID, "k_new / v_new is NULL");
+  CG_REQUIRE(B >= 0 && T >= 0, CG_ERR_INVALID, "B and T must be non-negative");
+  CG_REQUIRE(k && v, CG_ERR_INVALID, "k_new / v_new is NULL");
+  if (int64_t(B) * T == 0) return;  // empty tensors may carry NULL data pointers
+  CG_REQUIRE(k->data && v->data, CG_ERR_INVALID, "k_new / v_new data is NULL");
   CG_REQUIRE(k->dtype == v->dtype, CG_ERR_INVALID, "k_new and v_new must share a dtype");
   dtype_size(k->dtype);
-  CG_REQUIRE(B >= 0 && T >= 0, CG_ERR_INVALID, "B and T must be non-negative");
   CG_REQUIRE(positions || start >= 0, CG_ERR_RANGE, "start must be non-negative");
   CG_REQUIRE(positions || int64_t(start) + T <= layer->max_len, CG_ERR_RANGE,
              "write_range past max_len");
@@ -202,8 +204,10 @@ int cg_kv_read(const cg_kv_layer *layer, const int64_t *rows, int32_t B, int32_t
                void *k_out, void *v_out, void *stream) {
   return guarded([&] {
     check_layer(layer);
-    CG_REQUIRE(k_out && v_out, CG_ERR_INVALID, "outputs are NULL");
     CG_REQUIRE(B >= 0 && length >= 0, CG_ERR_INVALID, "B and length must be non-negative");
+    CG_REQUIRE(length <= layer->max_len, CG_ERR_RANGE, "read length past max_len");
+    if (int64_t(B) * length == 0) return;
+    CG_REQUIRE(k_out && v_out, CG_ERR_INVALID, "outputs are NULL");
     CG_REQUIRE(length <= layer->max_len, CG_ERR_RANGE, "read length past max_len");
     CG_REQUIRE(rows || B <= layer->capacity, CG_ERR_RANGE, "dense read past capacity");
     const int bytes = layer->head_dim * dtype_size(layer->dtype);
@@ -231,8 +235,9 @@ int cg_kv_copy_rows(const cg_kv_layer *layer, const int64_t *sources, const int6
                     int32_t n, int32_t length, void *stream) {
   return guarded([&] {
     check_layer(layer);
-    CG_REQUIRE(sources && targets, CG_ERR_INVALID, "sources / targets are NULL");
     CG_REQUIRE(n >= 0 && length >= 0, CG_ERR_INVALID, "n and length must be non-negative");
+    if (int64_t(n) * length == 0) return;
+    CG_REQUIRE(sources && targets, CG_ERR_INVALID, "sources / targets are NULL");
     CG_REQUIRE(length <= layer->max_len, CG_ERR_RANGE, "copy length past max_len");
     const int bytes = layer->head_dim * dtype_size(layer->dtype);
     hipStream_t s = as_stream(stream);

@@ -35,6 +35,7 @@ inline size_t align_up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
 
 struct Workspace {
   float *x;
+  void *xn;  // LayerNorm of x, the A operand of the next projection (compute type)
   float *q;
   void *attn;
   void *h1;
@@ -55,6 +56,7 @@ Workspace carve(const cg_trunk &t, int32_t n_tokens, int32_t n_seqs, char *base)
     return p;
   };
   w.x = reinterpret_cast<float *>(take(size_t(n_tokens) * d * 4));
+  w.xn = take(size_t(n_tokens) * d * act);
   w.q = reinterpret_cast<float *>(take(size_t(n_tokens) * hd * 4));
   w.attn = take(size_t(n_tokens) * hd * act);
   w.h1 = take(size_t(n_tokens) * ff * act);
@@ -102,32 +104,6 @@ __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t
     if (r < start || r >= stop) r = -1;
     readout_tok[i] = int32_t(r);
   }
-}
-
-// One wave per row: y = LayerNorm(x[src]) with fp32 two-pass statistics.
-__global__ void layernorm_rows_kernel(const float *__restrict__ x, const int32_t *__restrict__ index,
-                                      const float *__restrict__ w, const float *__restrict__ b,
-                                      float eps, float *__restrict__ y, int32_t n, int32_t d) {
-  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= n) return;
-  const int src = index ? index[row] : row;
-  float *out = y + int64_t(row) * d;
-  if (src < 0) {
-    for (int k = lane; k < d; k += 64) out[k] = 0.f;
-    return;
-  }
-  const float *in = x + int64_t(src) * d;
-  float s = 0.f;
-  for (int k = lane; k < d; k += 64) s += in[k];
-  const float mean = wave_sum(s) / float(d);
-  float v = 0.f;
-  for (int k = lane; k < d; k += 64) {
-    const float t = in[k] - mean;
-    v = fmaf(t, t, v);
-  }
-  const float rstd = rsqrtf(wave_sum(v) / float(d) + eps);
-  for (int k = lane; k < d; k += 64) out[k] = fmaf((in[k] - mean) * rstd, w[k], b[k]);
 }
 
 // One wave per row: y = rms_norm(src row) * gain; src row = table[ids[row]] or x[row].
@@ -323,7 +299,6 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
     const int max_len = cache[0].max_len;
     const int span = (r.span <= 0 || r.span > max_len) ? max_len : r.span;
     const int act_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
-    const int w_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
 
     {
       const int n = N > r.n_seqs ? N : r.n_seqs;
@@ -333,30 +308,65 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
       CG_LAUNCHED();
     }
     CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
+    launch_layernorm_rows(w.x, nullptr, t.layers[0].ln_attn_w, t.layers[0].ln_attn_b, c.eps, w.xn,
+                          act_dtype, N, d, s);
 
     const float ple_scale = [&] {
       if (c.per_layer_dim == 0 || c.per_layer_dim == d) return 1.0f;
       const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
       return 1.0f / sqrtf(float(repeats));
     }();
+    // Whole-row residual tiles fuse the next LayerNorm into the residual epilogue.
+    const bool fused_ln = d <= 256;
+
+    auto residual = [&](const void *A, int K, const void *W, const float *bias, const float *ln_w,
+                        const float *ln_b, const float *ple_rows, int layer) {
+      GemmArgs g{};
+      g.M = N;
+      g.N = d;
+      g.K = K;
+      g.compute = t.compute;
+      g.A = A;
+      g.lda = K;
+      g.W = W;
+      g.bias = bias;
+      g.resid = w.x;
+      g.ldr = d;
+      if (ple_rows) {
+        g.ple = ple_rows;
+        g.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
+        g.ple_off = layer * c.per_layer_dim;
+        g.ple_dim = c.per_layer_dim;
+        g.ple_scale = ple_scale;
+      }
+      if (ln_w && fused_ln) {
+        g.epi = EPI_RESID_LN;
+        g.ln_w = ln_w;
+        g.ln_b = ln_b;
+        g.eps = c.eps;
+        g.out = w.xn;
+        g.out_dtype = act_dtype;
+        g.ldo = d;
+        launch_gemm(g, s);
+        return;
+      }
+      g.epi = EPI_RESID;
+      launch_gemm(g, s);
+      if (ln_w) launch_layernorm_rows(w.x, nullptr, ln_w, ln_b, c.eps, w.xn, act_dtype, N, d, s);
+    };
 
     for (int l = 0; l < c.n_layers; ++l) {
       const cg_layer_params &P = t.layers[l];
       const cg_kv_layer &L = cache[l];
-      {  // LN1 + QKV + append
+      {  // QKV projection of LN1(x) + append
         GemmArgs g{};
         g.M = N;
         g.N = (H + 2 * KVH) * D;
         g.K = d;
         g.compute = t.compute;
-        g.a_mode = A_LN;
-        g.A = w.x;
+        g.A = w.xn;
         g.lda = d;
-        g.ln_w = P.ln_attn_w;
-        g.ln_b = P.ln_attn_b;
-        g.eps = c.eps;
         g.W = t.qkv_w[l];
-        g.w_dtype = w_dtype;
         g.epi = EPI_QKV;
         g.out = w.q;
         g.ldo = H * D;
@@ -405,36 +415,17 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
         a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
         launch_decode_attention(a, s);
       }
-      {  // out_proj + residual
-        GemmArgs g{};
-        g.M = N;
-        g.N = d;
-        g.K = H * D;
-        g.compute = t.compute;
-        g.a_mode = act_dtype == CG_BF16 ? A_BF16 : A_F32;
-        g.A = w.attn;
-        g.lda = H * D;
-        g.W = t.out_w[l];
-        g.w_dtype = w_dtype;
-        g.epi = EPI_RESID;
-        g.resid = w.x;
-        g.ldr = d;
-        launch_gemm(g, s);
-      }
-      {  // LN2 + up + GELU
+      // out_proj + residual, then LN2 -> xn
+      residual(w.attn, H * D, t.out_w[l], nullptr, P.ln_mlp_w, P.ln_mlp_b, nullptr, l);
+      {  // mlp[0] + GELU
         GemmArgs g{};
         g.M = N;
         g.N = c.d_ff;
         g.K = d;
         g.compute = t.compute;
-        g.a_mode = A_LN;
-        g.A = w.x;
+        g.A = w.xn;
         g.lda = d;
-        g.ln_w = P.ln_mlp_w;
-        g.ln_b = P.ln_mlp_b;
-        g.eps = c.eps;
         g.W = t.up_w[l];
-        g.w_dtype = w_dtype;
         g.bias = P.mlp_up_b;
         g.epi = EPI_GELU;
         g.out = w.h1;
@@ -442,35 +433,14 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
         g.ldo = c.d_ff;
         launch_gemm(g, s);
       }
-      {  // down + residual (+ PLE)
-        GemmArgs g{};
-        g.M = N;
-        g.N = d;
-        g.K = c.d_ff;
-        g.compute = t.compute;
-        g.a_mode = act_dtype == CG_BF16 ? A_BF16 : A_F32;
-        g.A = w.h1;
-        g.lda = c.d_ff;
-        g.W = t.down_w[l];
-        g.w_dtype = w_dtype;
-        g.bias = P.mlp_down_b;
-        g.epi = EPI_RESID;
-        g.resid = w.x;
-        g.ldr = d;
-        if (ple && c.per_layer_dim > 0) {
-          g.ple = ple;
-          g.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
-          g.ple_off = l * c.per_layer_dim;
-          g.ple_dim = c.per_layer_dim;
-          g.ple_scale = ple_scale;
-        }
-        launch_gemm(g, s);
-      }
+      // mlp[2] + residual (+ PLE), then the next block's LN1 -> xn
+      const bool last = l + 1 == c.n_layers;
+      residual(w.h1, c.d_ff, t.down_w[l], P.mlp_down_b, last ? nullptr : t.layers[l + 1].ln_attn_w,
+               last ? nullptr : t.layers[l + 1].ln_attn_b, (ple && c.per_layer_dim > 0) ? ple : nullptr, l);
     }
     const int rows_out = r.readout ? r.n_seqs : N;
-    layernorm_rows_kernel<<<rows_grid(rows_out, 4), 256, 0, s>>>(
-        w.x, r.readout ? w.readout_tok : nullptr, t.final_w, t.final_b, c.eps, hidden, rows_out, d);
-    CG_LAUNCHED();
+    launch_layernorm_rows(w.x, r.readout ? w.readout_tok : nullptr, t.final_w, t.final_b, c.eps, hidden,
+                          CG_F32, rows_out, d, s);
   });
 }
 
