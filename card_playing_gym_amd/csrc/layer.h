@@ -1,0 +1,63 @@
+// Internal interface of the fused per-layer kernel of the bf16 trunk step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cg {
+
+// One launch does, for a block of token rows:
+//   post  (do_post): x += attn . W_out^T; h = LN(x; ln2); x += GELU(h . W_up^T + b_up) . W_down^T
+//                    + b_down (+ per-layer embedding);   (DecoderBlock._finish + Trunk._add_ple)
+//   else           : x = x_src (the conditioned input; the first block's prologue)
+//   then either  (final_ln == 0): h = LN(x; ln) ; [q | k | v] = h . W_qkv^T, q stored, k / v
+//                    (+ value embedding) appended to the pool at each token's slot
+//                    (the next block's _qkv + KVCache.write_step)
+//   or           (final_ln == 1): hidden[tok_out[m]] = LN(x; ln) for readout tokens.
+struct TailArgs {
+  int32_t M;  // tokens
+  int32_t d, d_ff, n_qkv, q_cols, kv_heads, head_dim, max_len, kv_dtype;
+  float eps;
+
+  int32_t do_post;
+  const void *attn;  // [M, d] bf16 (attention output, heads x head_dim per token)
+  // Weights in fragment order (launch_pack_fragments).
+  const void *w_out;  // [d, d]
+  const void *w_up;   // [d_ff, d]
+  const float *b_up;  // [d_ff]
+  const void *w_down;  // [d, d_ff]
+  const float *b_down;  // [d]
+  const float *ln2_w, *ln2_b;
+  const float *ple;  // [M, ld_ple] or NULL
+  int64_t ld_ple;
+  int32_t ple_off, ple_dim;
+  float ple_scale;
+
+  const float *x_src;  // residual stream read
+  float *x;            // residual stream written (may alias x_src)
+
+  int32_t final_ln;
+  const float *ln_w, *ln_b;  // next block's ln_attn, or the final norm
+  const void *w_qkv;         // [n_qkv, d]
+  float *q;                  // [M, q_cols]
+  void *kc, *vc;
+  const int32_t *tok_row, *tok_pos;
+  const float *vemb;
+  int64_t ld_vemb;
+  int32_t vemb_off;  // < 0: none
+  float *hidden;     // final_ln: [rows, d]
+  const int32_t *tok_out;
+};
+
+// The fused kernel reads its four weight matrices in MFMA fragment order: W [N, K] (fp32,
+// row-major) -> bf16 blocks of 16 rows x 32 k, k zero-padded to a multiple of 32.
+size_t packed_fragment_bytes(int N, int K);
+void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_t stream);
+
+// Shapes the fused kernel is built for: d_model <= 256 and a multiple of 16, d_ff a
+// multiple of 16, n_qkv a multiple of 16, bf16 projections.
+bool tail_supported(int d, int d_ff, int n_qkv);
+
+void launch_tail(const TailArgs &a, hipStream_t stream);
+
+}  // namespace cg

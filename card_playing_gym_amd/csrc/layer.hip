@@ -1,0 +1,568 @@
+// Fused per-layer kernel of the bf16 trunk step (gfx950).
+//
+// After a layer's attention, everything up to the next layer's attention runs in one
+// launch per block of BM token rows (DecoderBlock._finish + Trunk._add_ple +
+// DecoderBlock._qkv + KVCache.write_step of the next block, cardgym/nn/trunk.py:141-157,
+// 318-333, cardgym/nn/kv_cache.py:84-105; for the last block the final LayerNorm at the
+// readout tokens, trunk.py:429):
+//
+//   x1 = x + attn . W_out^T                     (stage "out")
+//   h  = LN(x1; ln_mlp)                        -> LDS panel (bf16)
+//   for each 256-wide chunk c of d_ff:         (stages "up c", "down c")
+//     g_c = GELU(h . W_up[c]^T + b_up[c])      -> LDS (bf16, double-buffered)
+//     acc += g_c . W_down[:, c]^T
+//   x2 = x1 + acc + b_down (+ per-layer embedding)
+//   h' = LN(x2; next ln_attn)                  -> LDS panel
+//   [q | k | v] = h' . W_qkv^T                 (stages "qkv c"): q stored, k / v (+ value
+//                                               embedding) written to the pool
+//
+// Work split: the block's eight waves split every stage's output columns (32 each); the
+// A operand (BM rows x 256 k, bf16) is read from LDS by all eight waves, the B operand
+// (weights) streams from L2 straight into each wave's registers: lane l loads 16 bytes of
+// W row (col 16 j + l % 16) at k = 32 ks + 8 (l / 16), exactly the
+// v_mfma_f32_16x16x32_bf16 B-fragment, so weights never touch LDS.  Each fragment
+// register is refilled with stage s+1's fragment right after its MFMAs of stage s, which
+// keeps a whole stage of weights (128 KB per block) in flight.  Row statistics of the
+// LayerNorms reduce over the 16 lanes of a fragment row with shuffles, then over the
+// eight waves in LDS.
+#include "common.h"
+#include "layer.h"
+
+namespace cg {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+
+constexpr int PANEL = 256;            // widest K of a stage (d_model, and the chunk width)
+constexpr int ROWB = PANEL * 2 + 16;  // LDS bytes per panel row: bf16 + 16 B pad
+constexpr int WAVES = 8;              // waves per block; each owns 32 columns of a stage
+constexpr int FN = 2;                 // 16-column fragments per wave and stage
+constexpr int THREADS = 64 * WAVES;
+constexpr int KS = PANEL / 32;        // 32-wide k-steps per stage
+
+enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
+
+// Global reads go through buffer descriptors (base and size in scalar registers, 32-bit
+// per-lane byte offsets): an offset past the end returns 0 instead of faulting, so no
+// load needs a branch, and a fragment loads straight into the registers it is used from.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
+__device__ __forceinline__ Rsrc rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ float bloadf(Rsrc r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ int bloadi(Rsrc r, uint32_t off) {
+  return int(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+template <typename T>
+__device__ __forceinline__ void gst(T *p, T v) {
+  *p = v;
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for
+// its global loads (the next stage's weights stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+// Returns v unchanged but opaque to the optimiser.  Row and lane indices are passed
+// through it at the top of every stage so per-lane offsets are formed where they are used
+// instead of being hoisted out of the stage loop (where they exhaust registers).
+__device__ __forceinline__ int opaque(int v) {
+  __asm__ volatile("" : "+s"(v));
+  return v;
+}
+__device__ __forceinline__ int opaque_lane(int v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ f32x4 mma(const uint4 &a, const uint4 &b, f32x4 c) {
+  bf16x8 av, bv;
+  __builtin_memcpy(&av, &a, 16);
+  __builtin_memcpy(&bv, &b, 16);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, c, 0, 0, 0);
+}
+
+// Weights are stored in MFMA fragment order (pack_fragments below): matrix W [N, K] as
+// blocks of 16 rows x 32 k, block (nb, kb) at ((nb * kblocks + kb) * 64 + lane) * 16 bytes,
+// lane (li, lg) holding W[16 nb + li][32 kb + 8 lg .. +7] -- exactly the B fragment of
+// v_mfma_f32_16x16x32_bf16, so every fragment load is one contiguous 1 KB wave access.
+// A stage's slice for one wave: row blocks nb0 + j (j < FN), k blocks kb0 + ks (ks < KS).
+// Row blocks past the matrix read as 0 (their output columns are discarded by the
+// epilogue); k blocks past the stage's width meet zero A-panel columns.
+struct Slice {
+  Rsrc w;
+  uint32_t kblocks;
+  int nb0, kb0;
+};
+
+struct Plan {
+  int nc, nq, n_post, S;
+};
+
+__device__ __forceinline__ int stage_kind(const Plan &p, int s, int &chunk) {
+  if (s < p.n_post) {
+    if (s == 0) {
+      chunk = 0;
+      return ST_OUT;
+    }
+    chunk = (s - 1) >> 1;
+    return ((s - 1) & 1) ? ST_DOWN : ST_UP;
+  }
+  chunk = s - p.n_post;
+  return ST_QKV;
+}
+
+__device__ __forceinline__ uint32_t kblocks_of(int k) { return uint32_t(k + 31) / 32; }
+
+__device__ __forceinline__ Slice stage_slice(const TailArgs &a, const Plan &p, int s, int cw) {
+  int c;
+  const int kind = stage_kind(p, s, c);
+  const int d = a.d;
+  const uint32_t kd = kblocks_of(d), kf = kblocks_of(a.d_ff);
+  if (kind == ST_OUT) return Slice{rsrc(a.w_out, uint32_t(d) * kd * 64), kd, cw / 16, 0};
+  if (kind == ST_UP) return Slice{rsrc(a.w_up, uint32_t(a.d_ff) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
+  if (kind == ST_DOWN) return Slice{rsrc(a.w_down, uint32_t(d) * kf * 64), kf, cw / 16, (PANEL / 32) * c};
+  return Slice{rsrc(a.w_qkv, uint32_t(a.n_qkv) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
+}
+
+__device__ __forceinline__ uint32_t slice_base(const Slice &s, int j, int lane) {
+  return ((uint32_t(s.nb0 + j) * s.kblocks + uint32_t(s.kb0)) * 64 + uint32_t(lane)) * 16;
+}
+
+__device__ __forceinline__ void load_slice(uint4 (&buf)[KS][FN], const Slice &s, int lane) {
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const uint32_t base = slice_base(s, j, lane);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) buf[ks][j] = bload16(s.w, base + 1024 * ks);
+  }
+}
+
+// acc[i][j] += panel rows (16 i + l % 16) x W fragment j over all 256 k (panel columns
+// past a stage's width are zero, and output columns past the matrix are discarded by the
+// epilogue, so no step needs a guard).  Each fragment register is refilled with the next
+// stage's fragment as soon as its MFMAs are issued, so the next stage's weights stream in
+// during this stage; the code is branch-free so the loads land in the registers the
+// MFMAs read.
+template <int FM>
+__device__ __forceinline__ void stage_mma(f32x4 (&acc)[FM][FN], const unsigned char *lds,
+                                          uint4 (&w)[KS][FN], const Slice &next, int lane) {
+  const int li = lane & 15, lg = lane >> 4;
+  // All of the stage's A fragments first: one LDS round trip instead of one per k-step.
+  uint4 af[KS][FM];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[ks][i] = *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
+  uint32_t base[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) base[j] = slice_base(next, j, lane);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[ks][i], w[ks][j], acc[i][j]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+  }
+}
+
+template <int FM>
+__device__ __forceinline__ void zero(f32x4 (&acc)[FM][FN]) {
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Sum over the 16 lanes of a DPP row (the 16 columns of one MFMA fragment row): quad
+// butterflies, then rotations by 4 and 8 within the row; every lane ends with the sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum16(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp<0x124>(v);  // row_ror:4
+  v += dpp<0x128>(v);  // row_ror:8
+  return v;
+}
+
+// LayerNorm statistics of rows held in the MFMA layout: v[i][j][r] is row 16 i + 4 lg + r,
+// column cw + 16 j + li (columns >= d hold 0 and are excluded).  Two passes (mean, then
+// centred squares), each reduced over the fragment's 16 lanes and the block's waves.
+template <int BM>
+__device__ __forceinline__ void row_stats(const f32x4 (&v)[BM / 16][FN], int cw, int d, float eps,
+                                          float (&mean)[BM / 16][4], float (&rstd)[BM / 16][4],
+                                          float *red, int wave, int li, int lg) {
+  constexpr int FM = BM / 16;
+  const float inv_d = 1.0f / float(d);
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if (cw + 16 * j + li < d) {
+            const float x = v[i][j][r];
+            s += pass == 0 ? x : (x - mean[i][r]) * (x - mean[i][r]);
+          }
+        }
+        s = sum16(s);
+        if (li == 0) red[(pass * WAVES + wave) * BM + 16 * i + 4 * lg + r] = s;
+      }
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * i + 4 * lg + r;
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) s += red[(pass * WAVES + w) * BM + row];
+        if (pass == 0) mean[i][r] = s * inv_d;
+        else rstd[i][r] = rsqrtf(s * inv_d + eps);
+      }
+  }
+}
+
+// LN(v) -> the panel (bf16, the next QKV stage's A operand), or, for the last block, the
+// final norm -> hidden rows of readout tokens.
+template <int BM>
+__device__ __forceinline__ void next_prologue(const TailArgs &a, const f32x4 (&v)[BM / 16][FN],
+                                              unsigned char *panel, float *red, int m0, int cw,
+                                              int wave, int li, int lg) {
+  constexpr int FM = BM / 16;
+  float mean[FM][4], rstd[FM][4];
+  const Rsrc rw = rsrc(a.ln_w, uint32_t(a.d) * 4), rb = rsrc(a.ln_b, uint32_t(a.d) * 4);
+  float lw[FN], lb[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const uint32_t n = uint32_t(cw + 16 * j + li);
+    lw[j] = bloadf(rw, 4 * n);
+    lb[j] = bloadf(rb, 4 * n);
+  }
+  int out_row[FM][4];
+  if (a.final_ln) {
+    const Rsrc ro = rsrc(a.tok_out, uint32_t(a.M) * 4);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * i + 4 * lg + r;
+        out_row[i][r] = m < a.M ? bloadi(ro, 4 * uint32_t(m)) : -1;
+      }
+  }
+  row_stats<BM>(v, cw, a.d, a.eps, mean, rstd, red, wave, li, lg);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int n = cw + 16 * j + li;
+    if (n >= a.d) continue;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * i + 4 * lg + r;
+        const float y = fmaf((v[i][j][r] - mean[i][r]) * rstd[i][r], lw[j], lb[j]);
+        if (a.final_ln) {
+          if (out_row[i][r] >= 0) gst(a.hidden + int64_t(out_row[i][r]) * a.d + n, y);
+        } else {
+          *reinterpret_cast<bf16 *>(panel + row * ROWB + n * 2) = from_f32<bf16>(y);
+        }
+      }
+  }
+  if (!a.final_ln) lds_barrier();
+}
+
+__device__ __forceinline__ void store_kv(void *base, int dtype, int64_t index, float v) {
+  if (dtype == CG_BF16) gst(static_cast<bf16 *>(base) + index, from_f32<bf16>(v));
+  else if (dtype == CG_F16) gst(static_cast<f16 *>(base) + index, from_f32<f16>(v));
+  else gst(static_cast<float *>(base) + index, v);
+}
+
+template <int BM>
+__global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
+  constexpr int FM = BM / 16;
+  __shared__ __align__(16) unsigned char panel[BM * ROWB];
+  __shared__ __align__(16) unsigned char hbuf[2][BM * ROWB];
+  __shared__ float red[2 * WAVES * BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cw = 16 * FN * wave;
+  const int d = a.d;
+  Plan p;
+  p.nc = (a.d_ff + PANEL - 1) / PANEL;
+  p.nq = a.final_ln ? 0 : (a.n_qkv + PANEL - 1) / PANEL;
+  p.n_post = a.do_post ? 1 + 2 * p.nc : 0;
+  p.S = p.n_post + p.nq;
+  const uint32_t xbytes = uint32_t(a.M) * uint32_t(d) * 4;
+
+  uint4 cur[KS][FN];
+  if (p.S > 0) load_slice(cur, stage_slice(a, p, 0, cw), lane);
+
+  // Zero the LDS panels once: padding columns (k >= d, or past d_ff) stay zero.
+  for (int o = tid * 16; o < BM * ROWB; o += THREADS * 16) {
+    const uint4 z = {0u, 0u, 0u, 0u};
+    *reinterpret_cast<uint4 *>(panel + o) = z;
+    *reinterpret_cast<uint4 *>(hbuf[0] + o) = z;
+    *reinterpret_cast<uint4 *>(hbuf[1] + o) = z;
+  }
+  lds_barrier();
+
+  f32x4 acc[FM][FN], accd[FM][FN];
+  zero<FM>(accd);
+  {
+    const int m0 = blockIdx.x * BM;
+    const int li = lane & 15, lg = lane >> 4;
+    if (a.do_post) {
+      // Attention rows of this block -> panel (16-byte chunks; rows past M read as 0).
+      const int cpr = d / 8;
+      const Rsrc ra = rsrc(a.attn, uint32_t(a.M) * uint32_t(d) * 2);
+      for (int idx = tid; idx < BM * cpr; idx += THREADS) {
+        const int r = idx / cpr, c = idx % cpr;
+        *reinterpret_cast<uint4 *>(panel + r * ROWB + 16 * c) = bload16(ra, (uint32_t(m0 + r) * d + 8 * c) * 2);
+      }
+      lds_barrier();
+    } else {
+      // First block's prologue: the conditioned input is the residual stream.
+      const Rsrc rs = rsrc(a.x_src, xbytes);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * i + 4 * lg + r, n = cw + 16 * j + li;
+            const float v = bloadf(rs, (uint32_t(m) * d + n) * 4);
+            const bool ok = m < a.M && n < d;
+            if (ok && a.x != a.x_src) gst(a.x + int64_t(m) * d + n, v);
+            acc[i][j][r] = ok ? v : 0.f;
+          }
+      next_prologue<BM>(a, acc, panel, red, m0, cw, wave, li, lg);
+    }
+  }
+
+  for (int s = 0; s < p.S; ++s) {
+    const int m0 = opaque(blockIdx.x * BM);
+    const int lane_o = opaque_lane(lane);
+    const int li = lane_o & 15, lg = lane_o >> 4;
+    int c;
+    const int kind = stage_kind(p, s, c);
+    // The last stage re-reads its own (in-range) slice: the refill stays unconditional.
+    const Slice nx = stage_slice(a, p, s + 1 < p.S ? s + 1 : s, cw);
+    if (kind == ST_OUT) {
+      // ---- out-proj + residual, then LN(ln_mlp) -> panel
+      const Rsrc rs = rsrc(a.x_src, xbytes);
+      const Rsrc rw = rsrc(a.ln2_w, uint32_t(d) * 4), rb = rsrc(a.ln2_b, uint32_t(d) * 4);
+      float xr[FM][FN][4], lw[FN], lb[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = cw + 16 * j + li;
+        lw[j] = bloadf(rw, 4 * uint32_t(n));
+        lb[j] = bloadf(rb, 4 * uint32_t(n));
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xr[i][j][r] = bloadf(rs, (uint32_t(m0 + 16 * i + 4 * lg + r) * d + n) * 4);
+      }
+      zero<FM>(acc);
+      stage_mma<FM>(acc, panel, cur, nx, lane_o);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * i + 4 * lg + r, n = cw + 16 * j + li;
+            float v = 0.f;
+            if (m < a.M && n < d) {
+              v = acc[i][j][r] + xr[i][j][r];
+              gst(a.x + int64_t(m) * d + n, v);
+            }
+            acc[i][j][r] = v;
+          }
+      float mean[FM][4], rstd[FM][4];
+      row_stats<BM>(acc, cw, d, a.eps, mean, rstd, red, wave, li, lg);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = cw + 16 * j + li;
+        if (n >= d) continue;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * i + 4 * lg + r;
+            const float y = fmaf((acc[i][j][r] - mean[i][r]) * rstd[i][r], lw[j], lb[j]);
+            *reinterpret_cast<bf16 *>(panel + row * ROWB + n * 2) = from_f32<bf16>(y);
+          }
+      }
+      lds_barrier();
+    } else if (kind == ST_UP) {
+      // ---- up chunk c + GELU -> hbuf[c & 1]
+      const Rsrc rb = rsrc(a.b_up, uint32_t(a.d_ff) * 4);
+      float bias[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bias[j] = bloadf(rb, 4 * uint32_t(PANEL * c + cw + 16 * j + li));
+      zero<FM>(acc);
+      stage_mma<FM>(acc, panel, cur, nx, lane_o);
+      unsigned char *hb = hbuf[c & 1];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int col = cw + 16 * j + li;
+        const bool ok = PANEL * c + col < a.d_ff;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * i + 4 * lg + r;
+            const float g = ok ? gelu_erf(acc[i][j][r] + bias[j]) : 0.f;
+            *reinterpret_cast<bf16 *>(hb + row * ROWB + col * 2) = from_f32<bf16>(g);
+          }
+      }
+      lds_barrier();
+    } else if (kind == ST_DOWN) {
+      // ---- down chunk c (accumulates); after the last: residual (+PLE), next prologue
+      const bool last = c == p.nc - 1;
+      float xr[FM][FN][4], bias[FN];
+      if (last) {
+        const Rsrc rx = rsrc(a.x, xbytes), rb = rsrc(a.b_down, uint32_t(d) * 4);
+        const Rsrc rp = rsrc(a.ple, a.ple ? uint32_t(a.M) * uint32_t(a.ld_ple) * 4 : 0u);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int n = cw + 16 * j + li;
+          bias[j] = bloadf(rb, 4 * uint32_t(n));
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const uint32_t m = uint32_t(m0 + 16 * i + 4 * lg + r);
+              float v = bloadf(rx, (m * d + n) * 4);
+              if (a.ple)
+                v = fmaf(bloadf(rp, (m * uint32_t(a.ld_ple) + a.ple_off + n % a.ple_dim) * 4), a.ple_scale, v);
+              xr[i][j][r] = v;
+            }
+        }
+      }
+      stage_mma<FM>(accd, hbuf[c & 1], cur, nx, lane_o);
+      if (last) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int n = cw + 16 * j + li;
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int m = m0 + 16 * i + 4 * lg + r;
+              float v = 0.f;
+              if (m < a.M && n < d) {
+                v = xr[i][j][r] + accd[i][j][r] + bias[j];
+                gst(a.x + int64_t(m) * d + n, v);
+              }
+              accd[i][j][r] = v;
+            }
+        }
+        next_prologue<BM>(a, accd, panel, red, m0, cw, wave, li, lg);
+      }
+    } else {
+      // ---- qkv chunk: q stored, k / v appended to the pool
+      const Rsrc rr = rsrc(a.tok_row, uint32_t(a.M) * 4), rp = rsrc(a.tok_pos, uint32_t(a.M) * 4);
+      int trow[FM][4], tpos[FM][4];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t m = uint32_t(m0 + 16 * i + 4 * lg + r);
+          trow[i][r] = bloadi(rr, 4 * m);
+          tpos[i][r] = bloadi(rp, 4 * m);
+        }
+      zero<FM>(acc);
+      stage_mma<FM>(acc, panel, cur, nx, lane_o);
+      const int kvw = a.kv_heads * a.head_dim;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * i + 4 * lg + r;
+          if (m >= a.M) continue;
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int n = PANEL * c + cw + 16 * j + li;
+            if (n >= a.n_qkv) continue;
+            const float v = acc[i][j][r];
+            if (n < a.q_cols) {
+              gst(a.q + int64_t(m) * a.q_cols + n, v);
+            } else if (trow[i][r] >= 0) {
+              const bool is_v = n >= a.q_cols + kvw;
+              const int kvc = n - a.q_cols - (is_v ? kvw : 0);
+              const int h = kvc / a.head_dim, dd = kvc % a.head_dim;
+              float val = v;
+              if (is_v && a.vemb_off >= 0) val += a.vemb[int64_t(m) * a.ld_vemb + a.vemb_off + kvc];
+              const int64_t dst = ((int64_t(trow[i][r]) * a.kv_heads + h) * a.max_len + tpos[i][r]) * a.head_dim + dd;
+              store_kv(is_v ? a.vc : a.kc, a.kv_dtype, dst, val);
+            }
+          }
+        }
+    }
+  }
+}
+
+// W [N, K] fp32 row-major -> bf16 fragment order (see Slice), k padded to 32 with zeros.
+__global__ void pack_fragments_kernel(const float *__restrict__ src, bf16 *__restrict__ dst, int32_t N,
+                                      int32_t K, int32_t kblocks) {
+  const int64_t total = int64_t(N) * kblocks * 32;
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += int64_t(gridDim.x) * blockDim.x) {
+    const int t = int(e & 7);
+    const int lane = int((e >> 3) & 63);
+    const int64_t blk = e >> 9;
+    const int kb = int(blk % kblocks), nb = int(blk / kblocks);
+    const int row = 16 * nb + (lane & 15), k = 32 * kb + 8 * (lane >> 4) + t;
+    dst[e] = k < K ? from_f32<bf16>(src[int64_t(row) * K + k]) : bf16{0};
+  }
+}
+
+}  // namespace
+
+size_t packed_fragment_bytes(int N, int K) { return size_t(N) * ((K + 31) / 32) * 32 * 2; }
+
+void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_t s) {
+  CG_REQUIRE(N % 16 == 0, CG_ERR_UNSUPPORTED, "fragment packing needs a multiple of 16 rows");
+  const int kblocks = (K + 31) / 32;
+  const int64_t total = int64_t(N) * kblocks * 32;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  pack_fragments_kernel<<<unsigned(blocks), 256, 0, s>>>(src, static_cast<bf16 *>(dst), N, K, kblocks);
+  CG_LAUNCHED();
+}
+
+bool tail_supported(int d, int d_ff, int n_qkv) {
+  return d > 0 && d <= PANEL && d % 16 == 0 && d_ff > 0 && d_ff % 16 == 0 && n_qkv > 0 && n_qkv % 16 == 0;
+}
+
+void launch_tail(const TailArgs &a, hipStream_t s) {
+  CG_REQUIRE(tail_supported(a.d, a.d_ff, a.n_qkv), CG_ERR_UNSUPPORTED, "fused layer: unsupported shape");
+  if (a.M <= 0) return;
+  // 16-row blocks: one per CU at the benchmark's 4096 tokens.
+  layer_tail_kernel<16><<<unsigned((a.M + 15) / 16), THREADS, 0, s>>>(a);
+  CG_LAUNCHED();
+}
+
+}  // namespace cg

@@ -13,6 +13,7 @@
 #include "attention.h"
 #include "common.h"
 #include "gemm.h"
+#include "layer.h"
 
 struct cg_trunk {
   cg_trunk_config cfg;
@@ -21,6 +22,9 @@ struct cg_trunk {
   std::vector<cg_layer_params> layers;
   const float *final_w;
   const float *final_b;
+  // bf16 projections whose shape the fused layer kernel covers: weight copies are kept in
+  // its fragment order instead of row-major.
+  bool fused = false;
   // bf16 copies of the projection weights (compute == CG_BF16), one allocation.
   void *wbuf = nullptr;
   size_t wbuf_bytes = 0;
@@ -42,6 +46,7 @@ struct Workspace {
   int32_t *tok_row;
   int32_t *tok_pos;
   int32_t *readout_tok;
+  int32_t *tok_out;
   size_t bytes;
 };
 
@@ -63,17 +68,22 @@ Workspace carve(const cg_trunk &t, int32_t n_tokens, int32_t n_seqs, char *base)
   w.tok_row = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
   w.tok_pos = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
   w.readout_tok = reinterpret_cast<int32_t *>(take(size_t(n_seqs > 0 ? n_seqs : 1) * 4));
+  w.tok_out = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
   w.bytes = off;
   return w;
 }
 
-// Per-token cache slot (row, clamped write position) and per-sequence readout token.
+// Per-token cache slot (row, clamped write position), per-sequence readout token, and
+// per-token output row (tok_out: the sequence whose readout the token is, or -1; every
+// token is its own output row when readout is NULL).  Sequences whose readout offset is
+// outside their chunk get a zero hidden row.
 // Padded mode (seq_start NULL): token i belongs to sequence i / T.
 __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t *__restrict__ positions,
                             const int64_t *__restrict__ rows, const int64_t *__restrict__ readout,
                             int32_t n_seqs, int32_t n_tokens, int32_t T, int32_t max_len,
                             int32_t capacity, int32_t *__restrict__ tok_row,
-                            int32_t *__restrict__ tok_pos, int32_t *__restrict__ readout_tok) {
+                            int32_t *__restrict__ tok_pos, int32_t *__restrict__ readout_tok,
+                            int32_t *__restrict__ tok_out, float *__restrict__ hidden, int32_t d) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n_tokens) {
     int b, t;
@@ -96,12 +106,17 @@ __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t
     const bool ok = row >= 0 && row < capacity && pos >= 0;
     tok_row[i] = ok ? int32_t(row) : -1;
     tok_pos[i] = ok ? int32_t(pos) : 0;
+    tok_out[i] = readout ? (readout[b] == t ? b : -1) : i;
   }
   if (readout && i < n_seqs) {
     const int64_t start = seq_start ? seq_start[i] : int64_t(i) * T;
     const int64_t stop = seq_start ? seq_start[i + 1] : start + T;
     int64_t r = start + readout[i];
-    if (r < start || r >= stop) r = -1;
+    if (r < start || r >= stop) {
+      r = -1;
+      if (hidden)
+        for (int k = 0; k < d; ++k) hidden[int64_t(i) * d + k] = 0.f;
+    }
     readout_tok[i] = int32_t(r);
   }
 }
@@ -150,22 +165,39 @@ void convert_weights(cg_trunk &t, hipStream_t s) {
   const int qkv_rows = (t.cfg.n_heads + 2 * t.cfg.n_kv_heads) * t.head_dim;
   char *p = static_cast<char *>(t.wbuf);
   size_t off = 0;
-  auto conv = [&](const float *src, int64_t n) {
-    bf16 *dst = reinterpret_cast<bf16 *>(p + off);
-    off += align_up(size_t(n) * 2);
-    int64_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    to_bf16_kernel<<<unsigned(blocks), 256, 0, s>>>(src, dst, n);
-    CG_LAUNCHED();
+  // W [rows, cols] fp32 -> bf16, row-major or in the fused kernel's fragment order.
+  auto conv = [&](const float *src, int rows, int cols) {
+    void *dst = p + off;
+    if (t.fused) {
+      off += align_up(packed_fragment_bytes(rows, cols));
+      launch_pack_fragments(src, dst, rows, cols, s);
+    } else {
+      const int64_t n = int64_t(rows) * cols;
+      off += align_up(size_t(n) * 2);
+      int64_t blocks = (n + 255) / 256;
+      if (blocks > 4096) blocks = 4096;
+      to_bf16_kernel<<<unsigned(blocks), 256, 0, s>>>(src, static_cast<bf16 *>(dst), n);
+      CG_LAUNCHED();
+    }
     return static_cast<const void *>(dst);
   };
   for (int l = 0; l < t.cfg.n_layers; ++l) {
     const cg_layer_params &L = t.layers[l];
-    t.qkv_w[l] = conv(L.qkv_w, int64_t(qkv_rows) * d);
-    t.out_w[l] = conv(L.out_w, int64_t(d) * hd);
-    t.up_w[l] = conv(L.mlp_up_w, int64_t(ff) * d);
-    t.down_w[l] = conv(L.mlp_down_w, int64_t(d) * ff);
+    t.qkv_w[l] = conv(L.qkv_w, qkv_rows, d);
+    t.out_w[l] = conv(L.out_w, d, hd);
+    t.up_w[l] = conv(L.mlp_up_w, ff, d);
+    t.down_w[l] = conv(L.mlp_down_w, d, ff);
   }
+}
+
+size_t weight_bytes_per_layer(const cg_trunk &t) {
+  const cg_trunk_config &c = t.cfg;
+  const int hd = c.n_heads * t.head_dim;
+  const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * t.head_dim;
+  auto bytes = [&](int rows, int cols) {
+    return align_up(t.fused ? packed_fragment_bytes(rows, cols) : size_t(rows) * cols * 2);
+  };
+  return bytes(qkv_rows, c.d_model) + bytes(c.d_model, hd) + bytes(c.d_ff, c.d_model) + bytes(c.d_model, c.d_ff);
 }
 
 }  // namespace
@@ -222,12 +254,8 @@ int cg_trunk_create(const cg_trunk_config *config, const cg_layer_params *layers
       t->down_w[l] = t->layers[l].mlp_down_w;
     }
     if (compute_dtype == CG_BF16) {
-      const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * hd;
-      const size_t per_layer = align_up(size_t(qkv_rows) * c.d_model * 2) +
-                               align_up(size_t(c.d_model) * c.n_heads * hd * 2) +
-                               align_up(size_t(c.d_ff) * c.d_model * 2) +
-                               align_up(size_t(c.d_model) * c.d_ff * 2);
-      t->wbuf_bytes = per_layer * n;
+      t->fused = tail_supported(c.d_model, c.d_ff, (c.n_heads + 2 * c.n_kv_heads) * hd);
+      t->wbuf_bytes = weight_bytes_per_layer(*t) * n;
       CG_HIP(hipMalloc(&t->wbuf, t->wbuf_bytes));
       convert_weights(*t, nullptr);
       CG_HIP(hipStreamSynchronize(nullptr));
@@ -304,18 +332,131 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
       const int n = N > r.n_seqs ? N : r.n_seqs;
       plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout,
                                                   r.n_seqs, N, r.T, max_len, cache[0].capacity,
-                                                  w.tok_row, w.tok_pos, w.readout_tok);
+                                                  w.tok_row, w.tok_pos, w.readout_tok, w.tok_out,
+                                                  hidden, d);
       CG_LAUNCHED();
     }
-    CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
-    launch_layernorm_rows(w.x, nullptr, t.layers[0].ln_attn_w, t.layers[0].ln_attn_b, c.eps, w.xn,
-                          act_dtype, N, d, s);
-
     const float ple_scale = [&] {
       if (c.per_layer_dim == 0 || c.per_layer_dim == d) return 1.0f;
       const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
       return 1.0f / sqrtf(float(repeats));
     }();
+    auto attention = [&](int l) {
+      const cg_kv_layer &L = cache[l];
+      {
+        AttnArgs a{};
+        a.q = w.q;
+        a.q_dtype = CG_F32;
+        a.q_st = int64_t(H) * D;
+        a.q_sh = D;
+        a.q_sb = int64_t(r.T) * H * D;
+        a.out = w.attn;
+        a.out_dtype = act_dtype;
+        a.o_st = int64_t(H) * D;
+        a.o_sh = D;
+        a.o_sb = int64_t(r.T) * H * D;
+        a.k = L.k;
+        a.v = L.v;
+        a.kv_dtype = L.dtype;
+        a.rows = r.rows;
+        a.key_lengths = r.positions;
+        a.kl_add = 1;
+        a.seq_start = r.seq_start;
+        a.n_tokens = N;
+        a.n_seqs = r.n_seqs;
+        a.n_heads = H;
+        a.kv_heads = KVH;
+        a.head_dim = D;
+        a.T = r.T;
+        a.max_len = max_len;
+        a.capacity = L.capacity;
+        a.span = span;
+        a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
+        launch_decode_attention(a, s);
+      }
+    };
+
+    const int n_qkv = (H + 2 * KVH) * D;
+    if (t.fused) {
+      // bf16 projections: one fused launch per layer after its attention (layer.hip), plus
+      // the first block's LN + QKV + append.
+      auto base = [&] {
+        TailArgs ta{};
+        ta.M = N;
+        ta.d = d;
+        ta.d_ff = c.d_ff;
+        ta.n_qkv = n_qkv;
+        ta.q_cols = H * D;
+        ta.kv_heads = KVH;
+        ta.head_dim = D;
+        ta.max_len = max_len;
+        ta.kv_dtype = cache[0].dtype;
+        ta.eps = c.eps;
+        ta.q = w.q;
+        ta.tok_row = w.tok_row;
+        ta.tok_pos = w.tok_pos;
+        ta.vemb = values;
+        ta.ld_vemb = c.value_width;
+        ta.vemb_off = -1;
+        ta.hidden = hidden;
+        ta.tok_out = w.tok_out;
+        return ta;
+      };
+      auto set_next = [&](TailArgs &ta, int nl) {
+        if (nl == c.n_layers) {
+          ta.final_ln = 1;
+          ta.ln_w = t.final_w;
+          ta.ln_b = t.final_b;
+          return;
+        }
+        const cg_layer_params &Pn = t.layers[nl];
+        ta.final_ln = 0;
+        ta.ln_w = Pn.ln_attn_w;
+        ta.ln_b = Pn.ln_attn_b;
+        ta.w_qkv = t.qkv_w[nl];
+        ta.kc = cache[nl].k;
+        ta.vc = cache[nl].v;
+        ta.vemb_off = (values && Pn.value_index >= 0) ? Pn.value_index * KVH * D : -1;
+      };
+      {
+        TailArgs ta = base();
+        ta.do_post = 0;
+        ta.x_src = x;
+        ta.x = w.x;
+        set_next(ta, 0);
+        launch_tail(ta, s);
+      }
+      for (int l = 0; l < c.n_layers; ++l) {
+        attention(l);
+        const cg_layer_params &P = t.layers[l];
+        TailArgs ta = base();
+        ta.do_post = 1;
+        ta.attn = w.attn;
+        ta.w_out = t.out_w[l];
+        ta.w_up = t.up_w[l];
+        ta.b_up = P.mlp_up_b;
+        ta.w_down = t.down_w[l];
+        ta.b_down = P.mlp_down_b;
+        ta.ln2_w = P.ln_mlp_w;
+        ta.ln2_b = P.ln_mlp_b;
+        if (ple && c.per_layer_dim > 0) {
+          ta.ple = ple;
+          ta.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
+          ta.ple_off = l * c.per_layer_dim;
+          ta.ple_dim = c.per_layer_dim;
+          ta.ple_scale = ple_scale;
+        }
+        ta.x_src = w.x;
+        ta.x = w.x;
+        set_next(ta, l + 1);
+        launch_tail(ta, s);
+      }
+      return;
+    }
+
+    CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
+    launch_layernorm_rows(w.x, nullptr, t.layers[0].ln_attn_w, t.layers[0].ln_attn_b, c.eps, w.xn,
+                          act_dtype, N, d, s);
     // Whole-row residual tiles fuse the next LayerNorm into the residual epilogue.
     const bool fused_ln = d <= 256;
 
@@ -384,37 +525,7 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
         g.vemb_off = (values && P.value_index >= 0) ? P.value_index * KVH * D : -1;
         launch_gemm(g, s);
       }
-      {  // attention
-        AttnArgs a{};
-        a.q = w.q;
-        a.q_dtype = CG_F32;
-        a.q_st = int64_t(H) * D;
-        a.q_sh = D;
-        a.q_sb = int64_t(r.T) * H * D;
-        a.out = w.attn;
-        a.out_dtype = act_dtype;
-        a.o_st = int64_t(H) * D;
-        a.o_sh = D;
-        a.o_sb = int64_t(r.T) * H * D;
-        a.k = L.k;
-        a.v = L.v;
-        a.kv_dtype = L.dtype;
-        a.rows = r.rows;
-        a.key_lengths = r.positions;
-        a.kl_add = 1;
-        a.seq_start = r.seq_start;
-        a.n_tokens = N;
-        a.n_seqs = r.n_seqs;
-        a.n_heads = H;
-        a.kv_heads = KVH;
-        a.head_dim = D;
-        a.T = r.T;
-        a.max_len = max_len;
-        a.capacity = L.capacity;
-        a.span = span;
-        a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
-        launch_decode_attention(a, s);
-      }
+      attention(l);
       // out_proj + residual, then LN2 -> xn
       residual(w.attn, H * D, t.out_w[l], nullptr, P.ln_mlp_w, P.ln_mlp_b, nullptr, l);
       {  // mlp[0] + GELU

@@ -8,6 +8,7 @@ import numpy as np
 import torch
 
 from card_playing_gym_amd.nn.kv_cache import KVCache
+from card_playing_gym_amd.nn.trunk import Trunk, TrunkConfig
 from card_playing_gym_amd.synthetic import StepPlan, build_model
 from oracle.reference_path import RefCache, RefSynthetic, ref_config_of
 
@@ -92,3 +93,17 @@ def run_oracle(ref: RefSynthetic, cache: RefCache, plan: StepPlan, rows: bool):
 
 def max_err(a: torch.Tensor, b: torch.Tensor) -> float:
     return (a.detach().float().cpu() - b.detach().float().cpu()).abs().max().item()
+
+
+def random_trunk(config: TrunkConfig, seed: int = 0, scale: float = 0.05) -> dict[str, torch.Tensor]:
+    """A trunk state dict with every parameter perturbed (so zero-initialised PLE / VE
+    tables and biases carry signal), like the reference's ``randomize`` fixture."""
+
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        trunk = Trunk(config)
+        gen = torch.Generator().manual_seed(seed + 1)
+        with torch.no_grad():
+            for p in trunk.parameters():
+                p.add_(scale * torch.randn(p.shape, generator=gen))
+    return {f"trunk.{k}": v.detach().clone() for k, v in trunk.state_dict().items()}

@@ -32,6 +32,7 @@ import torch
 
 from card_playing_gym_amd.nn.trunk import Trunk, TrunkConfig
 from oracle.reference_path import RefCache, RefConfig, RefTrunk, ref_config_of
+from tests.helpers import random_trunk
 
 
 # ---- helpers -------------------------------------------------------------------------
@@ -45,20 +46,6 @@ def bf16_rne_bits(x: np.ndarray) -> np.ndarray:
     nan = np.isnan(x)
     rounded[nan] = 0x7FC0
     return rounded
-
-
-def random_trunk(config: TrunkConfig, seed: int = 0, scale: float = 0.05) -> dict[str, torch.Tensor]:
-    """A trunk state dict with every parameter perturbed (so zero-initialised PLE / VE
-    tables and biases carry signal), like the reference's ``randomize`` fixture."""
-
-    with torch.random.fork_rng(devices=[]):
-        torch.manual_seed(seed)
-        trunk = Trunk(config)
-        gen = torch.Generator().manual_seed(seed + 1)
-        with torch.no_grad():
-            for p in trunk.parameters():
-                p.add_(scale * torch.randn(p.shape, generator=gen))
-    return {f"trunk.{k}": v.detach().clone() for k, v in trunk.state_dict().items()}
 
 
 # ---- KV pool -------------------------------------------------------------------------
