@@ -154,7 +154,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
     return {
-        "kernel": "decode_attention_mfma_kernel<bf16,32,1>",
+        "kernel": "decode_attention_tr_kernel<bf16,32,1>",
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,

@@ -98,7 +98,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(AttnArgs a
 
   const int unit = blockIdx.x;
   const int b = unit / a.kv_heads, h = unit % a.kv_heads;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform: readfirstlane lets the compiler keep everything derived
+  // from it (unit, row, descriptors) in scalar registers.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slot = lane >> 2, e = lane & 3;
   const int G = a.n_heads / a.kv_heads;
 
@@ -329,7 +331,9 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
   constexpr int ROW = D * ES + 8;     // padded LDS row of V (bytes): conflict-free transposed reads
   __shared__ __align__(16) unsigned char vtile[4][KT * ROW];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform: readfirstlane lets the compiler keep everything derived
+  // from it (unit, row, pointers) in scalar registers.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int unit = blockIdx.x * 4 + wave;
   if (unit >= a.n_seqs * a.kv_heads) return;  // the whole wave leaves; no block barriers below
   const int b = unit / a.kv_heads, h = unit % a.kv_heads;
@@ -581,12 +585,340 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// 16-bit pools (bf16 / fp16), head_dim 32 / 64: the same dataflow as above with the VALU
+// and LDS work per key cut down.
+//   * K / V tiles arrive through a buffer descriptor over the (row, KV head) segment,
+//     unconditionally (keys past the visible range are clamped onto the last visible key,
+//     whose value is finite, and get probability 0), so the loads land directly in the
+//     registers the MFMAs read and the next tile's loads are in flight during this tile.
+//   * Masks are applied only on tiles that reach past some query's limit.
+//   * The per-query running max needs one cross-lane step per tile: the four lane groups
+//     holding a query column's keys meet through v_permlane16/32_swap (VALU, no LDS).  The
+//     running sum stays per lane and is merged once at the end.
+//   * V^T fragments for O^T += V^T . P^T come from V rows stored as loaded in LDS through
+//     ds_read_b64_tr_b16: within each 16-lane group, result lane i, element e is element
+//     i % 4 of the 8 bytes lane 4 e + i / 4 addressed; lane j addressing key (j / 4) of a
+//     4-key run at dims 4 (j % 4) .. +3 therefore receives 4 consecutive keys of dim j.
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+// Max / min of an int over the 16 lanes of a DPP row.
+__device__ __forceinline__ int row16_max(int v) {
+  v = max(v, dpp_i<0xB1>(v));
+  v = max(v, dpp_i<0x4E>(v));
+  v = max(v, dpp_i<0x124>(v));
+  v = max(v, dpp_i<0x128>(v));
+  return v;
+}
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x124>(v));
+  v = min(v, dpp_i<0x128>(v));
+  return v;
+}
+
+// SPLIT waves share one (sequence, KV head): wave p of the unit takes tiles p, p + SPLIT,
+// ...; their partial (max, sum, O) merge in LDS at the end (SPLIT 1: four units per block).
+template <typename TKV, int D, int NQT, int SPLIT>
+__global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
+  static_assert(SPLIT == 1 || SPLIT == 4, "a block holds 4 / SPLIT whole units");
+  constexpr int KT = 64;          // keys per tile
+  constexpr int NJ = KT / 16;     // 16-key score tiles per key tile
+  constexpr int DK = D / 32;      // 32-dim slices of a key (S^T k-steps)
+  constexpr int DH = D / 16;      // 16-dim slices of the output (O^T row tiles)
+  constexpr int ROW = D * 2 + 8;  // LDS bytes per V row (8-byte aligned, rows spread over banks)
+  __shared__ __align__(16) unsigned char vtile[4][KT * ROW];
+  // Partial results of the SPLIT waves of a unit: max and sum per query column, O^T tiles.
+  __shared__ float part_m[SPLIT > 1 ? 4 : 1][NQT][16], part_l[SPLIT > 1 ? 4 : 1][NQT][16];
+  __shared__ f32x4 part_o[SPLIT > 1 ? 4 : 1][NQT][DH][64];
+
+  // The wave index is uniform: readfirstlane lets the compiler keep everything derived
+  // from it (unit, row, descriptors) in scalar registers.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int unit = blockIdx.x * (4 / SPLIT) + wave / SPLIT;
+  const int part = wave % SPLIT;
+  // A unit's waves all leave together (same unit), so block barriers below stay matched.
+  if (unit >= a.n_seqs * a.kv_heads) return;
+  const int b = unit / a.kv_heads, h = unit % a.kv_heads;
+  const int li = lane & 15, lg = lane >> 4;
+  const int G = a.n_heads / a.kv_heads;
+  unsigned char *vt = vtile[wave];
+
+  const int64_t row = a.rows ? a.rows[b] : int64_t(b);
+  int64_t tok0 = 0, count = a.T;
+  if (a.seq_start) {
+    int64_t lo = a.seq_start[b], hi = a.seq_start[b + 1];
+    lo = lo < 0 ? 0 : (lo > a.n_tokens ? a.n_tokens : lo);
+    hi = hi < lo ? lo : (hi > a.n_tokens ? a.n_tokens : hi);
+    tok0 = lo;
+    count = hi - lo;
+  }
+  const int64_t q_base = a.seq_start ? tok0 * a.q_st : int64_t(b) * a.q_sb;
+  const int64_t o_base = a.seq_start ? tok0 * a.o_st : int64_t(b) * a.o_sb;
+  const int64_t kl = a.key_lengths[b] + a.kl_add;
+  const bool row_ok = row >= 0 && row < a.capacity;
+  // This (row, head) segment: max_len keys of D elements.
+  const int64_t seg = row_ok ? (row * a.kv_heads + h) * int64_t(a.max_len) * D : 0;
+  const uint32_t seg_bytes = uint32_t(a.max_len) * D * 2;
+  const Rsrc kres = make_rsrc(static_cast<const TKV *>(a.k) + seg, seg_bytes);
+  const Rsrc vres = make_rsrc(static_cast<const TKV *>(a.v) + seg, seg_bytes);
+
+  const int nq = int(count) * G;
+  for (int qg = 0; qg < nq; qg += NQT * 16) {
+    // ---- queries of this group: column li of tile qt is query qg + 16 qt + li ----------
+    int lim[NQT];
+    typename Mfma16<TKV>::vec qv[NQT][DK];
+    int kmax = 0, kmin = 0x7fffffff;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const int m = qg + 16 * qt + li;
+      f32x8 f[DK];
+      int l = 0;
+      if (m < nq) {
+        const int t = m / G, g = m % G;
+        const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st;
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[dk][e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e) * a.scale_log2;
+        int64_t lim64 = kl + t;
+        if (lim64 > a.span) lim64 = a.span;
+        l = (row_ok && lim64 > 0) ? int(lim64) : 0;
+        kmin = min(kmin, l);
+      } else {
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[dk][e] = 0.f;
+      }
+#pragma unroll
+      for (int dk = 0; dk < DK; ++dk) qv[qt][dk] = Mfma16<TKV>::from(f[dk]);
+      lim[qt] = l;
+      kmax = max(kmax, l);
+    }
+    // Uniform bounds: keys below kmin are visible to every query, none at or past kend.
+    const int kend = __builtin_amdgcn_readfirstlane(row16_max(kmax));
+    const int kfull = __builtin_amdgcn_readfirstlane(row16_min(kmin));
+
+    f32x4 acc[NQT][DH];
+    float mrun[NQT], lsum[NQT];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      mrun[qt] = NEG_BIG;
+      lsum[qt] = 0.f;
+#pragma unroll
+      for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // Lane l holds key 16 j + l % 16 of a tile at dims 32 dk + 8 (l / 16), for K and V.
+    uint4 kr[NJ][DK], vr[NJ][DK];
+    auto fetch = [&](int kb) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int key = min(kb + 16 * j + li, kend - 1);
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
+          kr[j][dk] = bload16(kres, off);
+          vr[j][dk] = bload16(vres, off);
+        }
+      }
+    };
+    if (part * KT < kend) fetch(part * KT);
+    for (int kb = part * KT; kb < kend; kb += SPLIT * KT) {
+      // ---- scores S^T[key, query] -----------------------------------------------------
+      f32x4 sc[NQT][NJ];
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int dk = 0; dk < DK; ++dk) {
+            typename Mfma16<TKV>::vec kvec;
+            __builtin_memcpy(&kvec, &kr[j][dk], 16);
+            s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
+          }
+          sc[qt][j] = s4;
+        }
+      // ---- V rows -> LDS (as loaded), then the next tile's loads ----------------------
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          unsigned char *dst = vt + (16 * j + li) * ROW + (32 * dk + 8 * lg) * 2;
+          reinterpret_cast<uint2 *>(dst)[0] = uint2{vr[j][dk].x, vr[j][dk].y};
+          reinterpret_cast<uint2 *>(dst)[1] = uint2{vr[j][dk].z, vr[j][dk].w};
+        }
+      fetch(kb + SPLIT * KT);  // clamped: past kend it re-reads the last visible key
+
+      // ---- mask (only tiles reaching past some query's limit) --------------------------
+      if (kb + KT > kfull) {
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (kb + 16 * j + 4 * lg + i >= lim[qt]) sc[qt][j][i] = -INFINITY;
+      }
+      // ---- online softmax per query column ----------------------------------------------
+      float p[NQT][NJ][4];
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        float tmax = NEG_BIG;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[qt][j][i]);
+        tmax = xor32_max(xor16_max(tmax));
+        const float mnew = fmaxf(mrun[qt], tmax);
+        const float corr = fast_exp2(mrun[qt] - mnew);
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p[qt][j][i] = fast_exp2(sc[qt][j][i] - mnew);
+            psum += p[qt][j][i];
+          }
+        lsum[qt] = fmaf(lsum[qt], corr, psum);
+        mrun[qt] = mnew;
+#pragma unroll
+        for (int dh = 0; dh < DH; ++dh) acc[qt][dh] *= corr;
+      }
+      // ---- O^T += V^T . P^T (k slot 8 (l / 16) + e of chunk c is key
+      //      32 c + 16 (e / 4) + 4 (l / 16) + e % 4) ------------------------------------------
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int c = 0; c < KT / 32; ++c) {
+        typename Mfma16<TKV>::vec pv[NQT];
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+          f32x8 f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = p[qt][2 * c + (e >> 2)][e & 3];
+          pv[qt] = Mfma16<TKV>::from(f);
+        }
+#pragma unroll
+        for (int dh = 0; dh < DH; ++dh) {
+          const unsigned char *src = vt + (32 * c + 4 * lg + (li >> 2)) * ROW + (16 * dh + 4 * (li & 3)) * 2;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4 *)(src));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4 *)(src + 16 * ROW));
+          typename Mfma16<TKV>::vec vv;
+          __builtin_memcpy(&vv, &lo, 8);
+          __builtin_memcpy(reinterpret_cast<char *>(&vv) + 8, &hi, 8);
+#pragma unroll
+          for (int qt = 0; qt < NQT; ++qt) acc[qt][dh] = Mfma16<TKV>::mma(vv, pv[qt], acc[qt][dh]);
+        }
+      }
+    }
+
+    if constexpr (SPLIT > 1) {
+      // ---- merge the unit's SPLIT partial softmax states (log-sum-exp) ------------------
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
+        lsum[qt] = xor32_sum(xor16_sum(lsum[qt]));
+        if (lg == 0) {
+          part_m[wave][qt][li] = mrun[qt];
+          part_l[wave][qt][li] = lsum[qt];
+        }
+#pragma unroll
+        for (int dh = 0; dh < DH; ++dh) part_o[wave][qt][dh][lane] = acc[qt][dh];
+      }
+      __syncthreads();
+      if (part == 0) {
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+          float mm = part_m[wave][qt][li];
+#pragma unroll
+          for (int w = 1; w < SPLIT; ++w) mm = fmaxf(mm, part_m[wave + w][qt][li]);
+          float l = 0.f;
+#pragma unroll
+          for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int w = 0; w < SPLIT; ++w) {
+            const float c = fast_exp2(part_m[wave + w][qt][li] - mm);
+            l = fmaf(part_l[wave + w][qt][li], c, l);
+#pragma unroll
+            for (int dh = 0; dh < DH; ++dh) acc[qt][dh] += part_o[wave + w][qt][dh][lane] * c;
+          }
+          lsum[qt] = l;
+        }
+      }
+      __syncthreads();  // partials consumed before the next query group reuses them
+      if (part != 0) continue;
+    }
+    // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const float total = SPLIT > 1 ? lsum[qt] : xor32_sum(xor16_sum(lsum[qt]));
+      const int m = qg + 16 * qt + li;
+      if (m >= nq) continue;
+      const int t = m / G, g = m % G;
+      const float inv = total > 0.f ? 1.0f / total : 0.f;
+      const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st;
+#pragma unroll
+      for (int dh = 0; dh < DH; ++dh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[qt][dh][i] * inv);
+    }
+  }
+}
+
+#ifndef TR_SPLIT
+#define TR_SPLIT 4
+#endif
+
 template <typename TKV, int D>
 void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
   const unsigned grid = unsigned((int64_t(a.n_seqs) * a.kv_heads + 3) / 4);
-  if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
-  else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);
-  else decode_attention_mfma_kernel<TKV, D, 4><<<grid, 256, 0, s>>>(a);
+  if constexpr (sizeof(TKV) == 2) {
+    CG_REQUIRE(int64_t(a.max_len) * D * 2 < (int64_t(1) << 31), CG_ERR_UNSUPPORTED,
+               "decode attention: one cache row of one head must stay below 2 GiB");
+    const unsigned units = unsigned(int64_t(a.n_seqs) * a.kv_heads);
+    if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT><<<(units * TR_SPLIT + 3) / 4, 256, 0, s>>>(a);
+    else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT><<<(units * TR_SPLIT + 3) / 4, 256, 0, s>>>(a);
+    else decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT><<<(units * TR_SPLIT + 3) / 4, 256, 0, s>>>(a);
+  } else {
+    if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
+    else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);
+    else decode_attention_mfma_kernel<TKV, D, 4><<<grid, 256, 0, s>>>(a);
+  }
   CG_LAUNCHED();
 }
 

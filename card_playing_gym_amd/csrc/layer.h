@@ -54,8 +54,8 @@ struct TailArgs {
 size_t packed_fragment_bytes(int N, int K);
 void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_t stream);
 
-// Shapes the fused kernel is built for: d_model <= 256 and a multiple of 16, d_ff a
-// multiple of 16, n_qkv a multiple of 16, bf16 projections.
+// Shapes the fused kernel is built for: d_model <= 256 and a multiple of 16, d_ff <= 1024
+// and n_qkv <= 768, both multiples of 16; bf16 projections.
 bool tail_supported(int d, int d_ff, int n_qkv);
 
 void launch_tail(const TailArgs &a, hipStream_t stream);

@@ -82,6 +82,11 @@ __device__ __forceinline__ int opaque(int v) {
   __asm__ volatile("" : "+s"(v));
   return v;
 }
+template <typename T>
+__device__ __forceinline__ const T *opaque_ptr(const T *p) {
+  __asm__ volatile("" : "+s"(p));
+  return p;
+}
 __device__ __forceinline__ int opaque_lane(int v) {
   __asm__ volatile("" : "+v"(v));
   return v;
@@ -131,10 +136,14 @@ __device__ __forceinline__ Slice stage_slice(const TailArgs &a, const Plan &p, i
   const int kind = stage_kind(p, s, c);
   const int d = a.d;
   const uint32_t kd = kblocks_of(d), kf = kblocks_of(a.d_ff);
-  if (kind == ST_OUT) return Slice{rsrc(a.w_out, uint32_t(d) * kd * 64), kd, cw / 16, 0};
-  if (kind == ST_UP) return Slice{rsrc(a.w_up, uint32_t(a.d_ff) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
-  if (kind == ST_DOWN) return Slice{rsrc(a.w_down, uint32_t(d) * kf * 64), kf, cw / 16, (PANEL / 32) * c};
-  return Slice{rsrc(a.w_qkv, uint32_t(a.n_qkv) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
+  // Descriptors are rebuilt per stage from laundered pointers: four of them hoisted out of
+  // the stage loop would hold 16 scalar registers for the whole kernel.
+  if (kind == ST_OUT) return Slice{rsrc(opaque_ptr(a.w_out), uint32_t(d) * kd * 64), kd, cw / 16, 0};
+  if (kind == ST_UP)
+    return Slice{rsrc(opaque_ptr(a.w_up), uint32_t(a.d_ff) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
+  if (kind == ST_DOWN)
+    return Slice{rsrc(opaque_ptr(a.w_down), uint32_t(d) * kf * 64), kf, cw / 16, (PANEL / 32) * c};
+  return Slice{rsrc(opaque_ptr(a.w_qkv), uint32_t(a.n_qkv) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
 }
 
 __device__ __forceinline__ uint32_t slice_base(const Slice &s, int j, int lane) {
@@ -160,22 +169,19 @@ template <int FM>
 __device__ __forceinline__ void stage_mma(f32x4 (&acc)[FM][FN], const unsigned char *lds,
                                           uint4 (&w)[KS][FN], const Slice &next, int lane) {
   const int li = lane & 15, lg = lane >> 4;
-  // All of the stage's A fragments first: one LDS round trip instead of one per k-step.
-  uint4 af[KS][FM];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[ks][i] = *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
   uint32_t base[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) base[j] = slice_base(next, j, lane);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
+    uint4 af[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[i] = *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[ks][i], w[ks][j], acc[i][j]);
+      for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[i], w[ks][j], acc[i][j]);
 #pragma unroll
     for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
   }
@@ -204,72 +210,106 @@ __device__ __forceinline__ float sum16(float v) {
 }
 
 // LayerNorm statistics of rows held in the MFMA layout: v[i][j][r] is row 16 i + 4 lg + r,
-// column cw + 16 j + li (columns >= d hold 0 and are excluded).  Two passes (mean, then
-// centred squares), each reduced over the fragment's 16 lanes and the block's waves.
+// column cw + 16 j + li (columns >= d hold 0 and are excluded).  Each wave first takes the
+// exact two-pass mean and centred sum of squares of its own columns (DPP sums over the
+// fragment's 16 lanes, no barrier), then the waves' (count, mean, M2) triples merge with
+// Chan et al.'s pairwise formula, M2 = sum_w [M2_w + n_w (mean_w - mean)^2]: one barrier.
 template <int BM>
 __device__ __forceinline__ void row_stats(const f32x4 (&v)[BM / 16][FN], int cw, int d, float eps,
                                           float (&mean)[BM / 16][4], float (&rstd)[BM / 16][4],
                                           float *red, int wave, int li, int lg) {
   constexpr int FM = BM / 16;
+  // Columns this wave holds (the same for every row): cw .. cw + 16 FN - 1, capped at d.
+  const int nw = max(0, min(16 * FN, d - cw));
+  const float inv_nw = nw > 0 ? 1.0f / float(nw) : 0.f;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if (cw + 16 * j + li < d) sum += v[i][j][r];
+      const float mw = sum16(sum) * inv_nw;
+      float sq = 0.f;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if (cw + 16 * j + li < d) sq += (v[i][j][r] - mw) * (v[i][j][r] - mw);
+      const float m2 = sum16(sq);
+      if (li == 0) {
+        const int row = 16 * i + 4 * lg + r;
+        red[(0 * WAVES + wave) * BM + row] = mw;
+        red[(1 * WAVES + wave) * BM + row] = m2;
+      }
+    }
+  lds_barrier();
   const float inv_d = 1.0f / float(d);
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * i + 4 * lg + r;
+      float total = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s = 0.f;
+      for (int w = 0; w < WAVES; ++w)
+        total = fmaf(float(max(0, min(16 * FN, d - 16 * FN * w))), red[(0 * WAVES + w) * BM + row], total);
+      const float mu = total * inv_d;
+      float m2 = 0.f;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          if (cw + 16 * j + li < d) {
-            const float x = v[i][j][r];
-            s += pass == 0 ? x : (x - mean[i][r]) * (x - mean[i][r]);
-          }
-        }
-        s = sum16(s);
-        if (li == 0) red[(pass * WAVES + wave) * BM + 16 * i + 4 * lg + r] = s;
+      for (int w = 0; w < WAVES; ++w) {
+        const float n = float(max(0, min(16 * FN, d - 16 * FN * w)));
+        const float dm = red[(0 * WAVES + w) * BM + row] - mu;
+        m2 += fmaf(n * dm, dm, red[(1 * WAVES + w) * BM + row]);
       }
-    lds_barrier();
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * i + 4 * lg + r;
-        float s = 0.f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) s += red[(pass * WAVES + w) * BM + row];
-        if (pass == 0) mean[i][r] = s * inv_d;
-        else rstd[i][r] = rsqrtf(s * inv_d + eps);
-      }
-  }
+      mean[i][r] = mu;
+      rstd[i][r] = rsqrtf(m2 * inv_d + eps);
+    }
+}
+
+// GELU with erf (torch.nn.GELU()): 0.5 x (1 + erf(x / sqrt 2)), erf from the rational
+// approximation of Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7, far below the bf16
+// rounding the result gets): erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-z^2},
+// t = 1 / (1 + p |z|), sign restored for z < 0.  About a dozen VALU instructions.
+__device__ __forceinline__ float gelu_fast(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
+  const float erf_abs = fmaf(-poly * t, e, 1.0f);
+  const float erf_z = x < 0.f ? -erf_abs : erf_abs;
+  return 0.5f * x * (1.0f + erf_z);
 }
 
 // LN(v) -> the panel (bf16, the next QKV stage's A operand), or, for the last block, the
 // final norm -> hidden rows of readout tokens.
+// Per-layer vectors and the block's token slots, staged in LDS by the kernel prologue.
+struct Params {
+  float *b_up, *b_down, *ln2_w, *ln2_b, *ln_w, *ln_b;  // [d_ff] and [PANEL] each
+  int *tok_row, *tok_pos, *tok_out;                    // [BM] each
+};
+
 template <int BM>
-__device__ __forceinline__ void next_prologue(const TailArgs &a, const f32x4 (&v)[BM / 16][FN],
+__device__ __forceinline__ void next_prologue(const TailArgs &a, const Params &prm, const f32x4 (&v)[BM / 16][FN],
                                               unsigned char *panel, float *red, int m0, int cw,
                                               int wave, int li, int lg) {
   constexpr int FM = BM / 16;
   float mean[FM][4], rstd[FM][4];
-  const Rsrc rw = rsrc(a.ln_w, uint32_t(a.d) * 4), rb = rsrc(a.ln_b, uint32_t(a.d) * 4);
   float lw[FN], lb[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const uint32_t n = uint32_t(cw + 16 * j + li);
-    lw[j] = bloadf(rw, 4 * n);
-    lb[j] = bloadf(rb, 4 * n);
+    const int n = cw + 16 * j + li;
+    lw[j] = prm.ln_w[n];
+    lb[j] = prm.ln_b[n];
   }
   int out_row[FM][4];
   if (a.final_ln) {
-    const Rsrc ro = rsrc(a.tok_out, uint32_t(a.M) * 4);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 16 * i + 4 * lg + r;
-        out_row[i][r] = m < a.M ? bloadi(ro, 4 * uint32_t(m)) : -1;
-      }
+      for (int r = 0; r < 4; ++r) out_row[i][r] = prm.tok_out[16 * i + 4 * lg + r];
   }
   row_stats<BM>(v, cw, a.d, a.eps, mean, rstd, red, wave, li, lg);
 #pragma unroll
@@ -298,25 +338,63 @@ __device__ __forceinline__ void store_kv(void *base, int dtype, int64_t index, f
   else gst(static_cast<float *>(base) + index, v);
 }
 
-template <int BM>
+// MODE: 0 = first block's prologue (x = x_src, LN + QKV), 1 = post + next QKV, 2 = post +
+// final norm.  NC / NQ: 256-wide chunks of d_ff / of the QKV width.  The stage sequence is
+// a compile-time constant, so the fully unrolled stage loop folds every stage's kind and
+// the weight registers flow from stage to stage without merges.
+template <int BM, int MODE, int NC, int NQ>
 __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   constexpr int FM = BM / 16;
+  constexpr bool POST = MODE != 0, FINAL = MODE == 2;
   __shared__ __align__(16) unsigned char panel[BM * ROWB];
   __shared__ __align__(16) unsigned char hbuf[2][BM * ROWB];
   __shared__ float red[2 * WAVES * BM];
+  extern __shared__ float dyn[];  // Params: d_ff + 5 PANEL floats, then 3 BM ints
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is uniform: readfirstlane keeps its derived column ranges scalar.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cw = 16 * FN * wave;
   const int d = a.d;
+  constexpr int N_POST = POST ? 1 + 2 * NC : 0;
+  constexpr int S = N_POST + (FINAL ? 0 : NQ);
   Plan p;
-  p.nc = (a.d_ff + PANEL - 1) / PANEL;
-  p.nq = a.final_ln ? 0 : (a.n_qkv + PANEL - 1) / PANEL;
-  p.n_post = a.do_post ? 1 + 2 * p.nc : 0;
-  p.S = p.n_post + p.nq;
+  p.nc = NC;
+  p.nq = FINAL ? 0 : NQ;
+  p.n_post = N_POST;
+  p.S = S;
   const uint32_t xbytes = uint32_t(a.M) * uint32_t(d) * 4;
 
   uint4 cur[KS][FN];
   if (p.S > 0) load_slice(cur, stage_slice(a, p, 0, cw), lane);
+
+  Params prm;
+  prm.b_up = dyn;
+  prm.b_down = dyn + a.d_ff;
+  prm.ln2_w = prm.b_down + PANEL;
+  prm.ln2_b = prm.ln2_w + PANEL;
+  prm.ln_w = prm.ln2_b + PANEL;
+  prm.ln_b = prm.ln_w + PANEL;
+  prm.tok_row = reinterpret_cast<int *>(prm.ln_b + PANEL);
+  prm.tok_pos = prm.tok_row + BM;
+  prm.tok_out = prm.tok_pos + BM;
+  {
+    const int m0 = blockIdx.x * BM;
+    for (int i = tid; i < a.d_ff; i += THREADS) prm.b_up[i] = a.do_post ? a.b_up[i] : 0.f;
+    for (int i = tid; i < PANEL; i += THREADS) {
+      const bool in = i < d;
+      prm.b_down[i] = in && a.do_post ? a.b_down[i] : 0.f;
+      prm.ln2_w[i] = in && a.do_post ? a.ln2_w[i] : 0.f;
+      prm.ln2_b[i] = in && a.do_post ? a.ln2_b[i] : 0.f;
+      prm.ln_w[i] = in ? a.ln_w[i] : 0.f;
+      prm.ln_b[i] = in ? a.ln_b[i] : 0.f;
+    }
+    for (int i = tid; i < BM; i += THREADS) {
+      const bool in = m0 + i < a.M;
+      prm.tok_row[i] = in && !a.final_ln ? a.tok_row[m0 + i] : -1;
+      prm.tok_pos[i] = in && !a.final_ln ? a.tok_pos[m0 + i] : 0;
+      prm.tok_out[i] = in && a.final_ln ? a.tok_out[m0 + i] : -1;
+    }
+  }
 
   // Zero the LDS panels once: padding columns (k >= d, or past d_ff) stay zero.
   for (int o = tid * 16; o < BM * ROWB; o += THREADS * 16) {
@@ -356,11 +434,12 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
             if (ok && a.x != a.x_src) gst(a.x + int64_t(m) * d + n, v);
             acc[i][j][r] = ok ? v : 0.f;
           }
-      next_prologue<BM>(a, acc, panel, red, m0, cw, wave, li, lg);
+      next_prologue<BM>(a, prm, acc, panel, red, m0, cw, wave, li, lg);
     }
   }
 
-  for (int s = 0; s < p.S; ++s) {
+#pragma clang loop unroll(full)
+  for (int s = 0; s < S; ++s) {
     const int m0 = opaque(blockIdx.x * BM);
     const int lane_o = opaque_lane(lane);
     const int li = lane_o & 15, lg = lane_o >> 4;
@@ -370,19 +449,21 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
     const Slice nx = stage_slice(a, p, s + 1 < p.S ? s + 1 : s, cw);
     if (kind == ST_OUT) {
       // ---- out-proj + residual, then LN(ln_mlp) -> panel
-      const Rsrc rs = rsrc(a.x_src, xbytes);
-      const Rsrc rw = rsrc(a.ln2_w, uint32_t(d) * 4), rb = rsrc(a.ln2_b, uint32_t(d) * 4);
+      const Rsrc rs = rsrc(opaque_ptr(a.x_src), xbytes);
       float xr[FM][FN][4], lw[FN], lb[FN];
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int n = cw + 16 * j + li;
-        lw[j] = bloadf(rw, 4 * uint32_t(n));
-        lb[j] = bloadf(rb, 4 * uint32_t(n));
+        lw[j] = prm.ln2_w[n];
+        lb[j] = prm.ln2_b[n];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) xr[i][j][r] = bloadf(rs, (uint32_t(m0 + 16 * i + 4 * lg + r) * d + n) * 4);
       }
+      // Issue the residual loads ahead of this stage's weight refills: loads complete in
+      // order, so the epilogue then waits only for them, not for the next stage's weights.
+      __builtin_amdgcn_sched_barrier(0);
       zero<FM>(acc);
       stage_mma<FM>(acc, panel, cur, nx, lane_o);
 #pragma unroll
@@ -417,10 +498,12 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
       lds_barrier();
     } else if (kind == ST_UP) {
       // ---- up chunk c + GELU -> hbuf[c & 1]
-      const Rsrc rb = rsrc(a.b_up, uint32_t(a.d_ff) * 4);
       float bias[FN];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bias[j] = bloadf(rb, 4 * uint32_t(PANEL * c + cw + 16 * j + li));
+      for (int j = 0; j < FN; ++j) {
+        const int n = PANEL * c + cw + 16 * j + li;
+        bias[j] = n < a.d_ff ? prm.b_up[n] : 0.f;
+      }
       zero<FM>(acc);
       stage_mma<FM>(acc, panel, cur, nx, lane_o);
       unsigned char *hb = hbuf[c & 1];
@@ -433,7 +516,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int row = 16 * i + 4 * lg + r;
-            const float g = ok ? gelu_erf(acc[i][j][r] + bias[j]) : 0.f;
+            const float g = ok ? gelu_fast(acc[i][j][r] + bias[j]) : 0.f;
             *reinterpret_cast<bf16 *>(hb + row * ROWB + col * 2) = from_f32<bf16>(g);
           }
       }
@@ -443,12 +526,12 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
       const bool last = c == p.nc - 1;
       float xr[FM][FN][4], bias[FN];
       if (last) {
-        const Rsrc rx = rsrc(a.x, xbytes), rb = rsrc(a.b_down, uint32_t(d) * 4);
-        const Rsrc rp = rsrc(a.ple, a.ple ? uint32_t(a.M) * uint32_t(a.ld_ple) * 4 : 0u);
+        const Rsrc rx = rsrc(opaque_ptr(a.x), xbytes);
+        const Rsrc rp = rsrc(opaque_ptr(a.ple), a.ple ? uint32_t(a.M) * uint32_t(a.ld_ple) * 4 : 0u);
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const int n = cw + 16 * j + li;
-          bias[j] = bloadf(rb, 4 * uint32_t(n));
+          bias[j] = prm.b_down[n];
 #pragma unroll
           for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -461,6 +544,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
             }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);  // residual loads ahead of the weight refills
       stage_mma<FM>(accd, hbuf[c & 1], cur, nx, lane_o);
       if (last) {
 #pragma unroll
@@ -479,19 +563,17 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
               accd[i][j][r] = v;
             }
         }
-        next_prologue<BM>(a, accd, panel, red, m0, cw, wave, li, lg);
+        next_prologue<BM>(a, prm, accd, panel, red, m0, cw, wave, li, lg);
       }
     } else {
       // ---- qkv chunk: q stored, k / v appended to the pool
-      const Rsrc rr = rsrc(a.tok_row, uint32_t(a.M) * 4), rp = rsrc(a.tok_pos, uint32_t(a.M) * 4);
       int trow[FM][4], tpos[FM][4];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t m = uint32_t(m0 + 16 * i + 4 * lg + r);
-          trow[i][r] = bloadi(rr, 4 * m);
-          tpos[i][r] = bloadi(rp, 4 * m);
+          trow[i][r] = prm.tok_row[16 * i + 4 * lg + r];
+          tpos[i][r] = prm.tok_pos[16 * i + 4 * lg + r];
         }
       zero<FM>(acc);
       stage_mma<FM>(acc, panel, cur, nx, lane_o);
@@ -554,15 +636,32 @@ void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_
 }
 
 bool tail_supported(int d, int d_ff, int n_qkv) {
-  return d > 0 && d <= PANEL && d % 16 == 0 && d_ff > 0 && d_ff % 16 == 0 && n_qkv > 0 && n_qkv % 16 == 0;
+  return d > 0 && d <= PANEL && d % 16 == 0 && d_ff > 0 && d_ff % 16 == 0 && d_ff <= 4 * PANEL &&
+         n_qkv > 0 && n_qkv % 16 == 0 && n_qkv <= 3 * PANEL;
 }
 
 void launch_tail(const TailArgs &a, hipStream_t s) {
   CG_REQUIRE(tail_supported(a.d, a.d_ff, a.n_qkv), CG_ERR_UNSUPPORTED, "fused layer: unsupported shape");
   if (a.M <= 0) return;
-  // 16-row blocks: one per CU at the benchmark's 4096 tokens.
-  layer_tail_kernel<16><<<unsigned((a.M + 15) / 16), THREADS, 0, s>>>(a);
-  CG_LAUNCHED();
+  constexpr int BM = 16;  // 16-row blocks: one per CU at the benchmark's 4096 tokens
+  const int nc = (a.d_ff + PANEL - 1) / PANEL, nq = (a.n_qkv + PANEL - 1) / PANEL;
+  const int mode = !a.do_post ? 0 : (a.final_ln ? 2 : 1);
+  const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + 3 * BM * 4;
+  const unsigned grid = unsigned((a.M + BM - 1) / BM);
+  auto go = [&](auto kernel) {
+    kernel<<<grid, THREADS, dyn, s>>>(a);
+    CG_LAUNCHED();
+  };
+#define CG_TAIL_CASE(MODE, NC, NQ) \
+  if (mode == MODE && (MODE == 0 || nc == NC) && (MODE == 2 || nq == NQ)) return go(layer_tail_kernel<BM, MODE, NC, NQ>)
+  CG_TAIL_CASE(0, 1, 1); CG_TAIL_CASE(0, 1, 2); CG_TAIL_CASE(0, 1, 3);
+  CG_TAIL_CASE(1, 1, 1); CG_TAIL_CASE(1, 1, 2); CG_TAIL_CASE(1, 1, 3);
+  CG_TAIL_CASE(1, 2, 1); CG_TAIL_CASE(1, 2, 2); CG_TAIL_CASE(1, 2, 3);
+  CG_TAIL_CASE(1, 3, 1); CG_TAIL_CASE(1, 3, 2); CG_TAIL_CASE(1, 3, 3);
+  CG_TAIL_CASE(1, 4, 1); CG_TAIL_CASE(1, 4, 2); CG_TAIL_CASE(1, 4, 3);
+  CG_TAIL_CASE(2, 1, 1); CG_TAIL_CASE(2, 2, 1); CG_TAIL_CASE(2, 3, 1); CG_TAIL_CASE(2, 4, 1);
+#undef CG_TAIL_CASE
+  throw Error(CG_ERR_UNSUPPORTED, "fused layer: unsupported chunk counts");
 }
 
 }  // namespace cg
