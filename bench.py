@@ -49,6 +49,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-steps", type=int, default=4)
     p.add_argument("--ref-steps", type=int, default=8)
     p.add_argument("--no-baselines", action="store_true")
+    p.add_argument(
+        "--traffic-probe", action="store_true",
+        help="run only the decode-attention launches of the timed steps and a 256 MiB calibration copy "
+        "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), then exit",
+    )
     return p.parse_args()
 
 
@@ -150,9 +155,13 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     avg_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
     achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
+    # HBM bytes per launch from the committed counter passes (FETCH_SIZE / WRITE_SIZE,
+    # calibrated on a plain copy), valid when they were taken on this same workload.
     traffic = None
     if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
+        recorded = json.loads(TRAFFIC_FILE.read_text())
+        if abs(recorded.get("algorithmic_bytes_per_launch", 0) - bytes_per_launch) <= 0.01 * bytes_per_launch:
+            traffic = recorded.get("bytes_per_launch")
     return {
         "kernel": "decode_attention_tr_kernel<bf16,32,1>",
         "bound": "hbm",
@@ -167,8 +176,10 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     }
 
 
-def cpu_baseline(name: str, games: int, steps: int) -> dict:
-    """The oracle's reference path on the host cores, on `games` of the workload's games."""
+def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) -> dict:
+    """The oracle's reference path on the host cores, on `games` of the workload's games, at
+    steps first .. first + steps (the middle of the timed range: context lengths there are
+    the timed region's average)."""
 
     from card_playing_gym_amd.synthetic import WORKLOADS, Driver, build_model
     from oracle.reference_path import RefCache, RefSynthetic, ref_config_of
@@ -181,8 +192,10 @@ def cpu_baseline(name: str, games: int, steps: int) -> dict:
     state = {k: v.detach() for k, v in model.state_dict().items()}
     ref = RefSynthetic(state, ref_config_of(config), w.precision)
     small = type(w)(**{**w.__dict__, "games": games})
-    driver = Driver(small, seed=0, max_len=w.max_len(steps + 1))
+    driver = Driver(small, seed=0, max_len=w.max_len(horizon))
     max_len = driver.max_len
+    for _ in range(first - 1):  # advance the host state (lengths) to the sampled steps
+        driver.step()
     cache = RefCache(config.n_layers, config.n_kv_heads, config.head_dim, games, max_len, w.kv_dtype)
     times = []
     with torch.no_grad():
@@ -204,13 +217,16 @@ def cpu_baseline(name: str, games: int, steps: int) -> dict:
         "cores": cores,
         "kind": "port",
         "sample": f"{name} restated reference path (eager PyTorch CPU, {w.precision} rounding, {w.kv_dtype} KV): "
-        f"{games} of the {w.games} games, 1 untimed + {steps} timed steps, "
-        f"{per_step * 1e3:.0f} ms/step",
+        f"{games} of the {w.games} games, 1 untimed + {steps} timed steps from step {first} (the middle of "
+        f"the GPU's timed range), {per_step * 1e3:.0f} ms/step",
     }
 
 
-def reference_gpu(bench: Bench, steps: int) -> dict:
-    """The restated reference path on the MI355X: eager, and one step captured in a graph."""
+def reference_gpu(bench: Bench, steps: int, first: int) -> dict:
+    """The restated reference path on the MI355X, eager and captured in a graph, on steps
+    first .. first + steps - 1 (the middle of the timed range).  span is what the
+    reference's collector passes: the longest row after the append, rounded up to 32
+    (cardgym/rl/continuous.py:338), one value for the sampled steps (one graph shape)."""
 
     from oracle.reference_path import RefCache, RefSynthetic, ref_config_of
 
@@ -223,7 +239,8 @@ def reference_gpu(bench: Bench, steps: int) -> dict:
     tok = torch.zeros((bench.games, 1, 1), dtype=torch.int64, device=dev)
     pos = torch.zeros(bench.games, dtype=torch.int64, device=dev)
     rows = torch.arange(bench.games, dtype=torch.int64, device=dev)
-    span = min(int(-(-(bench.plans[0].positions.max() + steps + 2) // 32) * 32), bench.max_len)
+    last = max(int(bench.plans[s].positions.max()) for s in range(first, first + steps))
+    span = min(int(-(-(last + 1) // 32) * 32), bench.max_len)
 
     def body():
         hidden = ref.forward_ragged(tok, pos, cache, bench.readout, span=span, rows=rows if bench.gathered else None)
@@ -236,11 +253,11 @@ def reference_gpu(bench: Bench, steps: int) -> dict:
 
     result = {}
     with torch.no_grad():
-        load(0)
+        load(first)
         body()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for s in range(steps):
+        for s in range(first, first + steps):
             load(s)
             body()
         torch.cuda.synchronize()
@@ -256,14 +273,14 @@ def reference_gpu(bench: Bench, steps: int) -> dict:
             body()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for s in range(steps):
+        for s in range(first, first + steps):
             load(s)
             graph.replay()
         torch.cuda.synchronize()
         graphed = (time.perf_counter() - t0) / steps
         result["graph_game_tokens_per_s"] = round(bench.games / graphed, 1)
         result["span"] = span
-        result["steps"] = steps
+        result["steps"] = f"{first}..{first + steps - 1}"
     del cache
     torch.cuda.empty_cache()
     return result
@@ -285,6 +302,21 @@ def main() -> int:
     log(f"bench: setting up {args.workload} ({args.warmup} warmup + {args.steps} timed steps)")
     bench = Bench(args.workload, args.steps, args.warmup)
     w = bench.workload
+    if args.traffic_probe:
+        # Counter passes read per-dispatch HBM traffic: the attention launches of the timed
+        # steps (as the roofline replays them) and a plain device copy of known size, whose
+        # reading calibrates the counters.
+        with torch.no_grad():
+            roof = attention_roofline(bench, args.warmup, args.steps)
+            src = torch.ones(256 << 20, dtype=torch.uint8, device=bench.device)
+            dst = torch.empty_like(src)
+            for _ in range(4):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+        print(json.dumps({"probe": "traffic", "kernel": roof["kernel"], "launches": roof["launches"],
+                          "algorithmic_bytes_per_launch": roof["algorithmic_bytes_per_launch"],
+                          "copy_bytes": src.numel(), "copy_launches": 4}), flush=True)
+        return 0
     with torch.no_grad():
         bench.load(0)
         bench.capture()
@@ -312,13 +344,14 @@ def main() -> int:
     extra = {}
     cpu = None
     if not args.no_baselines:
-        extra["reference_gpu"] = reference_gpu(bench, args.ref_steps)
+        middle = args.warmup + args.steps // 2 - args.ref_steps // 2
+        extra["reference_gpu"] = reference_gpu(bench, args.ref_steps, middle)
         best = max(extra["reference_gpu"]["eager_game_tokens_per_s"], extra["reference_gpu"]["graph_game_tokens_per_s"])
         extra["reference_gpu"]["speedup_vs_best"] = round(value / best, 2)
         log(f"bench: reference path on the GPU {extra['reference_gpu']}")
         del bench.cache
         torch.cuda.empty_cache()
-        cpu = cpu_baseline(args.workload, args.cpu_games, args.cpu_steps)
+        cpu = cpu_baseline(args.workload, args.cpu_games, args.cpu_steps, middle, args.warmup + args.steps)
         log(f"bench: cpu baseline {cpu}")
     result = {
         "metric": "game-tokens/sec at 4096 games; decode-attn HBM GB/s vs peak",

@@ -649,10 +649,10 @@ __device__ __forceinline__ int row16_min(int v) {
 
 // SPLIT waves share one (sequence, KV head): wave p of the unit takes tiles p, p + SPLIT,
 // ...; their partial (max, sum, O) merge in LDS at the end (SPLIT 1: four units per block).
-template <typename TKV, int D, int NQT, int SPLIT>
+template <typename TKV, int D, int NQT, int SPLIT, int KT>
 __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
   static_assert(SPLIT == 1 || SPLIT == 4, "a block holds 4 / SPLIT whole units");
-  constexpr int KT = 64;          // keys per tile
+  static_assert(KT % 32 == 0, "key tiles are whole 32-key MFMA steps");
   constexpr int NJ = KT / 16;     // 16-key score tiles per key tile
   constexpr int DK = D / 32;      // 32-dim slices of a key (S^T k-steps)
   constexpr int DH = D / 16;      // 16-dim slices of the output (O^T row tiles)
@@ -903,6 +903,9 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
 #ifndef TR_SPLIT
 #define TR_SPLIT 4
 #endif
+#ifndef TR_KT
+#define TR_KT 64
+#endif
 
 template <typename TKV, int D>
 void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
@@ -911,9 +914,10 @@ void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
     CG_REQUIRE(int64_t(a.max_len) * D * 2 < (int64_t(1) << 31), CG_ERR_UNSUPPORTED,
                "decode attention: one cache row of one head must stay below 2 GiB");
     const unsigned units = unsigned(int64_t(a.n_seqs) * a.kv_heads);
-    if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT><<<(units * TR_SPLIT + 3) / 4, 256, 0, s>>>(a);
-    else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT><<<(units * TR_SPLIT + 3) / 4, 256, 0, s>>>(a);
-    else decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT><<<(units * TR_SPLIT + 3) / 4, 256, 0, s>>>(a);
+    const unsigned tr_grid = (units * TR_SPLIT + 3) / 4;
+    if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT, TR_KT><<<tr_grid, 256, 0, s>>>(a);
+    else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT, TR_KT><<<tr_grid, 256, 0, s>>>(a);
+    else decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64><<<tr_grid, 256, 0, s>>>(a);
   } else {
     if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
     else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);

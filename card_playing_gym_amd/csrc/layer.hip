@@ -21,8 +21,8 @@
 // (weights) streams from L2 straight into each wave's registers: lane l loads 16 bytes of
 // W row (col 16 j + l % 16) at k = 32 ks + 8 (l / 16), exactly the
 // v_mfma_f32_16x16x32_bf16 B-fragment, so weights never touch LDS.  Each fragment
-// register is refilled with stage s+1's fragment right after its MFMAs of stage s, which
-// keeps a whole stage of weights (128 KB per block) in flight.  Row statistics of the
+// register is refilled with stage s+2's fragment right after its MFMAs of stage s, which
+// keeps up to two stages of weights (256 KB per block) in flight.  Row statistics of the
 // LayerNorms reduce over the 16 lanes of a fragment row with shuffles, then over the
 // eight waves in LDS.
 #include "common.h"
@@ -167,23 +167,28 @@ __device__ __forceinline__ void load_slice(uint4 (&buf)[KS][FN], const Slice &s,
 // MFMAs read.
 template <int FM>
 __device__ __forceinline__ void stage_mma(f32x4 (&acc)[FM][FN], const unsigned char *lds,
-                                          uint4 (&w)[KS][FN], const Slice &next, int lane) {
+                                          uint4 (&w)[KS][FN], const Slice &next, bool refill, int lane) {
   const int li = lane & 15, lg = lane >> 4;
+  // The stage's A fragments are read up front: one LDS round trip instead of one per k-step.
+  uint4 af[KS][FM];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[ks][i] = *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
   uint32_t base[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) base[j] = slice_base(next, j, lane);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    uint4 af[FM];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[i] = *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[i], w[ks][j], acc[i][j]);
+      for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[ks][i], w[ks][j], acc[i][j]);
+    if (refill) {
 #pragma unroll
-    for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+      for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+    }
   }
 }
 
@@ -364,8 +369,11 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   p.S = S;
   const uint32_t xbytes = uint32_t(a.M) * uint32_t(d) * 4;
 
-  uint4 cur[KS][FN];
-  if (p.S > 0) load_slice(cur, stage_slice(a, p, 0, cw), lane);
+  // Two stages of weights in flight: stage s computes from wbuf[s & 1] and refills it with
+  // stage s + 2's fragments (the stage sequence is unrolled, so the index is static).
+  uint4 wbuf[2][KS][FN];
+  if (S > 0) load_slice(wbuf[0], stage_slice(a, p, 0, cw), lane);
+  if (S > 1) load_slice(wbuf[1], stage_slice(a, p, 1, cw), lane);
 
   Params prm;
   prm.b_up = dyn;
@@ -445,8 +453,9 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
     const int li = lane_o & 15, lg = lane_o >> 4;
     int c;
     const int kind = stage_kind(p, s, c);
-    // The last stage re-reads its own (in-range) slice: the refill stays unconditional.
-    const Slice nx = stage_slice(a, p, s + 1 < p.S ? s + 1 : s, cw);
+    const bool refill = s + 2 < S;
+    const Slice nx = stage_slice(a, p, refill ? s + 2 : s, cw);
+    uint4(&cur)[KS][FN] = wbuf[s & 1];
     if (kind == ST_OUT) {
       // ---- out-proj + residual, then LN(ln_mlp) -> panel
       const Rsrc rs = rsrc(opaque_ptr(a.x_src), xbytes);
@@ -465,7 +474,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
       // order, so the epilogue then waits only for them, not for the next stage's weights.
       __builtin_amdgcn_sched_barrier(0);
       zero<FM>(acc);
-      stage_mma<FM>(acc, panel, cur, nx, lane_o);
+      stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -505,7 +514,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
         bias[j] = n < a.d_ff ? prm.b_up[n] : 0.f;
       }
       zero<FM>(acc);
-      stage_mma<FM>(acc, panel, cur, nx, lane_o);
+      stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
       unsigned char *hb = hbuf[c & 1];
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
@@ -545,7 +554,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // residual loads ahead of the weight refills
-      stage_mma<FM>(accd, hbuf[c & 1], cur, nx, lane_o);
+      stage_mma<FM>(accd, hbuf[c & 1], cur, nx, refill, lane_o);
       if (last) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -576,7 +585,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
           tpos[i][r] = prm.tok_pos[16 * i + 4 * lg + r];
         }
       zero<FM>(acc);
-      stage_mma<FM>(acc, panel, cur, nx, lane_o);
+      stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
       const int kvw = a.kv_heads * a.head_dim;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
