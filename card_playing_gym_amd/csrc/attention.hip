@@ -607,8 +607,12 @@ typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 __device__ __forceinline__ Rsrc make_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, int(bytes), 0x00020000);
 }
+// Cache policy of the K / V stream loads (buffer instruction bits: 1 sc0, 2 nt, 16 sc1).
+#ifndef CG_KV_CPOL
+#define CG_KV_CPOL 2
+#endif
 __device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t off) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CG_KV_CPOL);
   return uint4{v[0], v[1], v[2], v[3]};
 }
 __device__ __forceinline__ float xor16_max(float v) {
