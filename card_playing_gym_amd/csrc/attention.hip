@@ -653,8 +653,12 @@ __device__ __forceinline__ int row16_min(int v) {
 
 // SPLIT waves share one (sequence, KV head): wave p of the unit takes tiles p, p + SPLIT,
 // ...; their partial (max, sum, O) merge in LDS at the end (SPLIT 1: four units per block).
-template <typename TKV, int D, int NQT, int SPLIT, int KT>
-__global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
+#ifndef TR_WAVES_PER_EU
+#define TR_WAVES_PER_EU 4
+#endif
+template <typename TKV, int D, int NQT, int SPLIT, int KT, int DEPTH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NQT == 1 && D == 32 ? TR_WAVES_PER_EU : 1)))
+void decode_attention_tr_kernel(AttnArgs a) {
   static_assert(SPLIT == 1 || SPLIT == 4, "a block holds 4 / SPLIT whole units");
   static_assert(KT % 32 == 0, "key tiles are whole 32-key MFMA steps");
   constexpr int NJ = KT / 16;     // 16-key score tiles per key tile
@@ -699,26 +703,78 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
 
   const int nq = int(count) * G;
   for (int qg = 0; qg < nq; qg += NQT * 16) {
-    // ---- queries of this group: column li of tile qt is query qg + 16 qt + li ----------
+    // ---- key limits of this group's queries (column li of tile qt is query qg + 16 qt + li)
     int lim[NQT];
-    typename Mfma16<TKV>::vec qv[NQT][DK];
     int kmax = 0, kmin = 0x7fffffff;
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
       const int m = qg + 16 * qt + li;
-      f32x8 f[DK];
       int l = 0;
       if (m < nq) {
-        const int t = m / G, g = m % G;
-        const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st;
-#pragma unroll
-        for (int dk = 0; dk < DK; ++dk)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[dk][e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e) * a.scale_log2;
-        int64_t lim64 = kl + t;
+        int64_t lim64 = kl + m / G;
         if (lim64 > a.span) lim64 = a.span;
         l = (row_ok && lim64 > 0) ? int(lim64) : 0;
         kmin = min(kmin, l);
+      }
+      lim[qt] = l;
+      kmax = max(kmax, l);
+    }
+    // Uniform bounds: keys below kmin are visible to every query, none at or past kend.
+    const int kend = __builtin_amdgcn_readfirstlane(row16_max(kmax));
+    const int kfull = __builtin_amdgcn_readfirstlane(row16_min(kmin));
+
+    // Lane l holds key 16 j + l % 16 of a tile at dims 32 dk + 8 (l / 16), for K and V.
+    uint4 kr[DEPTH][NJ][DK], vr[DEPTH][NJ][DK];
+    auto fetch = [&](int st, int kb) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int key = min(kb + 16 * j + li, kend - 1);
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
+          kr[st][j][dk] = bload16(kres, off);
+          vr[st][j][dk] = bload16(vres, off);
+        }
+      }
+    };
+    // The first DEPTH key tiles are requested before the queries, so the latencies overlap.
+    if (part * KT < kend) {
+#pragma unroll
+      for (int st = 0; st < DEPTH; ++st) fetch(st, part * KT + st * SPLIT * KT);
+    }
+
+    // ---- queries (scaled by softmax scale * log2 e); fp32 rows at 16-byte alignment load as
+    //      two float4 per 8 dims -------------------------------------------------------------
+    const bool q4 = a.q_dtype == CG_F32 &&
+                    ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 3) | (a.q_sh & 3) | (a.q_st & 3) | (q_base & 3)) == 0;
+    typename Mfma16<TKV>::vec qv[NQT][DK];
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      const int m = qg + 16 * qt + li;
+      f32x8 f[DK];
+      if (m < nq) {
+        const int t = m / G, g = m % G;
+        const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st;
+        if (q4) {
+#pragma unroll
+          for (int dk = 0; dk < DK; ++dk) {
+            const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.q) + qo + 32 * dk + 8 * lg);
+            const float4 x0 = src[0], x1 = src[1];
+            f[dk][0] = x0.x * a.scale_log2;
+            f[dk][1] = x0.y * a.scale_log2;
+            f[dk][2] = x0.z * a.scale_log2;
+            f[dk][3] = x0.w * a.scale_log2;
+            f[dk][4] = x1.x * a.scale_log2;
+            f[dk][5] = x1.y * a.scale_log2;
+            f[dk][6] = x1.z * a.scale_log2;
+            f[dk][7] = x1.w * a.scale_log2;
+          }
+        } else {
+#pragma unroll
+          for (int dk = 0; dk < DK; ++dk)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[dk][e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e) * a.scale_log2;
+        }
       } else {
 #pragma unroll
         for (int dk = 0; dk < DK; ++dk)
@@ -727,12 +783,7 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int dk = 0; dk < DK; ++dk) qv[qt][dk] = Mfma16<TKV>::from(f[dk]);
-      lim[qt] = l;
-      kmax = max(kmax, l);
     }
-    // Uniform bounds: keys below kmin are visible to every query, none at or past kend.
-    const int kend = __builtin_amdgcn_readfirstlane(row16_max(kmax));
-    const int kfull = __builtin_amdgcn_readfirstlane(row16_min(kmin));
 
     f32x4 acc[NQT][DH];
     float mrun[NQT], lsum[NQT];
@@ -744,22 +795,11 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
       for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Lane l holds key 16 j + l % 16 of a tile at dims 32 dk + 8 (l / 16), for K and V.
-    uint4 kr[NJ][DK], vr[NJ][DK];
-    auto fetch = [&](int kb) {
+    for (int kb0 = part * KT; kb0 < kend; kb0 += DEPTH * SPLIT * KT) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int key = min(kb + 16 * j + li, kend - 1);
-#pragma unroll
-        for (int dk = 0; dk < DK; ++dk) {
-          const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
-          kr[j][dk] = bload16(kres, off);
-          vr[j][dk] = bload16(vres, off);
-        }
-      }
-    };
-    if (part * KT < kend) fetch(part * KT);
-    for (int kb = part * KT; kb < kend; kb += SPLIT * KT) {
+     for (int st = 0; st < DEPTH; ++st) {
+      const int kb = kb0 + st * SPLIT * KT;
+      if (st > 0 && kb >= kend) break;
       // ---- scores S^T[key, query] -----------------------------------------------------
       f32x4 sc[NQT][NJ];
 #pragma unroll
@@ -770,7 +810,7 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
 #pragma unroll
           for (int dk = 0; dk < DK; ++dk) {
             typename Mfma16<TKV>::vec kvec;
-            __builtin_memcpy(&kvec, &kr[j][dk], 16);
+            __builtin_memcpy(&kvec, &kr[st][j][dk], 16);
             s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
           }
           sc[qt][j] = s4;
@@ -781,10 +821,10 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
 #pragma unroll
         for (int dk = 0; dk < DK; ++dk) {
           unsigned char *dst = vt + (16 * j + li) * ROW + (32 * dk + 8 * lg) * 2;
-          reinterpret_cast<uint2 *>(dst)[0] = uint2{vr[j][dk].x, vr[j][dk].y};
-          reinterpret_cast<uint2 *>(dst)[1] = uint2{vr[j][dk].z, vr[j][dk].w};
+          reinterpret_cast<uint2 *>(dst)[0] = uint2{vr[st][j][dk].x, vr[st][j][dk].y};
+          reinterpret_cast<uint2 *>(dst)[1] = uint2{vr[st][j][dk].z, vr[st][j][dk].w};
         }
-      fetch(kb + SPLIT * KT);  // clamped: past kend it re-reads the last visible key
+      fetch(st, kb + DEPTH * SPLIT * KT);  // clamped: past kend it re-reads the last visible key
 
       // ---- mask (only tiles reaching past some query's limit) --------------------------
       if (kb + KT > kfull) {
@@ -850,6 +890,7 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
           for (int qt = 0; qt < NQT; ++qt) acc[qt][dh] = Mfma16<TKV>::mma(vv, pv[qt], acc[qt][dh]);
         }
       }
+     }
     }
 
     if constexpr (SPLIT > 1) {
@@ -910,6 +951,9 @@ __global__ __launch_bounds__(256) void decode_attention_tr_kernel(AttnArgs a) {
 #ifndef TR_KT
 #define TR_KT 64
 #endif
+#ifndef TR_DEPTH
+#define TR_DEPTH 1
+#endif
 
 template <typename TKV, int D>
 void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
@@ -919,9 +963,9 @@ void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
                "decode attention: one cache row of one head must stay below 2 GiB");
     const unsigned units = unsigned(int64_t(a.n_seqs) * a.kv_heads);
     const unsigned tr_grid = (units * TR_SPLIT + 3) / 4;
-    if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT, TR_KT><<<tr_grid, 256, 0, s>>>(a);
-    else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT, TR_KT><<<tr_grid, 256, 0, s>>>(a);
-    else decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64><<<tr_grid, 256, 0, s>>>(a);
+    if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT, TR_KT, TR_DEPTH><<<tr_grid, 256, 0, s>>>(a);
+    else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT, TR_KT, TR_DEPTH><<<tr_grid, 256, 0, s>>>(a);
+    else decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1><<<tr_grid, 256, 0, s>>>(a);
   } else {
     if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
     else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);
