@@ -39,14 +39,11 @@ __device__ __forceinline__ float from_f32<float>(float v) {
 }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
-  uint32_t u = __float_as_uint(v);
+  // v_cvt_pk_bf16_f32 rounds to nearest even (denormals kept); NaN is canonicalised to
+  // 0x7fc0, the quiet NaN torch's conversion produces.
+  const __bf16 h = __bf16(v);
   bf16 r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    r.bits = 0x7fc0;
-  } else {
-    u += 0x7fffu + ((u >> 16) & 1u);
-    r.bits = uint16_t(u >> 16);
-  }
+  r.bits = v != v ? uint16_t(0x7fc0) : __builtin_bit_cast(uint16_t, h);
   return r;
 }
 template <>

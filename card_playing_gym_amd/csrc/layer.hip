@@ -40,6 +40,10 @@ constexpr int WAVES = 8;              // waves per block; each owns 32 columns o
 constexpr int FN = 2;                 // 16-column fragments per wave and stage
 constexpr int THREADS = 64 * WAVES;
 constexpr int KS = PANEL / 32;        // 32-wide k-steps per stage
+#ifndef TAIL_RING
+#define TAIL_RING 2
+#endif
+constexpr int RING = TAIL_RING;       // stages of weights in flight per wave
 
 enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
 
@@ -62,9 +66,21 @@ __device__ __forceinline__ float bloadf(Rsrc r, uint32_t off) {
 __device__ __forceinline__ int bloadi(Rsrc r, uint32_t off) {
   return int(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
+// Results (residual rows, queries, appended keys / values, hidden rows) are written with
+// the non-temporal policy: left dirty in L2 they are written back while the next layer's
+// attention streams the pool, which slowed it by ~10 %.
+#ifndef TAIL_NT_STORE
+#define TAIL_NT_STORE 1
+#endif
 template <typename T>
 __device__ __forceinline__ void gst(T *p, T v) {
-  *p = v;
+  if constexpr (TAIL_NT_STORE && sizeof(T) == 4) {
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, v), reinterpret_cast<uint32_t *>(p));
+  } else if constexpr (TAIL_NT_STORE && sizeof(T) == 2) {
+    __builtin_nontemporal_store(__builtin_bit_cast(uint16_t, v), reinterpret_cast<uint16_t *>(p));
+  } else {
+    *p = v;
+  }
 }
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for
@@ -369,11 +385,45 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   p.S = S;
   const uint32_t xbytes = uint32_t(a.M) * uint32_t(d) * 4;
 
-  // Two stages of weights in flight: stage s computes from wbuf[s & 1] and refills it with
-  // stage s + 2's fragments (the stage sequence is unrolled, so the index is static).
-  uint4 wbuf[2][KS][FN];
-  if (S > 0) load_slice(wbuf[0], stage_slice(a, p, 0, cw), lane);
-  if (S > 1) load_slice(wbuf[1], stage_slice(a, p, 1, cw), lane);
+  // Prologue loads, issued before the weight stream (loads complete in order, so anything
+  // issued after the ring's 32 fragment loads per lane would wait for them): this block's
+  // attention rows (one 16-byte chunk per thread) and the per-layer vectors.
+  static_assert(BM * (PANEL / 8) <= THREADS, "one attention chunk per thread");
+  const int m0_ = blockIdx.x * BM;
+  const int cpr = d / 8;
+  uint4 arow = {0u, 0u, 0u, 0u};
+  if (POST && tid < BM * cpr) {
+    const Rsrc ra = rsrc(a.attn, uint32_t(a.M) * uint32_t(d) * 2);
+    arow = bload16(ra, (uint32_t(m0_ + tid / cpr) * d + 8 * (tid % cpr)) * 2);
+  }
+  constexpr int NB_UP = (4 * PANEL + THREADS - 1) / THREADS;
+  float v_up[NB_UP], v_vec[5];
+  int v_tok[3];
+#pragma unroll
+  for (int k = 0; k < NB_UP; ++k) {
+    const int i = tid + k * THREADS;
+    v_up[k] = POST && i < a.d_ff ? a.b_up[i] : 0.f;
+  }
+  {
+    const bool in = tid < d;
+    v_vec[0] = POST && in ? a.b_down[tid] : 0.f;
+    v_vec[1] = POST && in ? a.ln2_w[tid] : 0.f;
+    v_vec[2] = POST && in ? a.ln2_b[tid] : 0.f;
+    v_vec[3] = in ? a.ln_w[tid] : 0.f;
+    v_vec[4] = in ? a.ln_b[tid] : 0.f;
+    const bool tin = tid < BM && m0_ + tid < a.M;
+    v_tok[0] = tin && !a.final_ln ? a.tok_row[m0_ + tid] : -1;
+    v_tok[1] = tin && !a.final_ln ? a.tok_pos[m0_ + tid] : 0;
+    v_tok[2] = tin && a.final_ln ? a.tok_out[m0_ + tid] : -1;
+  }
+
+  // RING stages of weights in flight: stage s computes from wbuf[s % RING] and refills it
+  // with stage s + RING's fragments (the stage sequence is unrolled, so the index is
+  // static), so the weight stream keeps running through the epilogues' barriers.
+  uint4 wbuf[RING][KS][FN];
+#pragma unroll
+  for (int r = 0; r < RING; ++r)
+    if (S > r) load_slice(wbuf[r], stage_slice(a, p, r, cw), lane);
 
   Params prm;
   prm.b_up = dyn;
@@ -385,24 +435,6 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   prm.tok_row = reinterpret_cast<int *>(prm.ln_b + PANEL);
   prm.tok_pos = prm.tok_row + BM;
   prm.tok_out = prm.tok_pos + BM;
-  {
-    const int m0 = blockIdx.x * BM;
-    for (int i = tid; i < a.d_ff; i += THREADS) prm.b_up[i] = a.do_post ? a.b_up[i] : 0.f;
-    for (int i = tid; i < PANEL; i += THREADS) {
-      const bool in = i < d;
-      prm.b_down[i] = in && a.do_post ? a.b_down[i] : 0.f;
-      prm.ln2_w[i] = in && a.do_post ? a.ln2_w[i] : 0.f;
-      prm.ln2_b[i] = in && a.do_post ? a.ln2_b[i] : 0.f;
-      prm.ln_w[i] = in ? a.ln_w[i] : 0.f;
-      prm.ln_b[i] = in ? a.ln_b[i] : 0.f;
-    }
-    for (int i = tid; i < BM; i += THREADS) {
-      const bool in = m0 + i < a.M;
-      prm.tok_row[i] = in && !a.final_ln ? a.tok_row[m0 + i] : -1;
-      prm.tok_pos[i] = in && !a.final_ln ? a.tok_pos[m0 + i] : 0;
-      prm.tok_out[i] = in && a.final_ln ? a.tok_out[m0 + i] : -1;
-    }
-  }
 
   // Zero the LDS panels once: padding columns (k >= d, or past d_ff) stay zero.
   for (int o = tid * 16; o < BM * ROWB; o += THREADS * 16) {
@@ -411,6 +443,23 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
     *reinterpret_cast<uint4 *>(hbuf[0] + o) = z;
     *reinterpret_cast<uint4 *>(hbuf[1] + o) = z;
   }
+#pragma unroll
+  for (int k = 0; k < NB_UP; ++k) {
+    const int i = tid + k * THREADS;
+    if (i < a.d_ff) prm.b_up[i] = v_up[k];
+  }
+  if (tid < PANEL) {
+    prm.b_down[tid] = v_vec[0];
+    prm.ln2_w[tid] = v_vec[1];
+    prm.ln2_b[tid] = v_vec[2];
+    prm.ln_w[tid] = v_vec[3];
+    prm.ln_b[tid] = v_vec[4];
+  }
+  if (tid < BM) {
+    prm.tok_row[tid] = v_tok[0];
+    prm.tok_pos[tid] = v_tok[1];
+    prm.tok_out[tid] = v_tok[2];
+  }
   lds_barrier();
 
   f32x4 acc[FM][FN], accd[FM][FN];
@@ -418,14 +467,9 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   {
     const int m0 = blockIdx.x * BM;
     const int li = lane & 15, lg = lane >> 4;
-    if (a.do_post) {
-      // Attention rows of this block -> panel (16-byte chunks; rows past M read as 0).
-      const int cpr = d / 8;
-      const Rsrc ra = rsrc(a.attn, uint32_t(a.M) * uint32_t(d) * 2);
-      for (int idx = tid; idx < BM * cpr; idx += THREADS) {
-        const int r = idx / cpr, c = idx % cpr;
-        *reinterpret_cast<uint4 *>(panel + r * ROWB + 16 * c) = bload16(ra, (uint32_t(m0 + r) * d + 8 * c) * 2);
-      }
+    if (POST) {
+      // Attention rows of this block -> panel (rows past M read as 0).
+      if (tid < BM * cpr) *reinterpret_cast<uint4 *>(panel + (tid / cpr) * ROWB + 16 * (tid % cpr)) = arow;
       lds_barrier();
     } else {
       // First block's prologue: the conditioned input is the residual stream.
@@ -453,9 +497,9 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
     const int li = lane_o & 15, lg = lane_o >> 4;
     int c;
     const int kind = stage_kind(p, s, c);
-    const bool refill = s + 2 < S;
-    const Slice nx = stage_slice(a, p, refill ? s + 2 : s, cw);
-    uint4(&cur)[KS][FN] = wbuf[s & 1];
+    const bool refill = s + RING < S;
+    const Slice nx = stage_slice(a, p, refill ? s + RING : s, cw);
+    uint4(&cur)[KS][FN] = wbuf[s % RING];
     if (kind == ST_OUT) {
       // ---- out-proj + residual, then LN(ln_mlp) -> panel
       const Rsrc rs = rsrc(opaque_ptr(a.x_src), xbytes);
@@ -586,28 +630,36 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
         }
       zero<FM>(acc);
       stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
+      // Per output column: its role (q / k / v / none) and, for k and v, the offset of its
+      // (head, dim) inside a pool slot row; per token row: the slot's base offset.
       const int kvw = a.kv_heads * a.head_dim;
+      int role[FN], col[FN];
+      int64_t coff[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = PANEL * c + cw + 16 * j + li;
+        role[j] = n >= a.n_qkv ? -1 : (n < a.q_cols ? 0 : (n < a.q_cols + kvw ? 1 : 2));
+        const int kvc = n - a.q_cols - (role[j] == 2 ? kvw : 0);
+        const int h = kvc / a.head_dim;
+        col[j] = role[j] == 0 ? n : kvc;
+        coff[j] = int64_t(h) * a.max_len * a.head_dim + (kvc - h * a.head_dim);
+      }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + 16 * i + 4 * lg + r;
           if (m >= a.M) continue;
+          const int64_t slot = (int64_t(trow[i][r]) * a.kv_heads * a.max_len + tpos[i][r]) * a.head_dim;
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
-            const int n = PANEL * c + cw + 16 * j + li;
-            if (n >= a.n_qkv) continue;
             const float v = acc[i][j][r];
-            if (n < a.q_cols) {
-              gst(a.q + int64_t(m) * a.q_cols + n, v);
-            } else if (trow[i][r] >= 0) {
-              const bool is_v = n >= a.q_cols + kvw;
-              const int kvc = n - a.q_cols - (is_v ? kvw : 0);
-              const int h = kvc / a.head_dim, dd = kvc % a.head_dim;
+            if (role[j] == 0) {
+              gst(a.q + int64_t(m) * a.q_cols + col[j], v);
+            } else if (role[j] > 0 && trow[i][r] >= 0) {
               float val = v;
-              if (is_v && a.vemb_off >= 0) val += a.vemb[int64_t(m) * a.ld_vemb + a.vemb_off + kvc];
-              const int64_t dst = ((int64_t(trow[i][r]) * a.kv_heads + h) * a.max_len + tpos[i][r]) * a.head_dim + dd;
-              store_kv(is_v ? a.vc : a.kc, a.kv_dtype, dst, val);
+              if (role[j] == 2 && a.vemb_off >= 0) val += a.vemb[int64_t(m) * a.ld_vemb + a.vemb_off + col[j]];
+              store_kv(role[j] == 2 ? a.vc : a.kc, a.kv_dtype, slot + coff[j], val);
             }
           }
         }
