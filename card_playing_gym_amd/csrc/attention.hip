@@ -929,6 +929,8 @@ void decode_attention_tr_kernel(AttnArgs a) {
       if (part != 0) continue;
     }
     // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
+    const bool o4 = a.out_dtype == (sizeof(TKV) == 2 && std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16) &&
+                    ((reinterpret_cast<uintptr_t>(a.out) & 7) | (a.o_sb & 3) | (a.o_sh & 3) | (a.o_st & 3) | (o_base & 3)) == 0;
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
       const float total = SPLIT > 1 ? lsum[qt] : xor32_sum(xor16_sum(lsum[qt]));
@@ -937,10 +939,23 @@ void decode_attention_tr_kernel(AttnArgs a) {
       const int t = m / G, g = m % G;
       const float inv = total > 0.f ? 1.0f / total : 0.f;
       const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st;
+      if (o4) {
+        // 16-bit output: each lane's 4 consecutive dims as one 8-byte non-temporal store (a
+        // dirty line left in L2 is written back while the next kernel streams).
 #pragma unroll
-      for (int dh = 0; dh < DH; ++dh)
+        for (int dh = 0; dh < DH; ++dh) {
+          const TKV e0 = from_f32<TKV>(acc[qt][dh][0] * inv), e1 = from_f32<TKV>(acc[qt][dh][1] * inv);
+          const TKV e2 = from_f32<TKV>(acc[qt][dh][2] * inv), e3 = from_f32<TKV>(acc[qt][dh][3] * inv);
+          const uint64_t packed = uint64_t(e0.bits) | uint64_t(e1.bits) << 16 | uint64_t(e2.bits) << 32 |
+                                  uint64_t(e3.bits) << 48;
+          __builtin_nontemporal_store(packed, reinterpret_cast<uint64_t *>(static_cast<TKV *>(a.out) + oo + 16 * dh + 4 * lg));
+        }
+      } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[qt][dh][i] * inv);
+        for (int dh = 0; dh < DH; ++dh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[qt][dh][i] * inv);
+      }
     }
   }
 }
