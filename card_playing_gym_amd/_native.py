@@ -65,6 +65,15 @@ class TrunkConfig(ctypes.Structure):
     ]
 
 
+class HeadsConfig(ctypes.Structure):
+    _fields_ = [
+        ("d_model", c_int32),
+        ("n_policy", c_int32),
+        ("d_mid", c_int32),
+        ("n_value", c_int32),
+    ]
+
+
 class LayerParams(ctypes.Structure):
     _fields_ = [
         ("ln_attn_w", c_void_p),
@@ -129,6 +138,12 @@ _SIGNATURES = {
         c_int32,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, c_int32, c_void_p],
     ),
+    "cg_heads_create": (
+        c_int32, [P(HeadsConfig), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)],
+    ),
+    "cg_heads_refresh": (c_int32, [c_void_p, c_void_p]),
+    "cg_heads_destroy": (c_int32, [c_void_p]),
+    "cg_heads_forward": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
     "cg_advance_positions": (c_int32, [c_void_p, c_int32, c_int64, c_void_p]),
 }
 

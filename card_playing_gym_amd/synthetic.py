@@ -13,6 +13,7 @@ games).  ``Workload.plan`` produces the per-step host descriptors deterministica
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass, field
 
@@ -65,7 +66,10 @@ class SyntheticModel(SequenceModel):
         return out.view(*tokens.shape[:-1], d), None, None
 
     def heads(self, hidden: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """Policy logits [B, vocab] and seat values [B, seats], fp32."""
+        """Policy logits [B, vocab] and seat values [B, seats], fp32.
+
+        Under bf16 autocast one fused launch (``cg_heads_forward``) with autocast's
+        rounding; otherwise three fp32 ``cg_linear`` products."""
 
         require_device(hidden)
         device = hidden.device
@@ -74,23 +78,88 @@ class SyntheticModel(SequenceModel):
         h = hidden.float().contiguous()
         m, d = h.shape
         logits = torch.empty((m, self.vocab), device=device, dtype=torch.float32)
+        first, last = self.value_head[0], self.value_head[2]
+        values = torch.empty((m, last.out_features), device=device, dtype=torch.float32)
+        if compute == nat.CG_BF16:
+            handle = self._native_heads(device)
+            nat.call("cg_heads_forward", handle.handle, h.data_ptr(), m, logits.data_ptr(), values.data_ptr(), stream)
+            return logits, values
         nat.call(
             "cg_linear", h.data_ptr(), _param(self.policy_head.weight).data_ptr(),
             _param(self.policy_head.bias).data_ptr(), logits.data_ptr(), m, self.vocab, d,
             nat.CG_ACT_NONE, compute, stream,
         )
-        first, last = self.value_head[0], self.value_head[2]
         mid = torch.empty((m, first.out_features), device=device, dtype=torch.float32)
         nat.call(
             "cg_linear", h.data_ptr(), _param(first.weight).data_ptr(), _param(first.bias).data_ptr(),
             mid.data_ptr(), m, first.out_features, d, nat.CG_ACT_GELU, compute, stream,
         )
-        values = torch.empty((m, last.out_features), device=device, dtype=torch.float32)
         nat.call(
             "cg_linear", mid.data_ptr(), _param(last.weight).data_ptr(), _param(last.bias).data_ptr(),
             values.data_ptr(), m, last.out_features, first.out_features, nat.CG_ACT_NONE, compute, stream,
         )
         return logits, values
+
+    def _head_tensors(self) -> list[torch.Tensor]:
+        first, last = self.value_head[0], self.value_head[2]
+        return [self.policy_head.weight, self.policy_head.bias, first.weight, first.bias, last.weight, last.bias]
+
+    def _native_heads(self, device: torch.device) -> "_NativeHeads":
+        key = device.index if device.index is not None else torch.cuda.current_device()
+        cache = self.__dict__.setdefault("_heads_cache", {})
+        entry = cache.get(key)
+        if entry is not None and entry.sync(self._head_tensors(), stream_handle(device)):
+            return entry
+        if entry is not None:
+            entry.close()
+        entry = _NativeHeads(self)
+        cache[key] = entry
+        return entry
+
+    def _apply(self, fn, *args, **kwargs):
+        # Moving or casting parameters invalidates the heads handles (they hold raw pointers).
+        for entry in self.__dict__.get("_heads_cache", {}).values():
+            entry.close()
+        self.__dict__["_heads_cache"] = {}
+        return super()._apply(fn, *args, **kwargs)
+
+
+class _NativeHeads:
+    """A ``cg_heads`` handle over the model's head parameters (bf16 fragment copies)."""
+
+    def __init__(self, model: SyntheticModel) -> None:
+        self.params = [_param(t) for t in model._head_tensors()]
+        self.signature = tuple(t.data_ptr() for t in self.params)
+        self.versions = tuple(t._version for t in self.params)
+        first, last = model.value_head[0], model.value_head[2]
+        cfg = nat.HeadsConfig(model.trunk_config.d_model, model.vocab, first.out_features, last.out_features)
+        handle = ctypes.c_void_p()
+        nat.call("cg_heads_create", ctypes.byref(cfg), *(t.data_ptr() for t in self.params), ctypes.byref(handle))
+        self.handle = handle
+
+    def sync(self, tensors: list[torch.Tensor], stream: int) -> bool:
+        """False when the parameters moved (rebuild); re-derives the copies after edits."""
+
+        if tuple(t.data_ptr() for t in tensors) != self.signature or any(a is not b for a, b in zip(tensors, self.params)):
+            return False
+        versions = tuple(t._version for t in self.params)
+        if versions != self.versions:
+            nat.call("cg_heads_refresh", self.handle, stream)
+            self.versions = versions
+        return True
+
+    def close(self) -> None:
+        if self.handle:
+            try:
+                nat.lib().cg_heads_destroy(self.handle)
+            finally:
+                self.handle = ctypes.c_void_p()
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def build_model(config: TrunkConfig, seed: int = 0, device: str | torch.device = "cpu") -> SyntheticModel:

@@ -230,6 +230,36 @@ int cg_linear(const float *x, const float *w, const float *bias, float *y, int32
 int cg_linear_add_scale(const float *x, const float *w, const float *addend, float *y, int32_t m,
                         int32_t n, int32_t k, float scale, int32_t compute_dtype, void *stream);
 
+/* ---- policy and value heads ------------------------------------------------------ */
+
+/* The heads a rollout wave evaluates at every readout row (cardgym/rl/graphs.py:88-104):
+ * policy logits nn.Linear(d_model, n_policy) and value_mlp(d_model, n_value) =
+ * Linear(d_model, d_mid) -> GELU -> Linear(d_mid, n_value) (cardgym/nn/model.py:12-17),
+ * in one launch with the rounding of bf16 autocast: operands rounded to bf16, fp32
+ * accumulation, every Linear output and the GELU output rounded to bf16.  Replaces the
+ * three autocast nn.Linear calls of SequenceModel's graphable heads.
+ * Shapes: d_model and d_mid multiples of 16 up to 256, n_policy a multiple of 16 up to
+ * 1024, 1 <= n_value <= 16.  Weights are fp32, row-major [out, in], read at create and
+ * refresh time only (the handle keeps bf16 copies in the kernel's fragment order). */
+typedef struct cg_heads cg_heads;
+
+typedef struct {
+  int32_t d_model, n_policy, d_mid, n_value;
+} cg_heads_config;
+
+int cg_heads_create(const cg_heads_config *config, const float *policy_w, const float *policy_b,
+                    const float *value_w1, const float *value_b1, const float *value_w2,
+                    const float *value_b2, cg_heads **out);
+
+/* Re-derives the bf16 weight copies after the fp32 weights changed (an optimiser step). */
+int cg_heads_refresh(cg_heads *heads, void *stream);
+
+int cg_heads_destroy(cg_heads *heads);
+
+/* logits fp32 [m, n_policy], values fp32 [m, n_value] from hidden fp32 [m, d_model]. */
+int cg_heads_forward(const cg_heads *heads, const float *hidden, int32_t m, float *logits,
+                     float *values, void *stream);
+
 /* Adds `delta` to every entry of the int64 array a (n entries): the synthetic driver's
  * "every game appended one token" position update, kept on the device. */
 int cg_advance_positions(int64_t *positions, int32_t n, int64_t delta, void *stream);

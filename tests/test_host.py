@@ -123,6 +123,29 @@ def test_trunk_forward_checks_its_step_before_launching():
         assert lib.cg_trunk_destroy(handle) == 0
 
 
+def test_heads_create_validates_the_config():
+    lib = nat.lib()
+    handle = ctypes.c_void_p()
+
+    def create(*cfg):
+        config = nat.HeadsConfig(*cfg)
+        return lib.cg_heads_create(ctypes.byref(config), 16, 16, 16, 16, 16, 16, ctypes.byref(handle))
+
+    # Shapes outside the fused kernel are refused before any device call.
+    assert create(250, 512, 256, 2) == nat.CG_ERR_UNSUPPORTED  # d_model % 16
+    assert "multiples of 16" in nat.last_error()
+    assert create(288, 512, 256, 2) == nat.CG_ERR_UNSUPPORTED  # d_model > 256
+    assert create(256, 1040, 256, 2) == nat.CG_ERR_UNSUPPORTED  # n_policy > 1024
+    assert create(256, 520, 256, 2) == nat.CG_ERR_UNSUPPORTED  # n_policy % 16
+    assert create(256, 512, 272, 2) == nat.CG_ERR_UNSUPPORTED  # d_mid > 256
+    assert create(256, 512, 256, 0) == nat.CG_ERR_UNSUPPORTED
+    assert create(256, 512, 256, 17) == nat.CG_ERR_UNSUPPORTED
+    config = nat.HeadsConfig(256, 512, 256, 2)
+    assert lib.cg_heads_create(ctypes.byref(config), None, 16, 16, 16, 16, 16, ctypes.byref(handle)) == nat.CG_ERR_INVALID
+    assert lib.cg_heads_forward(None, 16, 4, 16, 16, None) == nat.CG_ERR_INVALID
+    assert lib.cg_heads_destroy(None) == 0
+
+
 def test_trunk_config_matches_the_reference_rules():
     assert TrunkConfig(n_layers=16, value_embeddings="alternating").value_layers == tuple(range(1, 16, 2))
     assert TrunkConfig(n_layers=5, value_embeddings="alternating").value_layers == (0, 2, 4)
