@@ -21,6 +21,7 @@
 #include <type_traits>
 
 #include "attention.h"
+#include "attn_dev.h"
 #include "common.h"
 
 namespace cg {
@@ -62,33 +63,8 @@ __device__ __forceinline__ void load_widen(const T *__restrict__ p, float (&out)
   for (int i = 0; i < N; ++i) out[i] = to_f32(tmp[i]);
 }
 
-__device__ __forceinline__ float load_any(const void *p, int dtype, int64_t i) {
-  switch (dtype) {
-    case CG_BF16:
-      return to_f32(static_cast<const bf16 *>(p)[i]);
-    case CG_F16:
-      return to_f32(static_cast<const f16 *>(p)[i]);
-    default:
-      return static_cast<const float *>(p)[i];
-  }
-}
-
-__device__ __forceinline__ void store_any(void *p, int dtype, int64_t i, float v) {
-  switch (dtype) {
-    case CG_BF16:
-      static_cast<bf16 *>(p)[i] = from_f32<bf16>(v);
-      break;
-    case CG_F16:
-      static_cast<f16 *>(p)[i] = from_f32<f16>(v);
-      break;
-    default:
-      static_cast<float *>(p)[i] = v;
-  }
-}
-
 constexpr int KEYS_PER_BLOCK = 64;
 constexpr int QB = 4;  // queries per pass over the keys
-constexpr float NEG_BIG = -1.0e30f;
 
 template <typename TKV, int D, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(AttnArgs a) {
@@ -293,33 +269,6 @@ __global__ __launch_bounds__(64 * WAVES) void decode_attention_kernel(AttnArgs a
 //     ordering of the product is chosen to match where the scores already are, so P never
 //     moves between lanes); V^T is read from a padded per-wave LDS copy of the V tile.
 // Query t of the sequence sees keys < min(key_lengths + t, span): per-column masks.
-typedef __attribute__((ext_vector_type(4))) float f32x4;
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
-typedef __attribute__((ext_vector_type(8))) float f32x8;
-
-template <typename TKV>
-struct Mfma16;  // 16-bit operand helpers
-
-template <>
-struct Mfma16<bf16> {
-  typedef bf16x8 vec;
-  static __device__ __forceinline__ vec from(const f32x8 &f) { return __builtin_convertvector(f, bf16x8); }
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma16<f16> {
-  typedef f16x8 vec;
-  static __device__ __forceinline__ vec from(const f32x8 &f) { return __builtin_convertvector(f, f16x8); }
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
 template <typename TKV, int D, int NQT>
 __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) {
   constexpr int ES = int(sizeof(TKV));
@@ -600,57 +549,6 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
 //     ds_read_b64_tr_b16: within each 16-lane group, result lane i, element e is element
 //     i % 4 of the 8 bytes lane 4 e + i / 4 addressed; lane j addressing key (j / 4) of a
 //     4-key run at dims 4 (j % 4) .. +3 therefore receives 4 consecutive keys of dim j.
-typedef __attribute__((ext_vector_type(4))) short s16x4;
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
-
-__device__ __forceinline__ Rsrc make_rsrc(const void *p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, int(bytes), 0x00020000);
-}
-// Cache policy of the K / V stream loads (buffer instruction bits: 1 sc0, 2 nt, 16 sc1).
-#ifndef CG_KV_CPOL
-#define CG_KV_CPOL 2
-#endif
-__device__ __forceinline__ uint4 bload16(Rsrc r, uint32_t off) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CG_KV_CPOL);
-  return uint4{v[0], v[1], v[2], v[3]};
-}
-__device__ __forceinline__ float xor16_max(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor32_max(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor16_sum(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float xor32_sum(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-// Max / min of an int over the 16 lanes of a DPP row.
-__device__ __forceinline__ int row16_max(int v) {
-  v = max(v, dpp_i<0xB1>(v));
-  v = max(v, dpp_i<0x4E>(v));
-  v = max(v, dpp_i<0x124>(v));
-  v = max(v, dpp_i<0x128>(v));
-  return v;
-}
-__device__ __forceinline__ int row16_min(int v) {
-  v = min(v, dpp_i<0xB1>(v));
-  v = min(v, dpp_i<0x4E>(v));
-  v = min(v, dpp_i<0x124>(v));
-  v = min(v, dpp_i<0x128>(v));
-  return v;
-}
-
 // SPLIT waves share one (sequence, KV head): wave p of the unit takes tiles p, p + SPLIT,
 // ...; their partial (max, sum, O) merge in LDS at the end (SPLIT 1: four units per block).
 #ifndef TR_WAVES_PER_EU
@@ -698,8 +596,8 @@ void decode_attention_tr_kernel(AttnArgs a) {
   // This (row, head) segment: max_len keys of D elements.
   const int64_t seg = row_ok ? (row * a.kv_heads + h) * int64_t(a.max_len) * D : 0;
   const uint32_t seg_bytes = uint32_t(a.max_len) * D * 2;
-  const Rsrc kres = make_rsrc(static_cast<const TKV *>(a.k) + seg, seg_bytes);
-  const Rsrc vres = make_rsrc(static_cast<const TKV *>(a.v) + seg, seg_bytes);
+  const Rsrc kres = kv_rsrc(static_cast<const TKV *>(a.k) + seg, seg_bytes);
+  const Rsrc vres = kv_rsrc(static_cast<const TKV *>(a.v) + seg, seg_bytes);
 
   const int nq = int(count) * G;
   for (int qg = 0; qg < nq; qg += NQT * 16) {
@@ -732,8 +630,8 @@ void decode_attention_tr_kernel(AttnArgs a) {
 #pragma unroll
         for (int dk = 0; dk < DK; ++dk) {
           const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
-          kr[st][j][dk] = bload16(kres, off);
-          vr[st][j][dk] = bload16(vres, off);
+          kr[st][j][dk] = kv_load16(kres, off);
+          vr[st][j][dk] = kv_load16(vres, off);
         }
       }
     };

@@ -426,8 +426,9 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
         set_next(ta, 0);
         launch_tail(ta, s);
       }
-      for (int l = 0; l < c.n_layers; ++l) {
-        attention(l);
+      // The tail of layer l: its post-attention half, then the next layer's QKV (or the
+      // final norm).
+      auto tail_of = [&](int l) {
         const cg_layer_params &P = t.layers[l];
         TailArgs ta = base();
         ta.do_post = 1;
@@ -449,7 +450,11 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
         ta.x_src = w.x;
         ta.x = w.x;
         set_next(ta, l + 1);
-        launch_tail(ta, s);
+        return ta;
+      };
+      for (int l = 0; l < c.n_layers; ++l) {
+        attention(l);
+        launch_tail(tail_of(l), s);
       }
       return;
     }
