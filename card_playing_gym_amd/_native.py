@@ -144,6 +144,12 @@ _SIGNATURES = {
     "cg_heads_refresh": (c_int32, [c_void_p, c_void_p]),
     "cg_heads_destroy": (c_int32, [c_void_p]),
     "cg_heads_forward": (c_int32, [c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
+    "cg_masked_probabilities": (
+        c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p],
+    ),
+    "cg_sample_rows": (
+        c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_void_p],
+    ),
     "cg_advance_positions": (c_int32, [c_void_p, c_int32, c_int64, c_void_p]),
 }
 

@@ -260,6 +260,21 @@ int cg_heads_destroy(cg_heads *heads);
 int cg_heads_forward(const cg_heads *heads, const float *hidden, int32_t m, float *logits,
                      float *values, void *stream);
 
+/* ---- policy sampling ------------------------------------------------------------- */
+
+/* masked_probabilities (cardgym/rl/ppo.py:75-82): softmax of each row of fp32 logits over
+ * its legal entries (mask bytes != 0), exactly 0 on illegal ones; numpy's float32 order
+ * (max, exp(x - max), pairwise-summed normaliser, correctly rounded division).  Rows
+ * without a legal entry give NaN rows, as numpy does.  Strides are in elements. */
+int cg_masked_probabilities(const float *logits, int64_t ld_logits, const uint8_t *mask, int64_t ld_mask,
+                            int32_t rows, int32_t width, float *probs, int64_t ld_probs, void *stream);
+
+/* sample_rows (cardgym/rl/ppo.py:85-94): per row, the number of float32 running sums of
+ * probs below the row's float64 uniform, clamped to the last legal index and replaced by
+ * it when illegal; int64 indices.  Bit-exact with the reference for the same inputs. */
+int cg_sample_rows(const float *probs, int64_t ld_probs, const uint8_t *mask, int64_t ld_mask,
+                   const double *uniforms, int32_t rows, int32_t width, int64_t *sampled, void *stream);
+
 /* Adds `delta` to every entry of the int64 array a (n entries): the synthetic driver's
  * "every game appended one token" position update, kept on the device. */
 int cg_advance_positions(int64_t *positions, int32_t n, int64_t delta, void *stream);

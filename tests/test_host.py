@@ -146,6 +146,16 @@ def test_heads_create_validates_the_config():
     assert lib.cg_heads_destroy(None) == 0
 
 
+def test_sampling_entry_points_check_their_arguments():
+    lib = nat.lib()
+    assert lib.cg_masked_probabilities(16, 4, 16, 4, -1, 4, 16, 4, None) == nat.CG_ERR_INVALID
+    assert lib.cg_masked_probabilities(16, 3, 16, 4, 2, 4, 16, 4, None) == nat.CG_ERR_INVALID  # stride < width
+    assert lib.cg_masked_probabilities(None, 4, 16, 4, 2, 4, 16, 4, None) == nat.CG_ERR_INVALID
+    assert lib.cg_masked_probabilities(None, 4, None, 4, 0, 4, None, 4, None) == 0  # nothing to do
+    assert lib.cg_sample_rows(16, 4, 16, 4, 16, 2, 0, 16, None) == nat.CG_ERR_INVALID  # width 0
+    assert lib.cg_sample_rows(16, 4, None, 4, 16, 2, 4, 16, None) == nat.CG_ERR_INVALID
+
+
 def test_trunk_config_matches_the_reference_rules():
     assert TrunkConfig(n_layers=16, value_embeddings="alternating").value_layers == tuple(range(1, 16, 2))
     assert TrunkConfig(n_layers=5, value_embeddings="alternating").value_layers == (0, 2, 4)

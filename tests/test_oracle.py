@@ -337,3 +337,60 @@ def test_bf16_policy_rounds_at_the_reference_points():
     out32 = ref32.forward_full(*ref32.condition(x))
     assert out16.dtype == torch.float32
     assert 0 < (out16 - out32).abs().max() < 5e-2
+
+
+# ---- policy sampling (cardgym/rl/ppo.py:75-94) -----------------------------------------
+
+from oracle.sampling import masked_probabilities, pairwise_sum_f32, sample_rows  # noqa: E402
+
+
+def test_sampling_oracle_reference_known_answer():
+    """The reference's own test (tests/rl/test_rl.py:39-47): probabilities sum to one and
+    no uniform (0, 1 or random) ever picks an illegal action."""
+
+    rng = np.random.default_rng(0)
+    mask = rng.random((200, 9)) < 0.4
+    mask[np.arange(200), rng.integers(0, 9, 200)] = True
+    probabilities = masked_probabilities(rng.normal(size=(200, 9)).astype(np.float32), mask)
+    np.testing.assert_allclose(probabilities.sum(1), 1.0, rtol=1e-6)
+    for uniforms in (np.zeros(200), np.ones(200), rng.random(200)):
+        sampled = sample_rows(probabilities, mask, uniforms)
+        assert mask[np.arange(200), sampled].all()
+
+
+def test_sampling_oracle_closed_forms():
+    # One legal entry: probability exactly 1 there, and it is picked for any uniform.
+    mask = np.zeros((3, 7), dtype=bool)
+    mask[np.arange(3), [0, 3, 6]] = True
+    logits = np.random.default_rng(1).normal(size=(3, 7)).astype(np.float32)
+    p = masked_probabilities(logits, mask)
+    assert (p[mask] == 1.0).all() and (p[~mask] == 0.0).all()
+    for u in (0.0, 0.5, 1.0):
+        assert (sample_rows(p, mask, np.full(3, u)) == [0, 3, 6]).all()
+    # k equal legal logits: 1/k each, exactly for k a power of two; the uniform picks the
+    # (floor(u k))-th legal entry away from the boundaries.
+    mask = np.ones((1, 8), dtype=bool)
+    p = masked_probabilities(np.full((1, 8), 3.0, dtype=np.float32), mask)
+    assert (p == np.float32(0.125)).all()
+    for u, want in ((0.01, 0), (0.3, 2), (0.99, 7), (0.0, 0), (1.0, 7)):
+        assert sample_rows(p, mask, np.array([u]))[0] == want
+    # u = 0 with the first entry illegal: nothing is below 0, entry 0 is illegal, so the
+    # reference falls back to the last legal entry, not the first.
+    mask = np.array([[False, True, True, False]])
+    p = masked_probabilities(np.zeros((1, 4), dtype=np.float32), mask)
+    assert sample_rows(p, mask, np.array([0.0]))[0] == 2
+
+
+def test_pairwise_order_matches_numpy_sum():
+    """The order the device normaliser follows is numpy's own: bit-equal sums for widths
+    across the block (128) and split boundaries, with values spanning many magnitudes."""
+
+    rng = np.random.default_rng(2)
+    for n in list(range(1, 40)) + [127, 128, 129, 136, 255, 256, 257, 384, 512, 513, 1000, 4099]:
+        row = (rng.standard_normal(n) * np.exp2(rng.integers(-20, 20, n))).astype(np.float32)
+        assert pairwise_sum_f32(row).tobytes() == np.sum(row).tobytes(), n
+        # np.cumsum is a plain running sum in float32 (what the sampler assumes).
+        run = np.float32(0)
+        for v in row:
+            run = np.float32(run + v)
+        assert np.cumsum(row)[-1].tobytes() == run.tobytes(), n
