@@ -11,7 +11,9 @@ Also reported (one JSON line on stdout):
     measured live with HIP events on the launch stream, against the 8 TB/s HBM peak;
   * cpu_baseline: the reference path restated in eager PyTorch (oracle/), on the host
     cores, on a bounded sample of the same workload;
-  * reference_gpu: the same restatement on the MI355X, eager and captured in a HIP graph.
+  * reference_gpu: the same restatement on the MI355X, eager and captured in a HIP graph;
+  * sampling: device policy sampling of the step's logits (masked softmax + inverse CDF);
+  * compaction: KVCache.copy_rows as self-play compacts the pool after games end.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 10]
 """
@@ -201,6 +203,46 @@ def sampling_time(bench: Bench, reps: int = 20) -> dict:
     return {"rows": rows, "width": width, "event_us_per_call": round(start.elapsed_time(end) * 1e3 / reps, 2)}
 
 
+def compaction_time(bench: Bench, reps: int = 5) -> dict:
+    """KV compaction as self-play runs it after games end (cardgym/rl/selfplay.py:353-372):
+    2048 two-seat games fill the 4096-row pool, 1/64 of them end, and every later game's
+    rows slide down over the gap, copying the cache's full prefix length.  Timed with HIP
+    events around `reps` calls; indices on the device (the pool classifies the chunk there)
+    and on the host (classified before upload)."""
+
+    cache = bench.cache
+    seats, games = 2, cache.capacity // 2
+    rng = np.random.default_rng(2)
+    alive = rng.random(games) >= 1 / 64
+    alive[0] = False  # at least one gap, ahead of almost every survivor
+    base = np.flatnonzero(alive) * seats
+    new = np.arange(base.size) * seats
+    moved = base != new
+    sources = (base[moved, None] + np.arange(seats)).reshape(-1)
+    targets = (new[moved, None] + np.arange(seats)).reshape(-1)
+    length = cache.max_len
+    moved_bytes = 2 * sources.size * cache.n_layers * 2 * cache.kv_heads * length * cache.head_dim * cache.dtype.itemsize
+    out = {"pairs": int(sources.size), "length": length, "layers": cache.n_layers,
+           "algorithmic_bytes": moved_bytes}
+    for where in ("device", "host"):
+        src = torch.from_numpy(sources)
+        dst = torch.from_numpy(targets)
+        if where == "device":
+            src, dst = src.to(bench.device), dst.to(bench.device)
+        cache.copy_rows(src, dst, length)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            cache.copy_rows(src, dst, length)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / reps
+        out[f"{where}_indices_us"] = round(us, 1)
+        out[f"{where}_indices_gbs"] = round(moved_bytes / us / 1e3, 1)
+    out["frac_of_peak"] = round(out["device_indices_gbs"] / HBM_PEAK_GBS, 4)
+    return out
+
+
 def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) -> dict:
     """The oracle's reference path on the host cores, on `games` of the workload's games, at
     steps first .. first + steps (the middle of the timed range: context lengths there are
@@ -375,6 +417,10 @@ def main() -> int:
         best = max(extra["reference_gpu"]["eager_game_tokens_per_s"], extra["reference_gpu"]["graph_game_tokens_per_s"])
         extra["reference_gpu"]["speedup_vs_best"] = round(value / best, 2)
         log(f"bench: reference path on the GPU {extra['reference_gpu']}")
+    # Rewrites cache rows: after everything that reads them.
+    extra["compaction"] = compaction_time(bench)
+    log(f"bench: compaction {extra['compaction']}")
+    if not args.no_baselines:
         del bench.cache
         torch.cuda.empty_cache()
         cpu = cpu_baseline(args.workload, args.cpu_games, args.cpu_steps, middle, args.warmup + args.steps)

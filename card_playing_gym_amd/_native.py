@@ -22,6 +22,7 @@ HEADER = PACKAGE.parent / "include" / "cardgym_hip.h"
 CG_OK, CG_ERR_INVALID, CG_ERR_UNSUPPORTED, CG_ERR_RANGE, CG_ERR_HIP = 0, 1, 2, 3, 4
 CG_F32, CG_BF16, CG_F16 = 0, 1, 2
 CG_ACT_NONE, CG_ACT_GELU = 0, 1
+CG_COPY_AUTO, CG_COPY_ORDERED = 0, 1
 
 c_int32 = ctypes.c_int32
 c_int64 = ctypes.c_int64
@@ -111,6 +112,10 @@ _SIGNATURES = {
     "cg_kv_write_range": (c_int32, [P(KVLayer), c_void_p, c_int32, P(KVSource), P(KVSource), c_int32, c_int32, c_void_p]),
     "cg_kv_read": (c_int32, [P(KVLayer), c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "cg_kv_copy_rows": (c_int32, [P(KVLayer), c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "cg_kv_copy_workspace_size": (c_size_t, [P(KVLayer), c_int32, c_int32, c_int32]),
+    "cg_kv_copy_rows_layers": (
+        c_int32, [P(KVLayer), c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_size_t, c_void_p],
+    ),
     "cg_kv_check_indices": (c_int32, [P(KVLayer), c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p]),
     "cg_decode_attention": (
         c_int32,

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import os
 
+import numpy as np
 import torch
 
 from .. import _native as nat
@@ -64,6 +65,8 @@ def _check_enabled() -> bool:
 class KVCache:
     # Cap on the gathered temporary one ``copy_rows`` chunk may hold (kv_cache.py:20-21).
     COPY_CHUNK_BYTES = 256 * 1024 * 1024
+    # Layers one cg_kv_copy_rows_layers call covers.
+    MAX_COPY_LAYERS = 64
 
     def __init__(
         self,
@@ -240,19 +243,69 @@ class KVCache:
         require_device(self.k[0])
         if length < 0 or length > self.max_len:
             raise IndexError("copy length past max_len")
+        # Indices the caller holds on the host are classified there (no device pass).
+        host = _host_indices(sources), _host_indices(targets)
         src = index_tensor(sources, self.device)
         dst = index_tensor(targets, self.device)
         if src.numel() != dst.numel():
             raise ValueError("sources and targets differ in length")
         if length == 0 or src.numel() == 0:
             return
+        for layer in range(self.n_layers):
+            self._validate(layer, src, None)
+            self._validate(layer, dst, None)
+        # Same chunking as the reference (kv_cache.py:124-127); the gathered temporary is
+        # as large as the reference's: all layers of a chunk for a stacked pool, one layer
+        # at a time otherwise.  Each call covers every layer (up to 64) of one chunk.
         row_bytes = max(self.kv_heads * length * self.head_dim * self.dtype.itemsize, 1)
+        staged_layers = 1
+        if self.stacked:
+            row_bytes *= self.n_layers
+            staged_layers = min(self.n_layers, self.MAX_COPY_LAYERS)
         chunk = max(self.COPY_CHUNK_BYTES // row_bytes, 1)
+        layers = self.layer_array()
+        stream = self._stream()
+        lib = nat.lib()
         for start in range(0, src.numel(), chunk):
             s, t = src[start : start + chunk], dst[start : start + chunk]
-            for layer in range(self.n_layers):
-                k_tmp, v_tmp = self.read(layer, s, length)
-                self.write_range(layer, t, 0, k_tmp, v_tmp)
+            plan = nat.CG_COPY_AUTO
+            if host[0] is not None and host[1] is not None:
+                hs, ht = host[0][start : start + chunk], host[1][start : start + chunk]
+                if ordered_pairs(hs, ht, self.capacity):
+                    plan = nat.CG_COPY_ORDERED
+            for first in range(0, self.n_layers, self.MAX_COPY_LAYERS):
+                count = min(self.MAX_COPY_LAYERS, self.n_layers - first)
+                view = ctypes_ref(layers[first])
+                one = lib.cg_kv_copy_workspace_size(view, count, s.numel(), length)
+                header = lib.cg_kv_copy_workspace_size(view, count, 0, 0)
+                size = header + (one - header) * min(staged_layers, count)
+                workspace = torch.empty(size, dtype=torch.uint8, device=self.device)
+                nat.call(
+                    "cg_kv_copy_rows_layers", view, count, s.data_ptr(), t.data_ptr(), s.numel(), length, plan,
+                    workspace.data_ptr(), size, stream,
+                )
+
+
+def _host_indices(values) -> np.ndarray | None:
+    """int64 numpy view of host-side indices; None for device tensors."""
+
+    if isinstance(values, torch.Tensor):
+        return None if values.device.type != "cpu" else values.detach().to(torch.int64).numpy().reshape(-1)
+    return np.asarray(values, dtype=np.int64).reshape(-1)
+
+
+def ordered_pairs(sources: np.ndarray, targets: np.ndarray, capacity: int) -> bool:
+    """True when every row lies in the pool and no pair writes a row that a later pair
+    reads: then copying the pairs one after the other equals gathering them all first."""
+
+    n = sources.size
+    if n == 0:
+        return True
+    if min(sources.min(), targets.min()) < 0 or max(sources.max(), targets.max()) >= capacity:
+        return False
+    last_reader = np.full(capacity, -1, dtype=np.int64)
+    np.maximum.at(last_reader, sources, np.arange(n, dtype=np.int64))
+    return bool((last_reader[targets] <= np.arange(n, dtype=np.int64)).all())
 
 
 def _ptr(tensor: torch.Tensor | None) -> int | None:

@@ -102,6 +102,24 @@ int cg_kv_read(const cg_kv_layer *layer, const int64_t *rows, int32_t B, int32_t
 int cg_kv_copy_rows(const cg_kv_layer *layer, const int64_t *sources, const int64_t *targets,
                     int32_t n, int32_t length, void *stream);
 
+/* KVCache.copy_rows (cardgym/nn/kv_cache.py:122-138) for one chunk over n_layers layers of
+ * one shape, with the reference's gather-then-write meaning: a target that is also a
+ * source of the chunk receives the source's old contents.  Chunks where no pair writes a
+ * row that a later pair reads (compaction: rows slide down) are copied at one read and one
+ * write per byte; others are staged through the workspace.  workspace: 16-byte aligned, at
+ * least cg_kv_copy_workspace_size bytes (the classification, then one layer's gathered
+ * prefixes); a larger one stages that many more layers per launch.  At most 64 layers.
+ * plan: CG_COPY_AUTO classifies the chunk on the device; CG_COPY_ORDERED is the caller's
+ * promise that every row is inside the pool and no pair writes a row that a later pair
+ * reads (it skips the classification and the staged launches; a broken promise gives
+ * wrong contents, never an access outside the pool's rows). */
+#define CG_COPY_AUTO 0
+#define CG_COPY_ORDERED 1
+size_t cg_kv_copy_workspace_size(const cg_kv_layer *layers, int32_t n_layers, int32_t n, int32_t length);
+int cg_kv_copy_rows_layers(const cg_kv_layer *layers, int32_t n_layers, const int64_t *sources,
+                           const int64_t *targets, int32_t n, int32_t length, int32_t plan, void *workspace,
+                           size_t workspace_size, void *stream);
+
 /* Validates row and position indices on the device (no host read-back): flag[0] is set
  * to 1 if any rows[b] is outside [0, capacity) or positions[i] outside [0, max_len).
  * flag must be zeroed by the caller.  n_pos is the length of positions. */

@@ -72,6 +72,9 @@ class RefCache:
         self.n_layers, self.capacity, self.max_len, self.dtype = n_layers, capacity, max_len, dtype
         self.kv_heads, self.head_dim = kv_heads, head_dim
         shape = (capacity, kv_heads, max_len, head_dim)
+        # kv_cache.py:40-41: one stacked tensor up to 2**31-1 elements; only copy_rows' chunk
+        # size depends on it (kv_cache.py:124-126).
+        self.stacked = n_layers * capacity * kv_heads * max_len * head_dim <= 2**31 - 1
         self.k = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(n_layers)]
         self.v = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(n_layers)]
 
@@ -104,6 +107,8 @@ class RefCache:
 
     def copy_rows(self, sources, targets, length):
         row_bytes = max(self.kv_heads * length * self.head_dim * self.dtype.itemsize, 1)
+        if self.stacked:
+            row_bytes *= self.n_layers
         chunk = max(self.COPY_CHUNK_BYTES // row_bytes, 1)
         for start in range(0, sources.shape[0], chunk):
             src, dst = sources[start : start + chunk], targets[start : start + chunk]

@@ -184,3 +184,149 @@ def test_out_of_range_indices_are_skipped_and_reported(device, monkeypatch):
         native.write_step(0, torch.tensor([99, 1]), torch.tensor([3, 3]), k, k)
     with pytest.raises(IndexError):
         native.write_step(0, torch.tensor([0, 1]), torch.tensor([3, 17]), k, k)
+
+
+def fill_pair(native, ref, gen):
+    for layer in range(native.n_layers):
+        shape = tuple(native.k[layer].shape)
+        fk = tricky(shape, gen).to(native.dtype)
+        fv = tricky(shape, gen).to(native.dtype)
+        native.k[layer].copy_(fk.to(native.device))
+        native.v[layer].copy_(fv.to(native.device))
+        ref.k[layer].copy_(fk)
+        ref.v[layer].copy_(fv)
+
+
+@pytest.mark.parametrize("cache_dtype", DTYPES)
+@pytest.mark.parametrize(
+    "sources,targets",
+    [
+        ([1, 2], [2, 1]),  # swap: both rows must see the other's old contents
+        ([5, 0, 7, 3], [2, 8, 6, 1]),  # disjoint: the direct path
+        ([3, 3, 3], [4, 5, 6]),  # one source fanned out
+        ([0, 1, 2, 3, 4, 5, 6, 7], [1, 2, 3, 4, 5, 6, 7, 8]),  # shift up by one: a chain of overlaps
+        ([1, 5, 6, 4], [2, 1, 7, 4]),  # staged (1), direct (5, 6) and a row onto itself (4) in one call
+    ],
+)
+def test_copy_rows_overlap_patterns(device, cache_dtype, sources, targets):
+    gen = torch.Generator().manual_seed(11)
+    native, ref = make_pair(cache_dtype, device)
+    fill_pair(native, ref, gen)
+    native.copy_rows(torch.tensor(sources), torch.tensor(targets), 17)
+    ref.copy_rows(torch.tensor(sources), torch.tensor(targets), 17)
+    torch.cuda.synchronize()
+    assert_same(native, ref)
+
+
+@pytest.mark.parametrize("stacked", [True, False])
+def test_copy_rows_chunked_compaction(device, stacked):
+    """selfplay.py:353-372's compaction pattern (survivors moved down, seats kept in order)
+    with a chunk cap small enough that the copy runs in many chunks, so overlaps cross
+    chunk boundaries exactly as the reference orders them."""
+
+    gen = torch.Generator().manual_seed(12)
+    native, ref = make_pair(torch.bfloat16, device, capacity=300, max_len=24, n_layers=3)
+    fill_pair(native, ref, gen)
+    for cache in (native, ref):
+        cache.COPY_CHUNK_BYTES = 7 * 2 * 19 * 32 * 2 * (3 if stacked else 1)
+        cache.stacked = stacked
+    alive = torch.rand(100, generator=gen) < 0.6
+    seats = 3
+    survivors = torch.nonzero(alive).flatten()
+    sources = (survivors[:, None] * seats + torch.arange(seats)).flatten()
+    targets = torch.arange(sources.numel())
+    native.copy_rows(sources, targets, 19)
+    ref.copy_rows(sources, targets, 19)
+    torch.cuda.synchronize()
+    assert_same(native, ref)
+
+
+@pytest.mark.parametrize("cache_dtype,head_dim", [(torch.bfloat16, 3), (torch.float16, 6), (torch.float32, 2), (torch.float32, 5)])
+def test_copy_rows_narrow_positions(device, cache_dtype, head_dim):
+    """Position widths that are not a multiple of 16 bytes (2-, 4- and 8-byte accesses)."""
+
+    gen = torch.Generator().manual_seed(13)
+    native, ref = make_pair(cache_dtype, device, head_dim=head_dim)
+    fill_pair(native, ref, gen)
+    sources, targets = torch.tensor([4, 5, 0]), torch.tensor([5, 3, 4])
+    native.copy_rows(sources, targets, 9)
+    ref.copy_rows(sources, targets, 9)
+    torch.cuda.synchronize()
+    assert_same(native, ref)
+
+
+def test_copy_rows_workspace_is_checked(device):
+    from card_playing_gym_amd import _native as nat
+
+    native, _ = make_pair(torch.float32, device)
+    layers = native.layer_array()
+    src = torch.tensor([1], device=device)
+    dst = torch.tensor([2], device=device)
+    need = nat.lib().cg_kv_copy_workspace_size(layers, 2, 1, 5)
+    assert need == 256 + 2 * 2 * 5 * 32 * 4  # classification, then one layer's K and V prefixes
+    small = torch.empty(need - 16, dtype=torch.uint8, device=device)
+    with pytest.raises(ValueError, match="workspace too small"):
+        nat.call("cg_kv_copy_rows_layers", layers, 2, src.data_ptr(), dst.data_ptr(), 1, 5, nat.CG_COPY_AUTO,
+                 small.data_ptr(), small.numel(), native._stream())
+
+
+def ordered(sources, targets) -> bool:
+    """No pair writes a row that a later pair reads (the chunks the ordered walk takes)."""
+
+    last = {}
+    for k, s in enumerate(sources):
+        last[s] = k
+    return all(last.get(t, -1) <= i for i, t in enumerate(targets))
+
+
+# Large enough (8 layers x 2 heads x K/V x 2048 16-byte slices) for the per-slice ordered
+# walk; smaller copies always take the staged path.
+WALK = dict(capacity=48, max_len=520, n_layers=8, kv_heads=2, head_dim=32)
+
+
+@pytest.mark.parametrize(
+    "sources,targets,is_ordered",
+    [
+        ([6, 7, 8, 9, 13, 14, 15, 16, 17, 30, 31], [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10], True),  # compaction
+        ([20, 21, 22], [30, 31, 32], True),  # disjoint
+        ([3, 3, 3], [4, 5, 6], True),  # fan-out
+        ([1, 5, 6, 4], [2, 1, 7, 4], True),  # a row onto itself, and a write after its read
+        ([1, 2], [2, 1], False),  # swap
+        (list(range(12)), list(range(1, 13)), False),  # shift up: each write precedes its read
+    ],
+)
+@pytest.mark.parametrize("indices_on", ["host", "device"])
+def test_copy_rows_ordered_walk(device, sources, targets, is_ordered, indices_on):
+    """Host indices are classified on the host (the walk alone runs for ordered chunks);
+    device indices on the device."""
+
+    assert ordered(sources, targets) == is_ordered
+    gen = torch.Generator().manual_seed(14)
+    native, ref = make_pair(torch.bfloat16, device, **WALK)
+    fill_pair(native, ref, gen)
+    where = "cpu" if indices_on == "host" else device
+    native.copy_rows(torch.tensor(sources, device=where), torch.tensor(targets, device=where), 512)
+    ref.copy_rows(torch.tensor(sources), torch.tensor(targets), 512)
+    torch.cuda.synchronize()
+    assert_same(native, ref)
+
+
+@pytest.mark.parametrize("stacked", [True, False])
+@pytest.mark.parametrize("indices_on", ["host", "device"])
+def test_copy_rows_ordered_walk_in_chunks(device, stacked, indices_on):
+    gen = torch.Generator().manual_seed(15)
+    native, ref = make_pair(torch.float16, device, **WALK)
+    fill_pair(native, ref, gen)
+    for cache in (native, ref):
+        cache.COPY_CHUNK_BYTES = 5 * 2 * 512 * 32 * 2 * (8 if stacked else 1)  # five rows a chunk
+        cache.stacked = stacked
+    alive = torch.tensor([0, 1, 1, 0, 1, 0, 0, 1, 1, 1, 0, 1, 1, 0, 1, 1], dtype=torch.bool)
+    survivors = torch.nonzero(alive).flatten()
+    sources = (survivors[:, None] * 3 + torch.arange(3)).flatten()
+    targets = torch.arange(sources.numel())
+    moved = sources != targets
+    where = "cpu" if indices_on == "host" else device
+    native.copy_rows(sources[moved].to(where), targets[moved].to(where), 512)
+    ref.copy_rows(sources[moved], targets[moved], 512)
+    torch.cuda.synchronize()
+    assert_same(native, ref)

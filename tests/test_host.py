@@ -261,3 +261,39 @@ def test_workload_shapes_match_the_benchmark_configs():
     cfg = trunk_config(16)
     assert (cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_ff) == (256, 8, 2, 32, 1024)
     assert textwrap.dedent("x") == "x"
+
+
+def test_ordered_pairs_matches_its_definition():
+    """ordered_pairs: every row in the pool and no pair i writes a row that a later pair k
+    reads (t_i == s_k, i < k) -- checked against that definition by brute force, and
+    against its consequence: copying the pairs in order equals gathering them first."""
+
+    from card_playing_gym_amd.nn.kv_cache import ordered_pairs
+
+    rng = np.random.default_rng(3)
+    seen = {True: 0, False: 0}
+    for _ in range(400):
+        cap = int(rng.integers(1, 12))
+        n = int(rng.integers(0, 8))
+        s = rng.integers(-1 if rng.random() < 0.1 else 0, cap + (1 if rng.random() < 0.1 else 0), n)
+        t = rng.permutation(cap)[: min(n, cap)] if rng.random() < 0.7 else rng.integers(0, cap, n)
+        s = s[: t.size]
+        got = ordered_pairs(s, t, cap)
+        inside = all(0 <= x < cap for x in list(s) + list(t))
+        brute = inside and not any(t[i] == s[k] for i in range(s.size) for k in range(i + 1, s.size))
+        assert got == brute, (s, t, cap)
+        seen[got] += 1
+        if got:
+            rows = np.arange(cap) * 10 + 7
+            gathered = rows.copy()
+            gathered[t] = rows[s]
+            walked = rows.copy()
+            for i in range(s.size):
+                walked[t[i]] = walked[s[i]]
+            if len(set(t.tolist())) == t.size:  # duplicate targets have no defined order
+                assert (walked == gathered).all()
+    assert seen[True] > 50 and seen[False] > 50
+    # Compaction (rows slide down) is ordered; a swap and a shift up are not.
+    assert ordered_pairs(np.array([3, 4, 5, 9]), np.array([0, 1, 2, 3]), 10)
+    assert not ordered_pairs(np.array([1, 2]), np.array([2, 1]), 4)
+    assert not ordered_pairs(np.array([0, 1, 2]), np.array([1, 2, 3]), 4)
