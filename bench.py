@@ -13,7 +13,8 @@ Also reported (one JSON line on stdout):
     cores, on a bounded sample of the same workload;
   * reference_gpu: the same restatement on the MI355X, eager and captured in a HIP graph;
   * sampling: device policy sampling of the step's logits (masked softmax + inverse CDF);
-  * compaction: KVCache.copy_rows as self-play compacts the pool after games end.
+  * compaction: KVCache.copy_rows as self-play compacts the pool after games end;
+  * prefill: forward_prefill throughput at two shapes, beside the reference path on the GPU.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 10]
 """
@@ -243,6 +244,52 @@ def compaction_time(bench: Bench, reps: int = 5) -> dict:
     return out
 
 
+def prefill_time(bench: Bench, with_reference: bool, reps: int = 3) -> dict:
+    """Prefill (SequenceModel.forward_prefill, cardgym/nn/trunk.py:376-389) of fresh rows of
+    the bench's pool: 4096 games x 16 tokens and 64 games x 512 tokens, bf16, wall time
+    over `reps` calls after one untimed call; with `with_reference`, the oracle's restated
+    reference path on the same GPU for the same shapes."""
+
+    from oracle.reference_path import RefCache, RefSynthetic, ref_config_of
+
+    cfg, dev = bench.config, bench.device
+    out = {}
+    ref = rcache = None
+    if with_reference:
+        state = {k: v.detach() for k, v in bench.model.state_dict().items()}
+        ref = RefSynthetic(state, ref_config_of(cfg), "bf16")
+        rcache = RefCache(cfg.n_layers, cfg.n_kv_heads, cfg.head_dim, 4096, 512, torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(4)
+
+    def wall(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    for games, length in ((4096, 16), (64, 512)):
+        tokens = torch.randint(0, 512, (games, length, 1), generator=gen, device=dev)
+        rows = torch.arange(games, device=dev)
+
+        def ours():
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                bench.model.forward_prefill(tokens, bench.cache, rows)
+
+        entry = {"tokens_per_s": round(games * length / wall(ours), 1)}
+        if ref is not None:
+            def theirs():
+                with torch.no_grad():
+                    ref.forward_prefill(tokens, rcache, rows)
+
+            entry["reference_gpu_tokens_per_s"] = round(games * length / wall(theirs), 1)
+            entry["speedup"] = round(entry["tokens_per_s"] / entry["reference_gpu_tokens_per_s"], 2)
+        out[f"{games}x{length}"] = entry
+    return out
+
+
 def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) -> dict:
     """The oracle's reference path on the host cores, on `games` of the workload's games, at
     steps first .. first + steps (the middle of the timed range: context lengths there are
@@ -417,9 +464,11 @@ def main() -> int:
         best = max(extra["reference_gpu"]["eager_game_tokens_per_s"], extra["reference_gpu"]["graph_game_tokens_per_s"])
         extra["reference_gpu"]["speedup_vs_best"] = round(value / best, 2)
         log(f"bench: reference path on the GPU {extra['reference_gpu']}")
-    # Rewrites cache rows: after everything that reads them.
+    # These rewrite cache rows: after everything that reads them.
     extra["compaction"] = compaction_time(bench)
     log(f"bench: compaction {extra['compaction']}")
+    extra["prefill"] = prefill_time(bench, with_reference=not args.no_baselines)
+    log(f"bench: prefill {extra['prefill']}")
     if not args.no_baselines:
         del bench.cache
         torch.cuda.empty_cache()

@@ -18,10 +18,12 @@
 //     traffic in the key loop except the 2-step quad reduction of the dot products); the
 //     16 slots and the waves are merged once at the end (log-sum-exp merge);
 //   * softmax in base 2 with log2(e) folded into the query scale.
+#include <algorithm>
 #include <type_traits>
 
 #include "attention.h"
 #include "attn_dev.h"
+
 #include "common.h"
 
 namespace cg {
@@ -600,7 +602,8 @@ void decode_attention_tr_kernel(AttnArgs a) {
   const Rsrc vres = kv_rsrc(static_cast<const TKV *>(a.v) + seg, seg_bytes);
 
   const int nq = int(count) * G;
-  for (int qg = 0; qg < nq; qg += NQT * 16) {
+  // Query groups of 16 NQT are dealt over the grid's y dimension (prefill: many per unit).
+  for (int qg = blockIdx.y * NQT * 16; qg < nq; qg += gridDim.y * NQT * 16) {
     // ---- key limits of this group's queries (column li of tile qt is query qg + 16 qt + li)
     int lim[NQT];
     int kmax = 0, kmin = 0x7fffffff;
@@ -867,6 +870,9 @@ void decode_attention_tr_kernel(AttnArgs a) {
 #ifndef TR_DEPTH
 #define TR_DEPTH 1
 #endif
+#ifndef TR_ONE_WAVE_ITEMS
+#define TR_ONE_WAVE_ITEMS 2048
+#endif
 
 template <typename TKV, int D>
 void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
@@ -878,7 +884,18 @@ void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
     const unsigned tr_grid = (units * TR_SPLIT + 3) / 4;
     if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT, TR_KT, TR_DEPTH><<<tr_grid, 256, 0, s>>>(a);
     else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT, TR_KT, TR_DEPTH><<<tr_grid, 256, 0, s>>>(a);
-    else decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1><<<tr_grid, 256, 0, s>>>(a);
+    else {
+      // Multi-token rows (prefill, chunks): one block row per 64 queries of a unit.  With
+      // enough (unit, query group) items to fill the chip, or no query seeing more than one
+      // 64-key tile, one wave takes a whole item (four per block); otherwise four waves
+      // split its key tiles and merge.
+      const dim3 grid_q(1, unsigned(std::min<int64_t>((int64_t(queries) + 63) / 64, 65535)));
+      if (a.span <= 64 || int64_t(units) * grid_q.y >= TR_ONE_WAVE_ITEMS) {
+        decode_attention_tr_kernel<TKV, D, 4, 1, 64, 1><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
+      } else {
+        decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1><<<dim3(tr_grid, grid_q.y), 256, 0, s>>>(a);
+      }
+    }
   } else {
     if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
     else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);

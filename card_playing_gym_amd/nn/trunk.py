@@ -422,7 +422,9 @@ class Trunk(nn.Module):
         readout = torch.full((batch,), length - 1, dtype=torch.int64, device=device)
         return self._run(
             x, ple, values, cache, n_seqs=batch, T=length, seq_start=None, positions=positions,
-            rows=None if rows is None else index_tensor(rows, device), readout=readout, span=None,
+            # Positions start at 0, so no key past the chunk's length is visible: span = length
+            # is exact and lets attention size its launch to the chunk.
+            rows=None if rows is None else index_tensor(rows, device), readout=readout, span=length,
         )
 
     def forward(

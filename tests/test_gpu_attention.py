@@ -63,6 +63,34 @@ def test_decode_attention_matches_oracle(device, dtype, D, heads, kv_heads, T):
         assert (got - literal).abs().max().item() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("T,prefix", [(16, 0), (40, 0), (40, 30), (150, 0), (64, 200)])
+def test_multi_token_rows(device, dtype, D, T, prefix):
+    """Prefill-sized rows: 4 query heads per KV head x T tokens, so several 64-query groups
+    per (row, head), dealt over the launch's second dimension; spans of at most 64 keys
+    (prefill of a short chunk) take one wave per (row, head)."""
+
+    gen = torch.Generator().manual_seed(T * 7 + prefix + D)
+    heads, kv_heads = 8, 2
+    capacity, max_len, B = 11, 320, 7
+    k_cache = torch.randn(capacity, kv_heads, max_len, D, generator=gen).to(dtype)
+    v_cache = torch.randn(capacity, kv_heads, max_len, D, generator=gen).to(dtype)
+    rows = torch.randperm(capacity, generator=gen)[:B]
+    positions = torch.full((B,), prefix) if prefix == 0 else torch.randint(0, prefix + 1, (B,), generator=gen)
+    key_lengths = positions + 1
+    span = int(positions.max()) + T
+    q = torch.randn(B, heads, T, D, generator=gen)
+    out = decode_attention(q.to(device), k_cache.to(device), v_cache.to(device), rows.to(device),
+                           key_lengths.to(device), span, 1.0 / math.sqrt(D))
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    exact = oracle(q, k_cache, v_cache, rows, key_lengths, span, heads, kv_heads, literal=False)
+    assert (got - exact).abs().max().item() <= TOL[dtype]
+    literal = oracle(q, k_cache, v_cache, rows, key_lengths, span, heads, kv_heads, literal=True)
+    assert (got - literal).abs().max().item() <= TOL[dtype]
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_span_caps_the_visible_keys(device, dtype):
     """A span shorter than a row's length truncates its keys, as reading k[:, :, :span] does."""
