@@ -126,25 +126,47 @@ template <int FM>
 __device__ __forceinline__ void stage_mma(f32x4 (&acc)[FM][FN], const unsigned char *lds,
                                           uint4 (&w)[KS][FN], const Slice &next, bool refill, int lane) {
   const int li = lane & 15, lg = lane >> 4;
-  // The stage's A fragments are read up front: one LDS round trip instead of one per k-step.
-  uint4 af[KS][FM];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[ks][i] = *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
   uint32_t base[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) base[j] = slice_base(next, j, lane);
+  auto a_frag = [&](int ks, int i) {
+    return *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
+  };
+  if constexpr (FM == 1) {
+    // One row tile: the stage's A fragments are read up front, one LDS round trip instead
+    // of one per k-step.
+    uint4 af[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) af[ks] = a_frag(ks, 0);
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[ks][i], w[ks][j], acc[i][j]);
-    if (refill) {
+      for (int j = 0; j < FN; ++j) acc[0][j] = mma(af[ks], w[ks][j], acc[0][j]);
+      if (refill) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+        for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+      }
+    }
+  } else {
+    // Taller blocks: the A fragments of k-step ks + 1 are read while ks multiplies (all of
+    // them up front would take 4 FM x KS registers); every weight fragment feeds FM MFMAs.
+    uint4 af[2][FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = a_frag(0, i);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[(ks + 1) & 1][i] = a_frag(ks + 1, i);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mma(af[ks & 1][i], w[ks][j], acc[i][j]);
+      if (refill) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+      }
     }
   }
 }

@@ -76,20 +76,61 @@ bool tail_supported(int d, int d_ff, int n_qkv) {
          n_qkv > 0 && n_qkv % 16 == 0 && n_qkv <= 3 * PANEL;
 }
 
+namespace {
+// Compute units of the current device (block rounds of the row-block choice below).
+int device_cus() {
+  static thread_local int dev = -1, cus = 256;
+  int d = 0;
+  if (hipGetDevice(&d) == hipSuccess && d != dev) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) == hipSuccess && n > 0) cus = n;
+    dev = d;
+  }
+  return cus;
+}
+
+// Rows per block: one block per CU at a time (eight waves), so a launch takes
+// ceil(blocks / CUs) rounds of one block's life, measured on MI355X at d 256 / d_ff 1024 as
+// about 9.5 us + 13.5 us per 16 rows (weights streamed once per block, epilogues and
+// row traffic per row).  16 rows keep the decode step (4096 rows) at one round of 256
+// blocks; taller blocks pay off once the rows fill several rounds (prefill, packed chunks).
+int tail_rows_per_block(int64_t M) {
+#ifdef CG_TAIL_FORCE_BM
+  if (M >= 0) return CG_TAIL_FORCE_BM;  // measurement builds only
+#endif
+  const int64_t cus = device_cus();
+  int best = 16;
+  double best_t = 1e30;
+  for (int bm : {16, 32, 64}) {
+    const int64_t rounds = ((M + bm - 1) / bm + cus - 1) / cus;
+    const double t = double(rounds) * (9.5 + 13.5 * bm / 16);
+    if (t < best_t - 1e-9) {
+      best_t = t;
+      best = bm;
+    }
+  }
+  return best;
+}
+}  // namespace
+
 void launch_tail(const TailArgs &a, hipStream_t s) {
   CG_REQUIRE(tail_supported(a.d, a.d_ff, a.n_qkv), CG_ERR_UNSUPPORTED, "fused layer: unsupported shape");
   if (a.M <= 0) return;
-  constexpr int BM = 16;  // 16-row blocks: one per CU at the benchmark's 4096 tokens
+  const int bm = tail_rows_per_block(a.M);
   const int nc = (a.d_ff + PANEL - 1) / PANEL, nq = (a.n_qkv + PANEL - 1) / PANEL;
   const int mode = !a.do_post ? 0 : (a.final_ln ? 2 : 1);
-  const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + 3 * BM * 4;
-  const unsigned grid = unsigned((a.M + BM - 1) / BM);
-  auto go = [&](auto kernel) {
-    kernel<<<grid, THREADS, dyn, s>>>(a);
+  auto go = [&](auto k16, auto k32, auto k64) {
+    const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + 3 * size_t(bm) * 4;
+    const unsigned grid = unsigned((a.M + bm - 1) / bm);
+    if (bm == 64) k64<<<grid, THREADS, dyn, s>>>(a);
+    else if (bm == 32) k32<<<grid, THREADS, dyn, s>>>(a);
+    else k16<<<grid, THREADS, dyn, s>>>(a);
     CG_LAUNCHED();
   };
-#define CG_TAIL_CASE(MODE, NC, NQ) \
-  if (mode == MODE && (MODE == 0 || nc == NC) && (MODE == 2 || nq == NQ)) return go(layer_tail_kernel<BM, MODE, NC, NQ>)
+#define CG_TAIL_CASE(MODE, NC, NQ)                                                       \
+  if (mode == MODE && (MODE == 0 || nc == NC) && (MODE == 2 || nq == NQ))                \
+    return go(layer_tail_kernel<16, MODE, NC, NQ>, layer_tail_kernel<32, MODE, NC, NQ>, \
+              layer_tail_kernel<64, MODE, NC, NQ>)
   CG_TAIL_CASE(0, 1, 1); CG_TAIL_CASE(0, 1, 2); CG_TAIL_CASE(0, 1, 3);
   CG_TAIL_CASE(1, 1, 1); CG_TAIL_CASE(1, 1, 2); CG_TAIL_CASE(1, 1, 3);
   CG_TAIL_CASE(1, 2, 1); CG_TAIL_CASE(1, 2, 2); CG_TAIL_CASE(1, 2, 3);

@@ -13,7 +13,11 @@ namespace {
 #ifndef TAIL_RING
 #define TAIL_RING 2
 #endif
-constexpr int RING = TAIL_RING;       // stages of weights in flight per wave
+// Stages of weights in flight per wave: two for 16- and 32-row blocks; one for 64-row
+// blocks, whose four row tiles per fragment keep each stage's MFMAs busy four times as long
+// (and whose accumulators leave no room for a second ring stage).
+template <int BM>
+constexpr int ring_of() { return BM >= 64 ? 1 : TAIL_RING; }
 
 enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
 
@@ -171,6 +175,7 @@ template <int BM, int MODE, int NC, int NQ>
 __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned char *panel,
                                           unsigned char (*hbuf)[BM * ROWB], float *red, float *dyn) {
   constexpr int FM = BM / 16;
+  constexpr int RING = ring_of<BM>();
   constexpr bool POST = MODE != 0, FINAL = MODE == 2;
 
   // The wave index is uniform: readfirstlane keeps its derived column ranges scalar.
@@ -187,15 +192,20 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   const uint32_t xbytes = uint32_t(a.M) * uint32_t(d) * 4;
 
   // Prologue loads, issued before the weight stream (loads complete in order, so anything
-  // issued after the ring's 32 fragment loads per lane would wait for them): this block's
-  // attention rows (one 16-byte chunk per thread) and the per-layer vectors.
-  static_assert(BM * (PANEL / 8) <= THREADS, "one attention chunk per thread");
+  // issued after the ring's fragment loads would wait for them): this block's attention
+  // rows (16-byte chunks, FM per thread at most) and the per-layer vectors.
+  static_assert(BM * (PANEL / 8) <= FM * THREADS, "FM attention chunks per thread");
   const int m0_ = blk * BM;
   const int cpr = d / 8;
-  uint4 arow = {0u, 0u, 0u, 0u};
-  if (POST && tid < BM * cpr) {
-    const Rsrc ra = rsrc(a.attn, uint32_t(a.M) * uint32_t(d) * 2);
-    arow = bload16(ra, (uint32_t(m0_ + tid / cpr) * d + 8 * (tid % cpr)) * 2);
+  uint4 arow[FM];
+#pragma unroll
+  for (int k = 0; k < FM; ++k) {
+    const int c = tid + k * THREADS;
+    arow[k] = uint4{0u, 0u, 0u, 0u};
+    if (POST && c < BM * cpr) {
+      const Rsrc ra = rsrc(a.attn, uint32_t(a.M) * uint32_t(d) * 2);
+      arow[k] = bload16(ra, (uint32_t(m0_ + c / cpr) * d + 8 * (c % cpr)) * 2);
+    }
   }
   constexpr int NB_UP = (4 * PANEL + THREADS - 1) / THREADS;
   float v_up[NB_UP], v_vec[5];
@@ -270,7 +280,11 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     const int li = lane & 15, lg = lane >> 4;
     if (POST) {
       // Attention rows of this block -> panel (rows past M read as 0).
-      if (tid < BM * cpr) *reinterpret_cast<uint4 *>(panel + (tid / cpr) * ROWB + 16 * (tid % cpr)) = arow;
+#pragma unroll
+      for (int k = 0; k < FM; ++k) {
+        const int c = tid + k * THREADS;
+        if (c < BM * cpr) *reinterpret_cast<uint4 *>(panel + (c / cpr) * ROWB + 16 * (c % cpr)) = arow[k];
+      }
       lds_barrier();
     } else {
       // First block's prologue: the conditioned input is the residual stream.

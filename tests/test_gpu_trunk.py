@@ -285,3 +285,44 @@ def test_bf16_trunk_shapes_with_conditioning(device, shape, packed):
     err = max_err(got, want)
     print(shape, packed, err)
     assert err <= BF16_TOL, err
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=["d64", "d240", "d256mha"])
+def test_bf16_tall_prefill_with_conditioning(device, shape):
+    """Prefill of 1024 rows x 32 tokens (32768 token rows): the fused layer kernel runs in
+    its taller row blocks, here with per-layer and value embeddings, partial FF chunks and
+    uneven column splits.  The last tokens' hidden states and the written keys / values
+    against the oracle's bf16 rounding path."""
+
+    config = TrunkConfig(**shape)
+    state = random_trunk(config, seed=6)
+    trunk = Trunk(config)
+    trunk.load_state_dict({k[len("trunk."):]: v for k, v in state.items()})
+    trunk = trunk.to(device)
+    ref = RefTrunk(state, ref_config_of(config), "bf16")
+    games, T = 1024, 32
+    native_cache, ref_cache = cache_pair(config, games, T, torch.bfloat16, device)
+    gen = torch.Generator().manual_seed(7)
+    raw = torch.randn(games, T, config.d_model, generator=gen)
+    ple_l = torch.randn(games, T, config.ple_width, generator=gen) if config.per_layer_dim else None
+    ve_l = torch.randn(games, T, config.value_width, generator=gen) if config.value_width else None
+    rows = torch.from_numpy(np.random.default_rng(2).permutation(games))
+    with torch.no_grad():
+        want = ref.forward_prefill(*ref.condition(raw, ple_l, ve_l), ref_cache, rows)
+        with autocast(device, "bf16"):
+            dev = lambda t: None if t is None else t.to(device)  # noqa: E731
+            got = trunk.forward_prefill(*trunk.condition(dev(raw), dev(ple_l), dev(ve_l)), native_cache, rows.to(device))
+    err = max_err(got, want)
+    sample = torch.tensor([0, 5, 511, 1023])
+
+    def rel_err(a, b):
+        # Cache entries are bf16 values of any magnitude (value embeddings are added before
+        # the write): a flipped rounding is one bf16 ulp, 2^-8 of the value, not 2e-2.
+        a, b = a.float().cpu(), b.float().cpu()
+        return ((a - b).abs() / b.abs().clamp(min=1.0)).max().item()
+
+    kv_err = max(rel_err(native_cache.k[l][sample], ref_cache.k[l][sample]) for l in range(config.n_layers))
+    kv_err = max(kv_err, max(rel_err(native_cache.v[l][sample], ref_cache.v[l][sample]) for l in range(config.n_layers)))
+    print(shape, err, kv_err)
+    assert err <= BF16_TOL, err
+    assert kv_err <= BF16_TOL, kv_err
