@@ -14,7 +14,8 @@ Also reported (one JSON line on stdout):
   * reference_gpu: the same restatement on the MI355X, eager and captured in a HIP graph;
   * sampling: device policy sampling of the step's logits (masked softmax + inverse CDF);
   * compaction: KVCache.copy_rows as self-play compacts the pool after games end;
-  * prefill: forward_prefill throughput at two shapes, beside the reference path on the GPU.
+  * prefill: forward_prefill throughput at two shapes, beside the reference path on the GPU;
+  * piquet_embed: the Piquet token embedder on one 4096-token wave, beside the reference path.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 10]
 """
@@ -290,6 +291,58 @@ def prefill_time(bench: Bench, with_reference: bool, reps: int = 3) -> dict:
     return out
 
 
+def piquet_embed_time(device: torch.device, with_reference: bool, tokens: int = 4096, reps: int = 20) -> dict:
+    """Piquet's token embedder (cardgym/games/piquet/model.py:286-341: 32 field lookups into
+    three tables, the card grid, the summary) for one rollout wave of `tokens` tokens of the
+    16-layer actor (d_model 256, PLE 16 x 64, alternating value embeddings, 2 grid blocks),
+    HIP events around `reps` calls; with `with_reference`, the oracle's restatement of the
+    reference's CUDA path (one-hot GEMM, unfused grid) on the same GPU."""
+
+    from card_playing_gym_amd.games.piquet import PiquetEmbedding, PiquetModelConfig
+
+    config = PiquetModelConfig()
+    tc = config.trunk()
+    module = PiquetEmbedding(config, tc.ple_width, tc.value_width).to(device)
+    g = torch.Generator().manual_seed(5)
+    from card_playing_gym_amd.games.piquet import CARD_VOCAB, FIELD_VOCAB, NUM_CARDS
+
+    fields = torch.stack([torch.randint(0, v, (tokens,), generator=g) for v in FIELD_VOCAB], dim=1)
+    codes = torch.randint(0, CARD_VOCAB, (tokens, NUM_CARDS), generator=g)
+    batch = torch.cat([fields, codes], dim=1).to(device)
+
+    def ours():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            module(batch)
+
+    def timed(fn) -> float:
+        fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / reps
+
+    us = timed(ours)
+    out = {"tokens": tokens, "us_per_wave": round(us, 2), "tokens_per_s": round(tokens / us * 1e6, 1)}
+    if with_reference:
+        from oracle.piquet import RefPiquetEmbedding
+
+        state = {"embedding." + k: v.detach() for k, v in module.state_dict().items()}
+        ref = RefPiquetEmbedding(state, config.card_layers, config.card_kernel, "bf16")
+
+        def theirs():
+            with torch.no_grad():
+                ref.forward(batch)
+
+        ref_us = timed(theirs)
+        out["reference_gpu_us_per_wave"] = round(ref_us, 2)
+        out["speedup"] = round(ref_us / us, 2)
+    return out
+
+
 def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) -> dict:
     """The oracle's reference path on the host cores, on `games` of the workload's games, at
     steps first .. first + steps (the middle of the timed range: context lengths there are
@@ -469,6 +522,8 @@ def main() -> int:
     log(f"bench: compaction {extra['compaction']}")
     extra["prefill"] = prefill_time(bench, with_reference=not args.no_baselines)
     log(f"bench: prefill {extra['prefill']}")
+    extra["piquet_embed"] = piquet_embed_time(bench.device, with_reference=not args.no_baselines)
+    log(f"bench: piquet embedder {extra['piquet_embed']}")
     if not args.no_baselines:
         del bench.cache
         torch.cuda.empty_cache()

@@ -75,6 +75,24 @@ class HeadsConfig(ctypes.Structure):
     ]
 
 
+class PiquetConfig(ctypes.Structure):
+    _fields_ = [
+        ("d_model", c_int32),
+        ("ple_width", c_int32),
+        ("value_width", c_int32),
+        ("table_rows", c_int32),
+        ("card_width", c_int32),
+        ("card_hidden", c_int32),
+        ("card_kernel", c_int32),
+        ("card_layers", c_int32),
+        ("eps", c_float),
+    ]
+
+
+class PiquetBlock(ctypes.Structure):
+    _fields_ = [(name, c_void_p) for name in ("norm", "along_w", "along_b", "across_w", "out_w", "out_b")]
+
+
 class LayerParams(ctypes.Structure):
     _fields_ = [
         ("ln_attn_w", c_void_p),
@@ -130,7 +148,7 @@ _SIGNATURES = {
         c_int32,
         [c_void_p, P(KVLayer), c_void_p, c_void_p, c_void_p, P(Ragged), c_void_p, c_void_p, c_size_t, c_void_p],
     ),
-    "cg_rmsnorm": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_int32, c_int32, c_void_p]),
+    "cg_rmsnorm": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_int32, c_void_p]),
     "cg_embed_rmsnorm": (
         c_int32,
         [c_void_p, c_int32, c_void_p, c_void_p, c_float, c_void_p, c_int32, c_int32, c_void_p, c_void_p],
@@ -141,7 +159,7 @@ _SIGNATURES = {
     ),
     "cg_linear_add_scale": (
         c_int32,
-        [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_float, c_int32, c_void_p],
+        [c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32, c_float, c_int32, c_void_p],
     ),
     "cg_heads_create": (
         c_int32, [P(HeadsConfig), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, P(c_void_p)],
@@ -156,6 +174,16 @@ _SIGNATURES = {
         c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_int32, c_void_p, c_void_p],
     ),
     "cg_advance_positions": (c_int32, [c_void_p, c_int32, c_int64, c_void_p]),
+    "cg_piquet_create": (
+        c_int32,
+        [P(PiquetConfig), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, P(c_void_p)],
+    ),
+    "cg_piquet_refresh": (c_int32, [c_void_p, c_void_p]),
+    "cg_piquet_destroy": (c_int32, [c_void_p]),
+    "cg_piquet_embed": (
+        c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
 }
 
 

@@ -34,7 +34,9 @@ struct GemmArgs {
   int64_t ld_ple;
   int32_t ple_off, ple_dim;
   float ple_scale;
-  const float *addend;
+  const void *addend;
+  int32_t add_dtype;  // CG_F32, or CG_BF16: the sum and the scaled sum round to bf16
+  int32_t round_c;    // round C + bias to bf16 first (an autocast Linear's output)
   int64_t ld_add;
   float scale;
   const float *ln_w, *ln_b;  // EPI_RESID_LN

@@ -247,7 +247,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs g) {
         if constexpr (EPI == EPI_STORE || EPI == EPI_GELU || EPI == EPI_SCALE_ADD) {
           float v = c;
           if constexpr (EPI == EPI_GELU) v = gelu_erf(c);
-          if constexpr (EPI == EPI_SCALE_ADD) v = (c + g.addend[int64_t(m) * g.ld_add + n]) * g.scale;
+          if constexpr (EPI == EPI_SCALE_ADD) {
+            const float cc = g.round_c ? to_f32(from_f32<bf16>(c)) : c;
+            const int64_t ai = int64_t(m) * g.ld_add + n;
+            if (g.add_dtype == CG_BF16) {
+              const float sum = to_f32(from_f32<bf16>(cc + to_f32(static_cast<const bf16 *>(g.addend)[ai])));
+              v = to_f32(from_f32<bf16>(sum * g.scale));
+            } else {
+              v = (cc + static_cast<const float *>(g.addend)[ai]) * g.scale;
+            }
+          }
           const int64_t o = int64_t(m) * g.ldo + n;
           if (g.out_dtype == CG_BF16) static_cast<bf16 *>(g.out)[o] = from_f32<bf16>(v);
           else static_cast<float *>(g.out)[o] = v;
@@ -424,14 +433,16 @@ extern "C" int cg_linear(const float *x, const float *w, const float *bias, floa
   });
 }
 
-extern "C" int cg_linear_add_scale(const float *x, const float *w, const float *addend, float *y,
-                                   int32_t m, int32_t n, int32_t k, float scale,
+extern "C" int cg_linear_add_scale(const float *x, const float *w, const void *addend, int32_t addend_dtype,
+                                   float *y, int32_t m, int32_t n, int32_t k, float scale,
                                    int32_t compute_dtype, void *stream) {
   return guarded([&] {
     if (m == 0) return;
     CG_REQUIRE(x && w && addend && y, CG_ERR_INVALID, "x, w, addend and y are required");
     CG_REQUIRE(compute_dtype == CG_F32 || compute_dtype == CG_BF16, CG_ERR_INVALID,
                "compute dtype must be CG_F32 or CG_BF16");
+    CG_REQUIRE(addend_dtype == CG_F32 || addend_dtype == CG_BF16, CG_ERR_INVALID,
+               "addend dtype must be CG_F32 or CG_BF16");
     GemmArgs g{};
     g.M = m;
     g.N = n;
@@ -442,6 +453,8 @@ extern "C" int cg_linear_add_scale(const float *x, const float *w, const float *
     g.W = w;
     g.epi = EPI_SCALE_ADD;
     g.addend = addend;
+    g.add_dtype = addend_dtype;
+    g.round_c = compute_dtype == CG_BF16;
     g.ld_add = n;
     g.scale = scale;
     g.out = y;

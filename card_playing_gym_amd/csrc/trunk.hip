@@ -122,7 +122,10 @@ __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t
 }
 
 // One wave per row: y = rms_norm(src row) * gain; src row = table[ids[row]] or x[row].
-__global__ void rmsnorm_rows_kernel(const float *__restrict__ x, const float *__restrict__ table,
+// XT float: fp32 rows; XT bf16: bf16 rows whose normalised value rounds to bf16 before the
+// gain (rms_norm(x.float()).to(x.dtype) * gain).
+template <typename XT>
+__global__ void rmsnorm_rows_kernel(const XT *__restrict__ x, const float *__restrict__ table,
                                     int32_t vocab, const int64_t *__restrict__ ids,
                                     const float *__restrict__ gain, float eps, float *__restrict__ y,
                                     int32_t n, int32_t d, int32_t *__restrict__ flag) {
@@ -130,7 +133,7 @@ __global__ void rmsnorm_rows_kernel(const float *__restrict__ x, const float *__
   const int lane = threadIdx.x & 63;
   if (row >= n) return;
   float *out = y + int64_t(row) * d;
-  const float *in;
+  float s = 0.f;
   if (ids) {
     const int64_t id = ids[row];
     if (id < 0 || id >= vocab) {
@@ -138,14 +141,19 @@ __global__ void rmsnorm_rows_kernel(const float *__restrict__ x, const float *__
       if (flag && lane == 0) flag[0] = 1;
       return;
     }
-    in = table + id * d;
-  } else {
-    in = x + int64_t(row) * d;
+    const float *in = table + id * d;
+    for (int k = lane; k < d; k += 64) s = fmaf(in[k], in[k], s);
+    const float r = rsqrtf(wave_sum(s) / float(d) + eps);
+    for (int k = lane; k < d; k += 64) out[k] = in[k] * r * gain[k];
+    return;
   }
-  float s = 0.f;
-  for (int k = lane; k < d; k += 64) s = fmaf(in[k], in[k], s);
+  const XT *in = x + int64_t(row) * d;
+  for (int k = lane; k < d; k += 64) {
+    const float v = to_f32(in[k]);
+    s = fmaf(v, v, s);
+  }
   const float r = rsqrtf(wave_sum(s) / float(d) + eps);
-  for (int k = lane; k < d; k += 64) out[k] = in[k] * r * gain[k];
+  for (int k = lane; k < d; k += 64) out[k] = to_f32(from_f32<XT>(to_f32(in[k]) * r)) * gain[k];
 }
 
 // fp32 -> bf16 (round to nearest even) weight copies.
@@ -560,14 +568,19 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
   });
 }
 
-int cg_rmsnorm(const float *x, const float *gain, float eps, float *y, int32_t n, int32_t d,
+int cg_rmsnorm(const void *x, int32_t x_dtype, const float *gain, float eps, float *y, int32_t n, int32_t d,
                void *stream) {
   return guarded([&] {
     CG_REQUIRE(x && gain && y, CG_ERR_INVALID, "x, gain and y are required");
     CG_REQUIRE(n >= 0 && d > 0, CG_ERR_INVALID, "bad sizes");
+    CG_REQUIRE(x_dtype == CG_F32 || x_dtype == CG_BF16, CG_ERR_INVALID, "x dtype must be CG_F32 or CG_BF16");
     if (n == 0) return;
-    rmsnorm_rows_kernel<<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
-        x, nullptr, 0, nullptr, gain, eps, y, n, d, nullptr);
+    if (x_dtype == CG_BF16)
+      rmsnorm_rows_kernel<bf16><<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
+          static_cast<const bf16 *>(x), nullptr, 0, nullptr, gain, eps, y, n, d, nullptr);
+    else
+      rmsnorm_rows_kernel<float><<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
+          static_cast<const float *>(x), nullptr, 0, nullptr, gain, eps, y, n, d, nullptr);
     CG_LAUNCHED();
   });
 }
@@ -578,7 +591,7 @@ int cg_embed_rmsnorm(const float *table, int32_t vocab, const int64_t *ids, cons
     CG_REQUIRE(table && ids && gain && y, CG_ERR_INVALID, "table, ids, gain and y are required");
     CG_REQUIRE(n >= 0 && d > 0 && vocab > 0, CG_ERR_INVALID, "bad sizes");
     if (n == 0) return;
-    rmsnorm_rows_kernel<<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
+    rmsnorm_rows_kernel<float><<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
         nullptr, table, vocab, ids, gain, eps, y, n, d, flag);
     CG_LAUNCHED();
   });

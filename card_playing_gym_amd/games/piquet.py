@@ -1,0 +1,249 @@
+"""Piquet's token embedder on the HIP path (API of cardgym.games.piquet.model).
+
+``PiquetEmbedding`` keeps the reference's module tree and parameter names
+(cardgym/games/piquet/model.py:114-341: ``fields``, ``ple_fields``, ``value_fields``,
+``grid.code``, ``grid.rank``, ``grid.blocks.{i}.{norm, along_rank, across_suits, out}``,
+``grid.norm``, ``grid.summary``), so a PiquetActor state dict's ``embedding.*`` entries load
+unchanged, and returns what the reference's forward returns under bf16 autocast: the
+trunk input sum, the per-layer and value lookups (bf16), keeping the per-card features
+for the card heads (``kept``, fp32).  The whole forward is two launches of
+``cg_piquet_embed`` (csrc/piquet.hip); there is no CPU path and no other precision: it
+runs on a ROCm device under ``torch.autocast("cuda", dtype=torch.bfloat16)``, the
+precision the reference's CUDA rollouts use, and raises otherwise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from .. import _native as nat
+from ..nn.kv_cache import require_device, stream_handle
+from ..nn.trunk import TrunkConfig
+
+# The token layout of cardgym/games/piquet/tokens.py:108-152 and the card numbering of
+# cards.py:11-14, 26-35 (card = suit * 8 + rank).
+NUM_SUITS, NUM_RANKS = 4, 8
+NUM_CARDS = NUM_SUITS * NUM_RANKS
+NUM_FIELDS = 32
+CARD_START = NUM_FIELDS
+CARD_VOCAB = 12
+_HEADS, _TRICKS, _TALON = 3, 12, 8  # engine.py:50-56
+_TOTAL_VOCAB = 120 + 21
+_LEAD_VOCAB = 2 * (60 + 14) + 1
+FIELD_VOCAB = (
+    8, 1 + _HEADS, 3, 2, NUM_CARDS + 1, 9, 9, 4, 4, 9, 76, 9, 3, 4, 64, 5, 3,
+    _TRICKS + 1, 3, 5, _TRICKS + 1, _TRICKS + 1, 100, 100, _TOTAL_VOCAB, _TOTAL_VOCAB,
+    6, 2, _TALON + 1, 16, 4, _LEAD_VOCAB,
+)
+FIELD_OFFSETS = tuple(sum(FIELD_VOCAB[:i]) for i in range(NUM_FIELDS))
+CARD_RANKS = tuple(card & 7 for card in range(NUM_CARDS))
+
+
+@dataclass(frozen=True)
+class PiquetModelConfig:
+    """The [model] section's embedder and trunk fields (model.py:79-112, same defaults)."""
+
+    d_model: int = 256
+    n_layers: int = 16
+    n_heads: int = 8
+    n_kv_heads: int = 2
+    d_ff: int = 512
+    per_layer_dim: int = 64
+    value_embeddings: str = "alternating"
+    card_width: int = 32
+    card_hidden: int = 64
+    card_layers: int = 2
+    card_kernel: int = 3
+
+    def trunk(self) -> TrunkConfig:
+        return TrunkConfig(
+            d_model=self.d_model, n_layers=self.n_layers, n_heads=self.n_heads, n_kv_heads=self.n_kv_heads,
+            d_ff=self.d_ff, per_layer_dim=self.per_layer_dim, value_embeddings=self.value_embeddings,
+            input_norm=True,
+        )
+
+
+def _init(module: nn.Module) -> None:
+    """N(0, 0.02) weights and zero biases (cardgym/nn/trunk.py:93-101)."""
+
+    if isinstance(module, (nn.Linear, nn.Conv1d)):
+        nn.init.normal_(module.weight, std=0.02)
+        if module.bias is not None:
+            nn.init.zeros_(module.bias)
+    elif isinstance(module, nn.Embedding):
+        nn.init.normal_(module.weight, std=0.02)
+
+
+class GridNorm(nn.Module):
+    """RMSNorm with a gain (model.py:114-125); evaluated inside the grid kernel."""
+
+    def __init__(self, width: int, eps: float = 1e-5) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(width))
+        self.eps = eps
+
+
+class GridBlock(nn.Module):
+    """Parameters of one grid block (model.py:128-151); evaluated inside the grid kernel."""
+
+    def __init__(self, width: int, hidden: int, kernel: int) -> None:
+        super().__init__()
+        self.kernel = kernel
+        self.norm = GridNorm(width)
+        self.along_rank = nn.Conv1d(width, hidden, kernel)
+        self.across_suits = nn.Linear(width, hidden, bias=False)
+        self.out = nn.Linear(hidden, width)
+
+
+class CardGrid(nn.Module):
+    """Parameters of the card grid (model.py:180-211)."""
+
+    def __init__(self, config: PiquetModelConfig) -> None:
+        super().__init__()
+        width = config.card_width
+        self.width = width
+        self.code = nn.Embedding(CARD_VOCAB, width)
+        self.rank = nn.Embedding(NUM_RANKS, width)
+        self.blocks = nn.ModuleList(
+            GridBlock(width, config.card_hidden, config.card_kernel) for _ in range(config.card_layers)
+        )
+        self.norm = GridNorm(width)
+        self.summary = nn.Linear(NUM_CARDS * width, config.d_model, bias=False)
+        for module in (self.code, self.rank, *self.blocks):
+            module.apply(_init)
+        with torch.no_grad():
+            for block in self.blocks:
+                block.out.weight.mul_(1.0 / max(len(self.blocks), 1) ** 0.5)
+        nn.init.normal_(self.summary.weight, std=0.02 * (NUM_FIELDS / (NUM_CARDS * width)) ** 0.5)
+
+
+class PiquetEmbedding(nn.Module):
+    """Token fields plus the card-grid summary (model.py:286-341), on the HIP path."""
+
+    def __init__(self, config: PiquetModelConfig, ple_width: int, value_width: int) -> None:
+        super().__init__()
+        self.config = config
+        self.kept: torch.Tensor | None = None
+        rows = sum(FIELD_VOCAB)
+        self.fields = nn.Embedding(rows, config.d_model)
+        _init(self.fields)
+        self.ple_fields = nn.Embedding(rows, ple_width) if ple_width else None
+        self.value_fields = nn.Embedding(rows, value_width) if value_width else None
+        for table in (self.ple_fields, self.value_fields):
+            if table is not None:
+                nn.init.zeros_(table.weight)
+        self.grid = CardGrid(config)
+        self._native: _NativePiquet | None = None
+
+    def _params(self) -> list[torch.Tensor]:
+        g = self.grid
+        out = [self.fields.weight, g.code.weight, g.rank.weight, g.norm.weight, g.summary.weight]
+        out += [t.weight for t in (self.ple_fields, self.value_fields) if t is not None]
+        for b in g.blocks:
+            out += [b.norm.weight, b.along_rank.weight, b.along_rank.bias, b.across_suits.weight, b.out.weight,
+                    b.out.bias]
+        for t in out:
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError("embedder parameters must be contiguous float32 tensors")
+        return out
+
+    def native(self, stream: int) -> _NativePiquet:
+        params = self._params()
+        if self._native is None or not self._native.sync(params, stream):
+            if self._native is not None:
+                self._native.close()
+            self._native = _NativePiquet(self, params)
+        return self._native
+
+    def forward(self, tokens: torch.Tensor):
+        """(x, ple lookup, value lookup) for [..., 64] tokens; ``kept`` = cards [..., 32, w]."""
+
+        require_device(tokens, self.fields.weight)
+        device = tokens.device
+        if not (torch.is_autocast_enabled(device.type) and torch.get_autocast_dtype(device.type) == torch.bfloat16):
+            raise RuntimeError("the HIP Piquet embedder runs under torch.autocast(device, dtype=torch.bfloat16) only")
+        lead = tokens.shape[:-1]
+        flat = tokens.reshape(-1, tokens.shape[-1])
+        if flat.shape[1] != NUM_FIELDS + NUM_CARDS:
+            raise ValueError("a Piquet token holds 32 fields and 32 card codes")
+        flat = flat.to(torch.int64).contiguous()
+        n = flat.shape[0]
+        c = self.config
+        x = torch.empty((n, c.d_model), device=device, dtype=torch.bfloat16)
+        ple = None if self.ple_fields is None else torch.empty((n, self.ple_fields.embedding_dim), device=device,
+                                                               dtype=torch.bfloat16)
+        values = None if self.value_fields is None else torch.empty((n, self.value_fields.embedding_dim),
+                                                                    device=device, dtype=torch.bfloat16)
+        cards = torch.empty((n, NUM_CARDS, c.card_width), device=device, dtype=torch.float32)
+        stream = stream_handle(device)
+        handle = self.native(stream)
+        nat.call(
+            "cg_piquet_embed", handle.handle, flat.data_ptr(), flat.shape[1], n, x.data_ptr(),
+            None if ple is None else ple.data_ptr(), None if values is None else values.data_ptr(),
+            cards.data_ptr(), None, stream,
+        )
+        self.kept = cards.view(*lead, NUM_CARDS, c.card_width)
+        return (
+            x.view(*lead, -1),
+            None if ple is None else ple.view(*lead, -1),
+            None if values is None else values.view(*lead, -1),
+        )
+
+
+class _NativePiquet:
+    """A ``cg_piquet`` handle over the embedder's parameters (bf16 copies of the tables and
+    the grid's matrices, re-derived when a parameter changes in place)."""
+
+    def __init__(self, module: PiquetEmbedding, params: list[torch.Tensor]) -> None:
+        self.params = params
+        self.signature = tuple(t.data_ptr() for t in params)
+        self.versions = tuple(t._version for t in params)
+        c = module.config
+        g = module.grid
+        cfg = nat.PiquetConfig(
+            c.d_model, 0 if module.ple_fields is None else module.ple_fields.embedding_dim,
+            0 if module.value_fields is None else module.value_fields.embedding_dim, sum(FIELD_VOCAB),
+            c.card_width, c.card_hidden, c.card_kernel, c.card_layers, g.norm.eps,
+        )
+        blocks = (nat.PiquetBlock * max(len(g.blocks), 1))()
+        for i, b in enumerate(g.blocks):
+            blocks[i] = nat.PiquetBlock(
+                b.norm.weight.data_ptr(), b.along_rank.weight.data_ptr(), b.along_rank.bias.data_ptr(),
+                b.across_suits.weight.data_ptr(), b.out.weight.data_ptr(), b.out.bias.data_ptr(),
+            )
+        offsets = (ctypes.c_int32 * NUM_FIELDS)(*FIELD_OFFSETS)
+        handle = ctypes.c_void_p()
+        nat.call(
+            "cg_piquet_create", ctypes.byref(cfg), offsets, module.fields.weight.data_ptr(),
+            None if module.ple_fields is None else module.ple_fields.weight.data_ptr(),
+            None if module.value_fields is None else module.value_fields.weight.data_ptr(),
+            g.code.weight.data_ptr(), g.rank.weight.data_ptr(), blocks, g.norm.weight.data_ptr(),
+            g.summary.weight.data_ptr(), ctypes.byref(handle),
+        )
+        self.handle = handle
+
+    def sync(self, params: list[torch.Tensor], stream: int) -> bool:
+        if tuple(t.data_ptr() for t in params) != self.signature or any(a is not b for a, b in zip(params, self.params)):
+            return False
+        versions = tuple(t._version for t in params)
+        if versions != self.versions:
+            nat.call("cg_piquet_refresh", self.handle, stream)
+            self.versions = versions
+        return True
+
+    def close(self) -> None:
+        if self.handle:
+            try:
+                nat.lib().cg_piquet_destroy(self.handle)
+            finally:
+                self.handle = ctypes.c_void_p()
+
+    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -103,11 +103,15 @@ class RMSNorm(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         require_device(x)
-        flat = x.reshape(-1, x.shape[-1]).float().contiguous()
-        out = torch.empty_like(flat)
+        # A bf16 input (a game embedder's autocast sum) keeps its dtype: the kernel rounds
+        # the normalised value to bf16 before the gain, as .to(x.dtype) does.
+        bf16 = x.dtype == torch.bfloat16
+        flat = x.reshape(-1, x.shape[-1])
+        flat = (flat if bf16 else flat.float()).contiguous()
+        out = torch.empty(flat.shape, device=flat.device, dtype=torch.float32)
         nat.call(
-            "cg_rmsnorm", flat.data_ptr(), _param(self.weight).data_ptr(), float(self.eps), out.data_ptr(),
-            flat.shape[0], flat.shape[1], stream_handle(x.device),
+            "cg_rmsnorm", flat.data_ptr(), nat.CG_BF16 if bf16 else nat.CG_F32, _param(self.weight).data_ptr(),
+            float(self.eps), out.data_ptr(), flat.shape[0], flat.shape[1], stream_handle(x.device),
         )
         return out.view(x.shape)
 
@@ -286,12 +290,17 @@ class Trunk(nn.Module):
             if ple_lookup is None:
                 raise ValueError("This trunk expects a per-layer embedding lookup.")
             flat = x.reshape(-1, x.shape[-1]).contiguous()
-            lookup = ple_lookup.reshape(flat.shape[0], -1).float().contiguous()
-            out = torch.empty_like(lookup)
+            # A bf16 lookup (a game embedder under autocast) is read as bf16 and the sum and
+            # its scaling round to bf16, as the reference's bf16 tensor arithmetic does.
+            bf16 = ple_lookup.dtype == torch.bfloat16
+            lookup = ple_lookup.reshape(flat.shape[0], -1)
+            lookup = (lookup if bf16 else lookup.float()).contiguous()
+            out = torch.empty(lookup.shape, device=lookup.device, dtype=torch.float32)
             nat.call(
                 "cg_linear_add_scale", flat.data_ptr(), _param(self.ple_context.weight).data_ptr(),
-                lookup.data_ptr(), out.data_ptr(), flat.shape[0], lookup.shape[1], flat.shape[1],
-                1.0 / math.sqrt(2.0), compute_dtype_code(x.device), stream_handle(x.device),
+                lookup.data_ptr(), nat.CG_BF16 if bf16 else nat.CG_F32, out.data_ptr(), flat.shape[0],
+                lookup.shape[1], flat.shape[1], 1.0 / math.sqrt(2.0), compute_dtype_code(x.device),
+                stream_handle(x.device),
             )
             ple = out.view(*lead, self.config.n_layers, self.config.per_layer_dim)
         values = None

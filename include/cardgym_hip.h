@@ -225,8 +225,10 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
 
 /* ---- conditioning, embedding and heads ------------------------------------------ */
 
-/* RMSNorm (cardgym/nn/trunk.py:104-115): y = rms_norm(x, eps) * gain, rows of width d. */
-int cg_rmsnorm(const float *x, const float *gain, float eps, float *y, int32_t n, int32_t d,
+/* RMSNorm (cardgym/nn/trunk.py:104-115): y = rms_norm(x, eps).to(x.dtype) * gain, rows of
+ * width d, fp32 out.  x_dtype CG_F32 (x float) or CG_BF16 (x bf16: the normalised value is
+ * rounded to bf16 before the gain, as .to(x.dtype) does). */
+int cg_rmsnorm(const void *x, int32_t x_dtype, const float *gain, float eps, float *y, int32_t n, int32_t d,
                void *stream);
 
 /* Embedding lookup then RMSNorm: y[i] = rms_norm(table[ids[i]]) * gain, the synthetic
@@ -244,9 +246,11 @@ int cg_linear(const float *x, const float *w, const float *bias, float *y, int32
 
 /* y = (x @ w^T + addend) * scale for fp32 x [m, k], w [n, k], addend [m, n]: the per-layer
  * embedding stream of Trunk.condition, ple = (ple_lookup + ple_context(x)) / sqrt(2)
- * (cardgym/nn/trunk.py:301-306). */
-int cg_linear_add_scale(const float *x, const float *w, const float *addend, float *y, int32_t m,
-                        int32_t n, int32_t k, float scale, int32_t compute_dtype, void *stream);
+ * (cardgym/nn/trunk.py:301-306).  compute_dtype CG_BF16 (autocast) rounds the projection to
+ * bf16 as the Linear's output; addend_dtype CG_BF16 (a bf16 lookup) also rounds the sum and
+ * the scaled sum to bf16, as bf16 tensor arithmetic does.  The product itself is fp32. */
+int cg_linear_add_scale(const float *x, const float *w, const void *addend, int32_t addend_dtype, float *y,
+                        int32_t m, int32_t n, int32_t k, float scale, int32_t compute_dtype, void *stream);
 
 /* ---- policy and value heads ------------------------------------------------------ */
 
@@ -296,6 +300,46 @@ int cg_sample_rows(const float *probs, int64_t ld_probs, const uint8_t *mask, in
 /* Adds `delta` to every entry of the int64 array a (n entries): the synthetic driver's
  * "every game appended one token" position update, kept on the device. */
 int cg_advance_positions(int64_t *positions, int32_t n, int64_t delta, void *stream);
+
+/* ---- Piquet's token embedder (cardgym/games/piquet/model.py:128-341) ----------------------
+ * PiquetEmbedding.forward for [n, 64] int64 tokens (32 fields, then 32 card codes):
+ *   x      = sum of the 32 field rows of `fields` (row = token field + field_offsets[f])
+ *            + CardGrid's summary of the cards                      -> bf16 [n, d_model]
+ *   ple    = the same rows of `ple_fields`  (when ple_width > 0)     -> bf16 [n, ple_width]
+ *   values = the same rows of `value_fields` (when value_width > 0)  -> bf16 [n, value_width]
+ *   cards  = CardGrid.cards: code + rank embeddings, card_layers GridBlocks (rank
+ *            convolution zero-padded, suit pooling, GELU MLP, residual), GridNorm
+ *                                                                    -> fp32 [n, 32, 32]
+ * with bf16 autocast's rounding (the CUDA one-hot GEMM path of model.py:255-270 for the
+ * fields).  Parameters are the reference's fp32 tensors in their own layouts; the handle
+ * keeps bf16 copies of the tables and the grid's matrices (cg_piquet_refresh after they
+ * change) and reads the small vectors in place.  Field ids outside the table and card codes
+ * outside [0, 12) contribute zero and set flag[0] = 1 (flag may be NULL). */
+typedef struct {
+  int32_t d_model, ple_width, value_width, table_rows;
+  int32_t card_width, card_hidden, card_kernel, card_layers;
+  float eps;
+} cg_piquet_config;
+
+typedef struct { /* one GridBlock (model.py:128-151) */
+  const float *norm;     /* [width] */
+  const float *along_w;  /* [hidden, width, kernel] (Conv1d) */
+  const float *along_b;  /* [hidden] */
+  const float *across_w; /* [hidden, width] */
+  const float *out_w;    /* [width, hidden] */
+  const float *out_b;    /* [width] */
+} cg_piquet_block;
+
+typedef struct cg_piquet cg_piquet;
+
+int cg_piquet_create(const cg_piquet_config *config, const int32_t *field_offsets, const float *fields,
+                     const float *ple_fields, const float *value_fields, const float *code, const float *rank,
+                     const cg_piquet_block *blocks, const float *grid_norm, const float *summary,
+                     cg_piquet **out);
+int cg_piquet_refresh(cg_piquet *embedder, void *stream);
+int cg_piquet_destroy(cg_piquet *embedder);
+int cg_piquet_embed(const cg_piquet *embedder, const int64_t *tokens, int64_t ld_tokens, int32_t n, void *x,
+                    void *ple, void *values, float *cards, int32_t *flag, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,171 @@
+"""The HIP Piquet embedder (csrc/piquet.hip) against the oracle's restatement of
+cardgym/games/piquet/model.py:128-341 under bf16 autocast.
+
+Bar: the bf16 tolerance of the path, |got - want| <= 2e-2 * max(1, |want|) for the trunk
+input sum, the per-layer and value lookups and the per-card features (both sides round
+the same products to bf16; accumulation order differs, so a rounding may flip by one bf16
+step).  Plus the model's own symmetry on the device: permuting suits permutes the cards.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from card_playing_gym_amd import _native as nat
+from card_playing_gym_amd.games.piquet import (
+    CARD_START, FIELD_VOCAB, NUM_CARDS, NUM_RANKS, PiquetEmbedding, PiquetModelConfig,
+)
+from oracle.piquet import RefPiquetEmbedding, random_state, random_tokens
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def rel_err(got: torch.Tensor, want: torch.Tensor) -> float:
+    got, want = got.detach().float().cpu(), want.detach().float().cpu()
+    return ((got - want).abs() / want.abs().clamp(min=1.0)).max().item()
+
+
+def twins(config: PiquetModelConfig, ple: int, values: int, device, seed: int = 0):
+    state = random_state(config.d_model, ple, values, width=config.card_width, hidden=config.card_hidden,
+                         layers=config.card_layers, kernel=config.card_kernel, seed=seed)
+    module = PiquetEmbedding(config, ple, values)
+    module.load_state_dict({k[len("embedding."):]: v for k, v in state.items()})
+    ref = RefPiquetEmbedding(state, config.card_layers, config.card_kernel, "bf16")
+    return module.to(device), ref
+
+
+def embed(module, tokens, device):
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        x, ple, values = module(tokens.to(device))
+    return x, ple, values, module.kept
+
+
+CASES = [
+    # (d_model, ple, values, hidden, layers, kernel, tokens)
+    (256, 1024, 512, 64, 2, 3, 4096),  # the 16-layer actor's embedder, one rollout wave
+    (256, 1024, 512, 64, 2, 3, 17),    # a partial block of 16 tokens
+    (128, 0, 0, 32, 1, 5, 40),
+    (512, 64, 0, 64, 4, 7, 33),
+    (384, 0, 128, 32, 0, 1, 16),       # no grid blocks: the final norm alone
+]
+
+
+@pytest.mark.parametrize("d,ple,values,hidden,layers,kernel,n", CASES)
+def test_embedder_matches_oracle(device, d, ple, values, hidden, layers, kernel, n):
+    config = PiquetModelConfig(d_model=d, card_hidden=hidden, card_layers=layers, card_kernel=kernel)
+    module, ref = twins(config, ple, values, device, seed=layers * 10 + kernel)
+    tokens = random_tokens(n, seed=n)
+    got = embed(module, tokens, device)
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        want = ref.forward(tokens)
+    for name, g, w in zip(("x", "ple", "values", "cards"), got, want):
+        if w is None:
+            assert g is None, name
+            continue
+        assert g.shape == w.shape and g.dtype == w.dtype, (name, g.shape, w.shape, g.dtype, w.dtype)
+        err = rel_err(g, w)
+        assert err <= TOL, (name, err)
+
+
+def test_suit_permutation_permutes_cards(device):
+    """The grid is suit-equivariant (model.py:1-14): permuting the suits of every token's
+    card codes permutes its per-card features the same way, on the device."""
+
+    config = PiquetModelConfig()
+    module, _ = twins(config, 1024, 512, device, seed=5)
+    tokens = random_tokens(64, seed=6)
+    perm = torch.tensor([3, 1, 0, 2])
+    card_perm = (perm[:, None] * NUM_RANKS + torch.arange(NUM_RANKS)).reshape(NUM_CARDS)
+    moved = tokens.clone()
+    moved[:, CARD_START:] = tokens[:, CARD_START:][:, card_perm]
+    base = embed(module, tokens, device)[3].cpu()
+    again = embed(module, moved, device)[3].cpu()
+    assert rel_err(again, base[:, card_perm]) <= TOL
+
+
+def test_bad_ids_and_codes_are_flagged(device):
+    config = PiquetModelConfig(card_layers=1)
+    module, ref = twins(config, 0, 0, device, seed=7)
+    tokens = random_tokens(20, seed=8)
+    bad = tokens.clone()
+    bad[3, 31] = 10_000  # past every field row
+    bad[5, CARD_START + 7] = 12  # no such card code
+    flat = bad.to(device)
+    flag = torch.zeros(1, dtype=torch.int32, device=device)
+    x = torch.empty((20, config.d_model), dtype=torch.bfloat16, device=device)
+    cards = torch.empty((20, NUM_CARDS, 32), device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    handle = module.native(stream)
+    nat.call("cg_piquet_embed", handle.handle, flat.data_ptr(), 64, 20, x.data_ptr(), None, None, cards.data_ptr(),
+             flag.data_ptr(), stream)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+    # The other tokens are untouched by the bad ones.
+    good = [i for i in range(20) if i not in (3, 5)]
+    want = ref.forward(tokens)
+    assert rel_err(x.cpu()[good], want[0][good]) <= TOL
+    assert rel_err(cards.cpu()[good], want[3][good]) <= TOL
+
+
+def test_refresh_after_an_optimiser_step(device):
+    config = PiquetModelConfig(card_layers=2)
+    module, _ = twins(config, 64, 0, device, seed=9)
+    tokens = random_tokens(32, seed=10)
+    before = embed(module, tokens, device)
+    with torch.no_grad():
+        module.grid.blocks[1].out.weight.mul_(2.0)
+        module.fields.weight.add_(0.5)
+    after = embed(module, tokens, device)
+    state = {"embedding." + k: v.detach().cpu() for k, v in module.state_dict().items()}
+    ref = RefPiquetEmbedding(state, 2, 3, "bf16")
+    want = ref.forward(tokens)
+    assert rel_err(after[0], want[0]) <= TOL and rel_err(after[3], want[3]) <= TOL
+    assert rel_err(before[0], want[0]) > TOL
+
+
+def test_piquet_trunk_step(device):
+    """One decode step of a Piquet-shaped trunk (PLE 64, alternating value embeddings,
+    d_ff 512; 4 layers) fed by the device embedder, against the oracle's embedder + trunk."""
+
+    from card_playing_gym_amd.nn.kv_cache import KVCache
+    from card_playing_gym_amd.nn.trunk import Trunk
+    from oracle.reference_path import RefCache, RefTrunk, ref_config_of
+    from tests.helpers import random_trunk
+
+    config = PiquetModelConfig(n_layers=4)
+    tc = config.trunk()
+    module, ref_embed = twins(config, tc.ple_width, tc.value_width, device, seed=11)
+    state = random_trunk(tc, seed=12)
+    trunk = Trunk(tc)
+    trunk.load_state_dict({k[len("trunk."):]: v for k, v in state.items()})
+    trunk = trunk.to(device)
+    ref = RefTrunk(state, ref_config_of(tc), "bf16")
+    games, max_len = 64, 32
+    rng = np.random.default_rng(13)
+    lengths = torch.from_numpy(rng.integers(0, 20, size=games))
+    cache = KVCache(n_layers=tc.n_layers, kv_heads=tc.n_kv_heads, head_dim=tc.head_dim, capacity=games,
+                    max_len=max_len, device=device, dtype=torch.bfloat16)
+    ref_cache = RefCache(tc.n_layers, tc.n_kv_heads, tc.head_dim, games, max_len, torch.bfloat16)
+    g = torch.Generator().manual_seed(14)
+    for layer in range(tc.n_layers):
+        k = torch.randn(games, tc.n_kv_heads, max_len, tc.head_dim, generator=g).bfloat16()
+        v = torch.randn(games, tc.n_kv_heads, max_len, tc.head_dim, generator=g).bfloat16()
+        cache.k[layer].copy_(k.to(device))
+        cache.v[layer].copy_(v.to(device))
+        ref_cache.k[layer].copy_(k)
+        ref_cache.v[layer].copy_(v)
+    tokens = random_tokens(games, seed=15).view(games, 1, 64)
+    readout = torch.zeros(games, dtype=torch.int64)
+    with torch.no_grad():
+        rx, rple, rvalues, _ = ref_embed.forward(tokens)
+        want = ref.forward_ragged(*ref.condition(rx, rple, rvalues), ref_cache, lengths, readout)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            x, ple, values = module(tokens.to(device))
+            got = trunk.forward_ragged(*trunk.condition(x, ple, values), cache, lengths.to(device), readout.to(device))
+    err = (got.float().cpu() - want.float()).abs().max().item()
+    assert err <= TOL, err

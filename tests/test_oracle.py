@@ -394,3 +394,90 @@ def test_pairwise_order_matches_numpy_sum():
         for v in row:
             run = np.float32(run + v)
         assert np.cumsum(row)[-1].tobytes() == run.tobytes(), n
+
+
+# ---- Piquet embedder (oracle/piquet.py) ----------------------------------------------------
+
+def _piquet(precision="fp32", layers=2, kernel=3, ple=64, values=32, seed=0):
+    from oracle.piquet import RefPiquetEmbedding, random_state
+
+    state = random_state(64, ple, values, layers=layers, kernel=kernel, seed=seed)
+    return RefPiquetEmbedding({k: v.double() for k, v in state.items()} if precision == "fp64" else state,
+                              layers, kernel, "fp32" if precision == "fp64" else precision)
+
+
+@pytest.mark.parametrize("kernel", [1, 3, 5])
+def test_piquet_rank_convolution_is_a_zero_padded_conv1d(kernel):
+    """The block-Toeplitz GEMM equals torch's conv1d along the ranks of each suit, with
+    zero padding (no wrap-around: a rank-0 card never sees rank 7)."""
+
+    from oracle.piquet import NUM_RANKS, NUM_SUITS
+
+    ref = _piquet("fp64", kernel=kernel)
+    g = torch.Generator().manual_seed(1)
+    rows = torch.randn(5, NUM_SUITS, NUM_RANKS * 32, generator=g, dtype=torch.float64)
+    got = ref.along(0, rows)
+    w = ref.s["grid.blocks.0.along_rank.weight"]
+    b = ref.s["grid.blocks.0.along_rank.bias"]
+    seq = rows.view(5 * NUM_SUITS, NUM_RANKS, 32).transpose(1, 2)  # [N, width, ranks]
+    want = torch.nn.functional.conv1d(seq, w, b, padding=kernel // 2)  # [N, hidden, ranks]
+    want = want.transpose(1, 2).reshape(5, NUM_SUITS, -1)
+    assert torch.allclose(got, want, atol=1e-12)
+    if kernel > 1:
+        # A wrapped (circular) convolution differs at the edge ranks.
+        wrapped = torch.nn.functional.conv1d(torch.nn.functional.pad(seq, (kernel // 2,) * 2, mode="circular"), w, b)
+        assert not torch.allclose(got, wrapped.transpose(1, 2).reshape(5, NUM_SUITS, -1), atol=1e-6)
+
+
+def test_piquet_pooling_norm_and_field_sums():
+    """Suit pooling is the mean over suits; GridNorm is x / sqrt(mean x^2 + eps) * w; the
+    one-hot GEMM equals embedding_bag's sums (the reference's CPU path, model.py:248-250)."""
+
+    from oracle.piquet import FIELD_OFFSETS, NUM_FIELDS, NUM_RANKS, NUM_SUITS, random_tokens
+
+    ref = _piquet("fp64")
+    g = torch.Generator().manual_seed(2)
+    rows = torch.randn(3, NUM_SUITS, NUM_RANKS * 32, generator=g, dtype=torch.float64)
+    assert torch.allclose(ref.pooled(rows), rows.mean(dim=1).view(3, NUM_RANKS, 32), atol=1e-14)
+    x = torch.randn(7, 32, generator=g, dtype=torch.float64) * 3
+    w = ref.s["grid.norm.weight"]
+    want = x / torch.sqrt((x * x).mean(dim=-1, keepdim=True) + 1e-5) * w
+    assert torch.allclose(ref.grid_norm(x, w), want, atol=1e-12)
+    tokens = random_tokens(9, seed=3)
+    ids = tokens[:, :NUM_FIELDS] + torch.tensor(FIELD_OFFSETS)
+    sums = ref.field_sums(ids)
+    for got, table in zip(sums, ref.tables()):
+        assert torch.allclose(got, torch.nn.functional.embedding_bag(ids, table, mode="sum"), atol=1e-12)
+
+
+def test_piquet_grid_is_suit_equivariant():
+    """Permuting the suits of the card codes permutes the per-card features the same way
+    (the grid mixes ranks within a suit and pools over suits: model.py:1-14), for the fp32
+    and the bf16 rounding paths; the summary, which keeps card identity, is not invariant."""
+
+    from oracle.piquet import NUM_CARDS, NUM_RANKS, NUM_SUITS, random_tokens
+
+    codes = random_tokens(6, seed=4)[:, 32:]
+    perm = torch.tensor([2, 0, 3, 1])
+    card_perm = (perm[:, None] * NUM_RANKS + torch.arange(NUM_RANKS)).reshape(NUM_CARDS)
+    for precision, tol in (("fp64", 1e-10), ("bf16", 2e-2)):  # bf16: pooling order may flip a rounding
+        ref = _piquet(precision)
+        base = ref.cards(codes.view(6, NUM_CARDS))
+        moved = ref.cards(codes[:, card_perm])
+        assert torch.allclose(moved, base[:, card_perm], atol=tol, rtol=0), precision
+    ref = _piquet("fp64")
+    s0 = ref.summary(ref.cards(codes))
+    s1 = ref.summary(ref.cards(codes[:, card_perm]))
+    assert not torch.allclose(s0, s1, atol=1e-6)
+
+
+def test_piquet_constants():
+    """The field table as tokens.py:121-125 lays it out: 32 fields, the card field one
+    past the 32 cards, partie totals and the lead in their coarse codes."""
+
+    from oracle.piquet import CARD_RANKS, FIELD_OFFSETS, FIELD_VOCAB, NUM_FIELDS
+
+    assert len(FIELD_VOCAB) == NUM_FIELDS == 32
+    assert FIELD_VOCAB[4] == 33 and FIELD_VOCAB[24] == FIELD_VOCAB[25] == 141 and FIELD_VOCAB[31] == 149
+    assert FIELD_OFFSETS[0] == 0 and FIELD_OFFSETS[-1] + FIELD_VOCAB[-1] == sum(FIELD_VOCAB)
+    assert CARD_RANKS[:9] == (0, 1, 2, 3, 4, 5, 6, 7, 0)
