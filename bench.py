@@ -15,7 +15,8 @@ Also reported (one JSON line on stdout):
   * sampling: device policy sampling of the step's logits (masked softmax + inverse CDF);
   * compaction: KVCache.copy_rows as self-play compacts the pool after games end;
   * prefill: forward_prefill throughput at two shapes, beside the reference path on the GPU;
-  * piquet_embed: the Piquet token embedder on one 4096-token wave, beside the reference path.
+  * piquet_embed: the Piquet token embedder on one 4096-token wave, beside the reference path;
+  * piquet_wave: a whole Piquet wave (embedder + 16-layer Piquet trunk step), graph-replayed.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 10]
 """
@@ -343,6 +344,88 @@ def piquet_embed_time(device: torch.device, with_reference: bool, tokens: int = 
     return out
 
 
+def piquet_wave_time(bench: Bench, with_reference: bool, steps: int = 20) -> dict:
+    """A Piquet rollout wave: 4096 games each append one token, embedded by the Piquet
+    embedder and run through the 16-layer Piquet trunk (d_ff 512, PLE 64, alternating value
+    embeddings; model.py:79-112) with the same context lengths as the bench's middle step,
+    the whole wave captured in one HIP graph and replayed `steps` times (wall time).  With
+    `with_reference`, the oracle's restated reference path for the same wave, graph-captured."""
+
+    from card_playing_gym_amd.games.piquet import CARD_VOCAB, FIELD_VOCAB, NUM_CARDS, PiquetEmbedding, PiquetModelConfig
+    from card_playing_gym_amd.nn.trunk import Trunk
+
+    dev, games = bench.device, bench.games
+    config = PiquetModelConfig()
+    tc = config.trunk()
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(7)
+        emb = PiquetEmbedding(config, tc.ple_width, tc.value_width)
+        trunk = Trunk(tc)
+    emb, trunk = emb.to(dev).eval(), trunk.to(dev).eval()
+    g = torch.Generator().manual_seed(8)
+    fields = torch.stack([torch.randint(0, v, (games,), generator=g) for v in FIELD_VOCAB], dim=1)
+    codes = torch.randint(0, CARD_VOCAB, (games, NUM_CARDS), generator=g)
+    tokens = torch.cat([fields, codes], dim=1).view(games, 1, -1).to(dev)
+    middle = len(bench.plans) // 2
+    positions = torch.from_numpy(bench.plans[middle].positions).to(dev)
+    readout = torch.zeros(games, dtype=torch.int64, device=dev)
+    max_len = bench.max_len
+    cache = trunk_cache = None
+    from card_playing_gym_amd.nn.kv_cache import KVCache
+
+    trunk_cache = KVCache(n_layers=tc.n_layers, kv_heads=tc.n_kv_heads, head_dim=tc.head_dim, capacity=games,
+                          max_len=max_len, device=dev, dtype=torch.bfloat16)
+
+    def body():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            x, ple, values = emb(tokens)
+            return trunk.forward_ragged(*trunk.condition(x, ple, values), trunk_cache, positions, readout)
+
+    def graphed(fn) -> float:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    with torch.no_grad():
+        t = graphed(body)
+    out = {"games": games, "ms_per_wave": round(t * 1e3, 4), "game_tokens_per_s": round(games / t, 1),
+           "trunk": "16 layers, d 256, 8/2 heads, d_ff 512, PLE 64, alternating VE, bf16 KV"}
+    del trunk_cache
+    if with_reference:
+        from oracle.piquet import RefPiquetEmbedding
+        from oracle.reference_path import RefCache, RefTrunk, ref_config_of
+
+        ref_emb = RefPiquetEmbedding({"embedding." + k: v.detach() for k, v in emb.state_dict().items()},
+                                     config.card_layers, config.card_kernel, "bf16")
+        ref = RefTrunk({"trunk." + k: v.detach() for k, v in trunk.state_dict().items()}, ref_config_of(tc), "bf16")
+        cache = RefCache(tc.n_layers, tc.n_kv_heads, tc.head_dim, games, max_len, torch.bfloat16, device=dev)
+        span = min(int(-(-(int(bench.plans[middle].positions.max()) + 1) // 32) * 32), max_len)
+
+        def ref_body():
+            x, ple, values, _ = ref_emb.forward(tokens)
+            return ref.forward_ragged(*ref.condition(x, ple, values), cache, positions, readout, span=span)
+
+        with torch.no_grad():
+            rt = graphed(ref_body)
+        out["reference_gpu_ms_per_wave"] = round(rt * 1e3, 4)
+        out["speedup"] = round(rt / t, 2)
+        del cache
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) -> dict:
     """The oracle's reference path on the host cores, on `games` of the workload's games, at
     steps first .. first + steps (the middle of the timed range: context lengths there are
@@ -524,6 +607,8 @@ def main() -> int:
     log(f"bench: prefill {extra['prefill']}")
     extra["piquet_embed"] = piquet_embed_time(bench.device, with_reference=not args.no_baselines)
     log(f"bench: piquet embedder {extra['piquet_embed']}")
+    extra["piquet_wave"] = piquet_wave_time(bench, with_reference=not args.no_baselines)
+    log(f"bench: piquet wave {extra['piquet_wave']}")
     if not args.no_baselines:
         del bench.cache
         torch.cuda.empty_cache()

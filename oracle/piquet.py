@@ -64,6 +64,12 @@ class RefPiquetEmbedding:
         self.bf16 = precision == "bf16"
         self.s = {k[len(prefix):]: v for k, v in state.items() if k.startswith(prefix)}
         self.layers, self.kernel, self.eps = card_layers, kernel, eps
+        self._consts: dict = {}  # per device: field offsets, card ranks (no copies under capture)
+
+    def _const(self, device):
+        if device not in self._consts:
+            self._consts[device] = (torch.tensor(FIELD_OFFSETS, device=device), torch.tensor(CARD_RANKS, device=device))
+        return self._consts[device]
 
     # -- precision policy ------------------------------------------------------
 
@@ -91,13 +97,17 @@ class RefPiquetEmbedding:
 
         w = self.s[f"grid.blocks.{block}.along_rank.weight"]  # [hidden, width, kernel]
         hidden, width, kernel = w.shape
-        half = kernel // 2
-        shifts = torch.zeros(kernel, NUM_RANKS, NUM_RANKS, dtype=w.dtype, device=w.device)
-        for tap in range(kernel):
-            for rank in range(NUM_RANKS):
-                source = rank + tap - half
-                if 0 <= source < NUM_RANKS:
-                    shifts[tap, source, rank] = 1.0
+        key = ("shifts", kernel, w.device, w.dtype)
+        if key not in self._consts:  # a registered buffer in the reference (model.py:141-148)
+            half = kernel // 2
+            shifts = torch.zeros(kernel, NUM_RANKS, NUM_RANKS, dtype=w.dtype)
+            for tap in range(kernel):
+                for rank in range(NUM_RANKS):
+                    source = rank + tap - half
+                    if 0 <= source < NUM_RANKS:
+                        shifts[tap, source, rank] = 1.0
+            self._consts[key] = shifts.to(w.device)
+        shifts = self._consts[key]
         t = torch.einsum("kio,hwk->iwoh", self._b(shifts), self._b(w))
         return t.reshape(NUM_RANKS * width, NUM_RANKS * hidden)
 
@@ -129,7 +139,7 @@ class RefPiquetEmbedding:
 
     def cards(self, codes):  # [..., 32] -> [..., 32, width] fp32
         lead = codes.shape[:-1]
-        ranks = torch.tensor(CARD_RANKS, device=codes.device)
+        ranks = self._const(codes.device)[1]
         grid = F.embedding(codes.long(), self.s["grid.code.weight"]) + F.embedding(ranks, self.s["grid.rank.weight"])
         width = grid.shape[-1]
         grid = grid.reshape(-1, NUM_SUITS, NUM_RANKS, width)
@@ -161,7 +171,7 @@ class RefPiquetEmbedding:
         """(x, ple lookup or None, value lookup or None, cards) for [..., 64] tokens."""
 
         tokens = tokens.long()
-        ids = tokens[..., :NUM_FIELDS] + torch.tensor(FIELD_OFFSETS, device=tokens.device)
+        ids = tokens[..., :NUM_FIELDS] + self._const(tokens.device)[0]
         cards = self.cards(tokens[..., CARD_START:])
         summary = self.summary(cards)
         sums = iter(self.field_sums(ids))
