@@ -443,11 +443,22 @@ class Trunk(nn.Module):
         values: torch.Tensor | None,
         bounds: torch.Tensor | None = None,
     ) -> torch.Tensor:
-        """Full causal forward over [B, T, d]; final-norm hidden states [B, T, d]
-        (trunk.py:348-374), run as a prefill into a scratch pool."""
+        """Full causal forward (trunk.py:348-374), run as a prefill into a scratch pool:
+        [B, T, d] -> final-norm hidden states [B, T, d]; with ``bounds`` the input is packed
+        rows [N, d] whose row i belongs to the sequence of rows ``[bounds[i, 0],
+        bounds[i, 1])`` (cardgym/nn/packing.py:36-40), -> [N, d].
 
+        Forward only: there is no backward on this path, so a call that autograd would
+        record (grad enabled and parameters requiring grad) raises instead of returning
+        a tensor the optimiser cannot differentiate."""
+
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            raise RuntimeError(
+                "Trunk.forward on the HIP path is inference-only (no backward kernels): call it under "
+                "torch.no_grad() / torch.inference_mode(), or train with cardgym.nn's trunk"
+            )
         if bounds is not None:
-            raise ValueError("Packed full forwards take forward_packed with a cache.")
+            return self._forward_bounds(x, ple, values, bounds)
         batch, length = x.shape[0], x.shape[1]
         cache = KVCache(
             n_layers=self.config.n_layers, kv_heads=self.config.n_kv_heads, head_dim=self.config.head_dim,
@@ -459,3 +470,30 @@ class Trunk(nn.Module):
             rows=None, readout=None, span=None,
         )
         return hidden.view(batch, length, self.config.d_model)
+
+    def _forward_bounds(self, x, ple, values, bounds) -> torch.Tensor:
+        n = x.shape[0]
+        b = torch.as_tensor(bounds).to("cpu", torch.int64)
+        if x.dim() != 2 or b.shape != (n, 2):
+            raise ValueError("packed rows take x [N, d] and bounds [N, 2]")
+        if n == 0:
+            return torch.empty((0, self.config.d_model), device=x.device, dtype=torch.float32)
+        starts, ends = b[:, 0], b[:, 1]
+        rows = torch.arange(n)
+        first = torch.ones(n, dtype=torch.bool)
+        first[1:] = starts[1:] != starts[:-1]
+        seq_start = torch.cat([rows[first], torch.tensor([n])])
+        lengths = seq_start[1:] - seq_start[:-1]
+        per_row = torch.repeat_interleave(seq_start[:-1], lengths)
+        if not (bool((starts == per_row).all()) and bool((ends == torch.repeat_interleave(seq_start[1:], lengths)).all())):
+            raise ValueError("bounds must describe sequences packed back to back (cardgym.nn.packing.Packing)")
+        longest = int(lengths.max())
+        cache = KVCache(
+            n_layers=self.config.n_layers, kv_heads=self.config.n_kv_heads, head_dim=self.config.head_dim,
+            capacity=lengths.numel(), max_len=longest, device=x.device, dtype=torch.float32,
+        )
+        positions = torch.zeros(lengths.numel(), dtype=torch.int64, device=x.device)
+        return self._run(
+            x, ple, values, cache, n_seqs=lengths.numel(), T=0, seq_start=seq_start.to(x.device), positions=positions,
+            rows=None, readout=None, span=longest,
+        )

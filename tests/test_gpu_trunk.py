@@ -326,3 +326,48 @@ def test_bf16_tall_prefill_with_conditioning(device, shape):
     print(shape, err, kv_err)
     assert err <= BF16_TOL, err
     assert kv_err <= BF16_TOL, kv_err
+
+
+def test_packed_rows_forward_matches_padded(device):
+    """Trunk.forward with bounds (packed rows, cardgym/nn/packing.py:36-40) equals the padded
+    full forward row for row, and the padded forward equals the oracle's full forward."""
+
+    config = TrunkConfig(d_model=64, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=128, per_layer_dim=16,
+                         value_embeddings="alternating")
+    state = random_trunk(config, seed=21)
+    trunk = Trunk(config)
+    trunk.load_state_dict({k[len("trunk."):]: v for k, v in state.items()})
+    trunk = trunk.to(device)
+    ref = RefTrunk(state, ref_config_of(config), "fp32")
+    lengths = [5, 1, 9, 3]
+    B, L = len(lengths), max(lengths)
+    gen = torch.Generator().manual_seed(22)
+    raw = torch.randn(B, L, config.d_model, generator=gen)
+    ple_l = torch.randn(B, L, config.ple_width, generator=gen)
+    ve_l = torch.randn(B, L, config.value_width, generator=gen)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    bounds = torch.from_numpy(np.concatenate(
+        [np.stack([np.full(n, s), np.full(n, s + n)], axis=1) for s, n in zip(starts, lengths)]))
+    keep = torch.cat([torch.arange(n) + b * L for b, n in enumerate(lengths)])
+    with torch.no_grad():
+        dev = lambda t: t.to(device)  # noqa: E731
+        padded = trunk(*trunk.condition(dev(raw), dev(ple_l), dev(ve_l)))
+        flat = lambda t: t.reshape(B * L, -1)[keep].to(device)  # noqa: E731
+        packed = trunk(*trunk.condition(flat(raw), flat(ple_l), flat(ve_l)), bounds.to(device))
+        want = ref.forward_full(*ref.condition(raw, ple_l, ve_l))
+    assert packed.shape == (sum(lengths), config.d_model)
+    torch.testing.assert_close(packed.cpu(), padded.reshape(B * L, -1).cpu()[keep], rtol=1e-5, atol=1e-5)
+    for b, n in enumerate(lengths):
+        assert max_err(padded[b, :n], want[b, :n]) <= 1e-4
+    with torch.no_grad(), pytest.raises(ValueError, match="back to back"):
+        trunk(*trunk.condition(flat(raw), flat(ple_l), flat(ve_l)), bounds.flip(0).to(device))
+
+
+def test_forward_with_grad_enabled_raises(device):
+    config = TrunkConfig(d_model=64, n_layers=1, n_heads=4, n_kv_heads=2, d_ff=128)
+    trunk = Trunk(config).to(device)
+    x = torch.randn(2, 3, 64, device=device)
+    with pytest.raises(RuntimeError, match="inference-only"):
+        trunk(*trunk.condition(x, None, None))
+    with torch.no_grad():
+        assert trunk(*trunk.condition(x, None, None)).shape == (2, 3, 64)
