@@ -93,6 +93,14 @@ class PiquetBlock(ctypes.Structure):
     _fields_ = [(name, c_void_p) for name in ("norm", "along_w", "along_b", "across_w", "out_w", "out_b")]
 
 
+class AttnTrain(ctypes.Structure):
+    _fields_ = [
+        ("n", c_int32), ("H", c_int32), ("KVH", c_int32), ("head_dim", c_int32), ("scale", c_float),
+        ("seq_start", c_void_p), ("seq_of", c_void_p), ("q", c_void_p), ("k", c_void_p), ("v", c_void_p),
+        ("ldq", c_int64), ("ldk", c_int64), ("ldv", c_int64), ("o", c_void_p), ("lse", c_void_p),
+    ]
+
+
 class LayerParams(ctypes.Structure):
     _fields_ = [
         ("ln_attn_w", c_void_p),
@@ -180,6 +188,28 @@ _SIGNATURES = {
          c_void_p, P(c_void_p)],
     ),
     "cg_piquet_refresh": (c_int32, [c_void_p, c_void_p]),
+    "cg_gemm_strided": (
+        c_int32,
+        [c_int32, c_int32, c_int32, c_float, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_float,
+         c_void_p, c_int64, c_void_p],
+    ),
+    "cg_layernorm_fwd": (
+        c_int32, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p],
+    ),
+    "cg_norm_bwd_workspace_size": (c_size_t, [c_int32, c_int32]),
+    "cg_norm_bwd": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+         c_void_p, c_size_t, c_int32, c_void_p],
+    ),
+    "cg_column_sum": (c_int32, [c_void_p, c_int32, c_int32, c_int64, c_void_p, c_int32, c_void_p]),
+    "cg_gelu_fwd": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "cg_gelu_bwd": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "cg_add_strided": (c_int32, [c_int32, c_int32, c_float, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
+    "cg_rmsnorm_fwd": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
+    "cg_seq_of": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p]),
+    "cg_attn_train_fwd": (c_int32, [P(AttnTrain), c_void_p]),
+    "cg_attn_train_bwd": (c_int32, [P(AttnTrain), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "cg_piquet_destroy": (c_int32, [c_void_p]),
     "cg_piquet_embed": (
         c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],

@@ -17,7 +17,7 @@ CSRC = Path(__file__).resolve().parent
 PACKAGE = CSRC.parent
 ROOT = PACKAGE.parent
 LIBRARY = PACKAGE / "libcardgym_hip.so"
-SOURCES = ("kv_ops.hip", "attention.hip", "gemm.hip", "layer.hip", "heads.hip", "sample.hip", "piquet.hip", "trunk.hip")
+SOURCES = ("kv_ops.hip", "attention.hip", "gemm.hip", "layer.hip", "heads.hip", "sample.hip", "piquet.hip", "train.hip", "trunk.hip")
 ARCH = os.environ.get("CARDGYM_HIP_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -280,6 +280,8 @@ class Trunk(nn.Module):
         """Normalise the embedding sum and shape the per-layer streams (trunk.py:285-312)."""
 
         require_device(x)
+        if self._recording(x):
+            return self._condition_train(x, ple_lookup, value_lookup)
         if self.input_norm is not None:
             x = self.input_norm(x)
         else:
@@ -303,6 +305,36 @@ class Trunk(nn.Module):
                 stream_handle(x.device),
             )
             ple = out.view(*lead, self.config.n_layers, self.config.per_layer_dim)
+        values = None
+        if self._value_index:
+            if value_lookup is None:
+                raise ValueError("This trunk expects a value-embedding lookup.")
+            values = value_lookup.view(*lead, len(self._value_index), self.config.kv_width)
+        return x, ple, values
+
+    def _recording(self, *inputs: torch.Tensor | None) -> bool:
+        """Whether autograd records this call (training)."""
+
+        if not torch.is_grad_enabled():
+            return False
+        return any(t is not None and t.requires_grad for t in inputs) or any(p.requires_grad for p in self.parameters())
+
+    def _condition_train(self, x, ple_lookup, value_lookup):
+        from .train import PleContextFunction, RMSNormFunction, _require_fp32
+
+        _require_fp32(x.device)
+        if self.input_norm is not None:
+            x = RMSNormFunction.apply(x, self.input_norm.weight, self.input_norm.eps)
+        else:
+            x = x.float()
+        lead = x.shape[:-1]
+        ple = None
+        if self.ple_context is not None:
+            if ple_lookup is None:
+                raise ValueError("This trunk expects a per-layer embedding lookup.")
+            ple = PleContextFunction.apply(ple_lookup, x, self.ple_context.weight).view(
+                *lead, self.config.n_layers, self.config.per_layer_dim
+            )
         values = None
         if self._value_index:
             if value_lookup is None:
@@ -448,15 +480,14 @@ class Trunk(nn.Module):
         rows [N, d] whose row i belongs to the sequence of rows ``[bounds[i, 0],
         bounds[i, 1])`` (cardgym/nn/packing.py:36-40), -> [N, d].
 
-        Forward only: there is no backward on this path, so a call that autograd would
-        record (grad enabled and parameters requiring grad) raises instead of returning
-        a tensor the optimiser cannot differentiate."""
+        When autograd records the call (training), it runs the fp32 training path
+        (card_playing_gym_amd/nn/train.py: the same forward keeping its activations, and a
+        HIP backward)."""
 
-        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
-            raise RuntimeError(
-                "Trunk.forward on the HIP path is inference-only (no backward kernels): call it under "
-                "torch.no_grad() / torch.inference_mode(), or train with cardgym.nn's trunk"
-            )
+        if self._recording(x, ple, values):
+            from .train import trunk_train_forward
+
+            return trunk_train_forward(self, x, ple, values, bounds)
         if bounds is not None:
             return self._forward_bounds(x, ple, values, bounds)
         batch, length = x.shape[0], x.shape[1]
@@ -471,13 +502,14 @@ class Trunk(nn.Module):
         )
         return hidden.view(batch, length, self.config.d_model)
 
-    def _forward_bounds(self, x, ple, values, bounds) -> torch.Tensor:
-        n = x.shape[0]
+    @staticmethod
+    def _seq_start_of(bounds) -> tuple[torch.Tensor, int]:
+        """Host seq_start [S + 1] and the longest sequence of packed-row bounds [N, 2]."""
+
         b = torch.as_tensor(bounds).to("cpu", torch.int64)
-        if x.dim() != 2 or b.shape != (n, 2):
-            raise ValueError("packed rows take x [N, d] and bounds [N, 2]")
-        if n == 0:
-            return torch.empty((0, self.config.d_model), device=x.device, dtype=torch.float32)
+        if b.dim() != 2 or b.shape[1] != 2:
+            raise ValueError("bounds must be [N, 2]")
+        n = b.shape[0]
         starts, ends = b[:, 0], b[:, 1]
         rows = torch.arange(n)
         first = torch.ones(n, dtype=torch.bool)
@@ -487,7 +519,17 @@ class Trunk(nn.Module):
         per_row = torch.repeat_interleave(seq_start[:-1], lengths)
         if not (bool((starts == per_row).all()) and bool((ends == torch.repeat_interleave(seq_start[1:], lengths)).all())):
             raise ValueError("bounds must describe sequences packed back to back (cardgym.nn.packing.Packing)")
-        longest = int(lengths.max())
+        return seq_start, int(lengths.max())
+
+    def _forward_bounds(self, x, ple, values, bounds) -> torch.Tensor:
+        n = x.shape[0]
+        b = torch.as_tensor(bounds)
+        if x.dim() != 2 or b.shape != (n, 2):
+            raise ValueError("packed rows take x [N, d] and bounds [N, 2]")
+        if n == 0:
+            return torch.empty((0, self.config.d_model), device=x.device, dtype=torch.float32)
+        seq_start, longest = self._seq_start_of(b)
+        lengths = seq_start[1:] - seq_start[:-1]
         cache = KVCache(
             n_layers=self.config.n_layers, kv_heads=self.config.n_kv_heads, head_dim=self.config.head_dim,
             capacity=lengths.numel(), max_len=longest, device=x.device, dtype=torch.float32,

@@ -341,6 +341,64 @@ int cg_piquet_destroy(cg_piquet *embedder);
 int cg_piquet_embed(const cg_piquet *embedder, const int64_t *tokens, int64_t ld_tokens, int32_t n, void *x,
                     void *ple, void *values, float *cards, int32_t *flag, void *stream);
 
+/* ---- training side (fp32): a packed-row trunk forward that keeps what its backward needs,
+ * and that backward (cardgym/nn/trunk.py:124-181, 285-374 under autograd; packed rows as in
+ * cardgym/nn/packing.py:36-40).  The composition (which buffers each layer keeps, the order
+ * of the backward) is card_playing_gym_amd/nn/train.py; these are its kernels. ---------- */
+
+/* C = alpha op(A) op(B) + beta C with A(i, k) = a[i * sam + k * sak] and B(k, j) =
+ * b[k * sbk + j * sbn]: every projection's forward, input gradient and weight gradient. */
+int cg_gemm_strided(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
+                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *stream);
+
+/* nn.LayerNorm forward keeping (mean, rstd) per row. */
+int cg_layernorm_fwd(const float *x, const float *w, const float *b, float eps, float *y, float *mean, float *rstd,
+                     int32_t n, int32_t d, void *stream);
+
+/* LayerNorm (mean != NULL) or gain-only RMSNorm (mean == NULL, db ignored) backward: dx per
+ * row; dw (and db) summed over the rows, added to dw / db when accumulate != 0. */
+size_t cg_norm_bwd_workspace_size(int32_t n, int32_t d);
+int cg_norm_bwd(const float *x, const float *dy, const float *w, const float *mean, const float *rstd, float *dx,
+                float *dw, float *db, int32_t n, int32_t d, void *workspace, size_t workspace_size,
+                int32_t accumulate, void *stream);
+
+/* out[c] (+)= sum_r x[r * ld + c]: bias gradients. */
+int cg_column_sum(const float *x, int32_t rows, int32_t cols, int64_t ld, float *out, int32_t accumulate,
+                  void *stream);
+
+/* nn.GELU() (erf) and its backward du = dg * GELU'(u). */
+int cg_gelu_fwd(const float *u, float *g, int64_t n, void *stream);
+int cg_gelu_bwd(const float *u, const float *dg, float *du, int64_t n, void *stream);
+
+/* dst[r, c] += alpha * src[r * ld_src + c] (ld_src 0: one row broadcast, a bias). */
+int cg_add_strided(int32_t rows, int32_t cols, float alpha, const float *src, int64_t ld_src, float *dst,
+                   int64_t ld_dst, void *stream);
+
+/* Gain-only RMSNorm (trunk.py:104-115) keeping rstd per row. */
+int cg_rmsnorm_fwd(const float *x, const float *w, float eps, float *y, float *rstd, int32_t n, int32_t d,
+                   void *stream);
+
+/* seq_of[t] = the packed sequence holding row t. */
+int cg_seq_of(const int64_t *seq_start, int32_t n_seqs, int32_t *seq_of, void *stream);
+
+/* Causal attention inside each packed sequence with GQA (F.scaled_dot_product_attention,
+ * is_causal, enable_gqa: trunk.py:159-164).  q [n, H, D] at row stride ldq, k / v [n, KVH, D]
+ * at ldk / ldv; o [n, H, D] dense; lse [n, H].  Forward writes o and lse; backward reads
+ * them and writes dq / dk / dv at the strides of q / k / v (and dsum [n, H]). */
+typedef struct {
+  int32_t n, H, KVH, head_dim;
+  float scale;
+  const int64_t *seq_start; /* [n_seqs + 1] */
+  const int32_t *seq_of;    /* [n] */
+  const float *q, *k, *v;
+  int64_t ldq, ldk, ldv;
+  float *o;
+  float *lse;
+} cg_attn_train;
+int cg_attn_train_fwd(const cg_attn_train *p, void *stream);
+int cg_attn_train_bwd(const cg_attn_train *p, const float *dout, float *dsum, float *dq, float *dk, float *dv,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,201 @@
+"""The training side (card_playing_gym_amd/nn/train.py, csrc/train.hip) against autograd.
+
+Each kernel first: the strided GEMM in its three layouts, LayerNorm / RMSNorm / GELU
+forward and backward, and causal packed-row GQA attention forward and backward against
+torch's autograd in float64 on the CPU.  Then the whole trunk: the gradients of every
+parameter, of the input and of the per-layer / value lookups against the oracle's
+reference path differentiated by autograd (fp32), padded and packed.  fp32 throughout;
+bar: max |err| <= 1e-4 * max(1, max |want|) per tensor (accumulation orders differ).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from card_playing_gym_amd import _native as nat
+from card_playing_gym_amd.nn import train as T
+from card_playing_gym_amd.nn.trunk import Trunk, TrunkConfig
+from oracle.reference_path import RefTrunk, ref_config_of
+from tests.helpers import random_trunk
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, tol=1e-4, what=""):
+    got, want = got.detach().double().cpu(), want.detach().double().cpu()
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    scale = max(1.0, want.abs().max().item())
+    err = (got - want).abs().max().item()
+    assert err <= tol * scale, (what, err, scale)
+
+
+def test_gemm_layouts(device):
+    g = torch.Generator().manual_seed(1)
+    m, n, k = 70, 45, 133
+    x = torch.randn(m, k, generator=g)
+    w = torch.randn(n, k, generator=g)
+    dy = torch.randn(m, n, generator=g)
+    xd, wd, dyd = x.to(device), w.to(device), dy.to(device)
+    out = torch.full((m, n), 2.0, device=device)
+    T.linear_nt(xd, wd, out, alpha=0.5, beta=3.0)
+    close(out, 0.5 * x.double() @ w.double().T + 6.0, what="nt")
+    out = torch.empty(m, k, device=device)
+    T.matmul_nn(dyd, wd, out)
+    close(out, dy.double() @ w.double(), what="nn")
+    out = torch.empty(n, k, device=device)
+    T.matmul_tn(dyd, xd, out)
+    close(out, dy.double().T @ x.double(), what="tn")
+
+
+@pytest.mark.parametrize("d", [64, 240, 256])
+def test_norms_and_gelu(device, d):
+    g = torch.Generator().manual_seed(d)
+    n = 131
+    x = (torch.randn(n, d, generator=g) * 3 + 1).double().requires_grad_()
+    w = (1 + 0.1 * torch.randn(d, generator=g)).double().requires_grad_()
+    b = (0.1 * torch.randn(d, generator=g)).double().requires_grad_()
+    dy = torch.randn(n, d, generator=g).double()
+    # LayerNorm
+    y = F.layer_norm(x, (d,), w, b, 1e-5)
+    y.backward(dy)
+    xd, wd, bd = x.detach().float().to(device), w.detach().float().to(device), b.detach().float().to(device)
+    yg, mean, rstd = T.layernorm_fwd(xd, wd, bd, 1e-5)
+    close(yg, y, what="ln y")
+    dw, db = torch.empty_like(wd), torch.empty_like(bd)
+    dx = T.norm_bwd(xd, dy.float().to(device), wd, mean, rstd, dw, db)
+    close(dx, x.grad, what="ln dx")
+    close(dw, w.grad, what="ln dw")
+    close(db, b.grad, what="ln db")
+    # RMSNorm (gain only) through the autograd function
+    x.grad = None
+    w.grad = None
+    y = F.rms_norm(x, (d,), w, 1e-5)
+    y.backward(dy)
+    xt = x.detach().float().to(device).requires_grad_()
+    wt = w.detach().float().to(device).requires_grad_()
+    yt = T.RMSNormFunction.apply(xt, wt, 1e-5)
+    yt.backward(dy.float().to(device))
+    close(yt, y, what="rms y")
+    close(xt.grad, x.grad, what="rms dx")
+    close(wt.grad, w.grad, what="rms dw")
+    # GELU
+    u = torch.randn(n, d, generator=g).double().requires_grad_()
+    gu = F.gelu(u)
+    gu.backward(dy)
+    ud = u.detach().float().to(device)
+    close(T.gelu_fwd(ud), gu, what="gelu")
+    close(T.gelu_bwd(ud, dy.float().to(device)), u.grad, what="gelu'")
+
+
+def packed_attention_reference(q, k, v, lengths, G):
+    """Causal GQA attention per packed sequence in float64 (the oracle: SDPA math)."""
+
+    outs, start = [], 0
+    for n in lengths:
+        qs = q[start : start + n].transpose(0, 1)[None]  # [1, H, n, D]
+        ks = k[start : start + n].transpose(0, 1).repeat_interleave(G, dim=0)[None]
+        vs = v[start : start + n].transpose(0, 1).repeat_interleave(G, dim=0)[None]
+        outs.append(F.scaled_dot_product_attention(qs, ks, vs, is_causal=True)[0].transpose(0, 1))
+        start += n
+    return torch.cat(outs)
+
+
+@pytest.mark.parametrize("D,H,KVH", [(32, 8, 2), (64, 4, 4), (16, 6, 3)])
+def test_attention_forward_backward(device, D, H, KVH):
+    g = torch.Generator().manual_seed(D + H)
+    lengths = [1, 7, 70, 130, 3]
+    n = sum(lengths)
+    Q, KVW = H * D, KVH * D
+    qkv = torch.randn(n, Q + 2 * KVW, generator=g, dtype=torch.float64)
+    q = qkv[:, :Q].view(n, H, D).clone().requires_grad_()
+    k = qkv[:, Q : Q + KVW].view(n, KVH, D).clone().requires_grad_()
+    v = qkv[:, Q + KVW :].view(n, KVH, D).clone().requires_grad_()
+    out = packed_attention_reference(q, k, v, lengths, H // KVH)
+    do = torch.randn(n, H, D, generator=g, dtype=torch.float64)
+    out.backward(do)
+    qkv_d = qkv.float().to(device)
+    seq_start = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int64, device=device)
+    seq_of = torch.empty(n, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    nat.call("cg_seq_of", seq_start.data_ptr(), len(lengths), seq_of.data_ptr(), stream)
+    o = torch.empty(n, Q, device=device)
+    lse = torch.empty(n, H, device=device)
+    ld = Q + 2 * KVW
+    at = nat.AttnTrain(n, H, KVH, D, 1.0 / math.sqrt(D), seq_start.data_ptr(), seq_of.data_ptr(), qkv_d.data_ptr(),
+                       T._ptr(qkv_d, Q), T._ptr(qkv_d, Q + KVW), ld, ld, ld, o.data_ptr(), lse.data_ptr())
+    nat.call("cg_attn_train_fwd", ctypes.byref(at), stream)
+    close(o.view(n, H, D), out, what="o")
+    dqkv = torch.empty_like(qkv_d)
+    dsum = torch.empty(n, H, device=device)
+    nat.call("cg_attn_train_bwd", ctypes.byref(at), do.float().to(device).data_ptr(), dsum.data_ptr(),
+             dqkv.data_ptr(), T._ptr(dqkv, Q), T._ptr(dqkv, Q + KVW), stream)
+    close(dqkv[:, :Q].view(n, H, D), q.grad, what="dq")
+    close(dqkv[:, Q : Q + KVW].view(n, KVH, D), k.grad, what="dk")
+    close(dqkv[:, Q + KVW :].view(n, KVH, D), v.grad, what="dv")
+
+
+CONFIGS = [
+    dict(d_model=64, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=128, per_layer_dim=16, value_embeddings="alternating"),
+    dict(d_model=96, n_layers=1, n_heads=3, n_kv_heads=1, d_ff=160, per_layer_dim=0, value_embeddings="all"),
+    dict(d_model=64, n_layers=2, n_heads=2, n_kv_heads=2, d_ff=64, per_layer_dim=64, value_embeddings="off"),
+]
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("shape", CONFIGS, ids=["ple16-ve-alt", "ve-all", "ple-full"])
+def test_trunk_gradients_match_autograd(device, shape, packed):
+    config = TrunkConfig(**shape)
+    state = random_trunk(config, seed=31)
+    trunk = Trunk(config)
+    trunk.load_state_dict({k[len("trunk."):]: v for k, v in state.items()})
+    trunk = trunk.to(device).train()
+    ref_state = {k: v.clone().requires_grad_() for k, v in state.items()}
+    ref = RefTrunk(ref_state, ref_config_of(config), "fp32")
+    g = torch.Generator().manual_seed(32)
+    lengths = [9, 3, 14, 1] if packed else [12] * 3
+    B, L = len(lengths), max(lengths)
+    raw = torch.randn(B, L, config.d_model, generator=g)
+    ple_l = torch.randn(B, L, config.ple_width, generator=g) if config.per_layer_dim else None
+    ve_l = torch.randn(B, L, config.value_width, generator=g) if config.value_width else None
+    weight = torch.randn(B, L, config.d_model, generator=g)
+    # The oracle: padded full forward, loss over each sequence's real rows.
+    inputs = [t.clone().requires_grad_() if t is not None else None for t in (raw, ple_l, ve_l)]
+    want = ref.forward_full(*ref.condition(*inputs))
+    mask = (torch.arange(L)[None, :] < torch.tensor(lengths)[:, None]).float()[..., None]
+    (want * weight * mask).sum().backward()
+    # Ours.
+    keep = torch.cat([torch.arange(n) + b * L for b, n in enumerate(lengths)])
+    if packed:
+        starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+        bounds = torch.from_numpy(np.concatenate(
+            [np.stack([np.full(n, s), np.full(n, s + n)], axis=1) for s, n in zip(starts, lengths)])).to(device)
+        pack = lambda t: None if t is None else t.reshape(B * L, -1)[keep].to(device).requires_grad_()  # noqa: E731
+        ours = [pack(t) for t in (raw, ple_l, ve_l)]
+        hidden = trunk(*trunk.condition(*ours), bounds)
+        (hidden * pack(weight).detach()).sum().backward()
+        for name, got, ref_in in zip(("x", "ple", "values"), ours, inputs):
+            if got is not None:
+                close(got.grad, ref_in.grad.reshape(B * L, -1)[keep], what=f"d{name}")
+    else:
+        ours = [None if t is None else t.to(device).requires_grad_() for t in (raw, ple_l, ve_l)]
+        hidden = trunk(*trunk.condition(*ours))
+        (hidden * weight.to(device)).sum().backward()
+        close(hidden, want, what="hidden")
+        for name, got, ref_in in zip(("x", "ple", "values"), ours, inputs):
+            if got is not None:
+                close(got.grad, ref_in.grad, what=f"d{name}")
+    for name, p in trunk.named_parameters():
+        close(p.grad, ref_state["trunk." + name].grad, what=name)
+
+
+def test_autocast_is_refused_for_training(device):
+    trunk = Trunk(TrunkConfig(d_model=64, n_layers=1, n_heads=4, n_kv_heads=2, d_ff=128)).to(device)
+    x = torch.randn(2, 3, 64, device=device)
+    with torch.autocast("cuda", dtype=torch.bfloat16), pytest.raises(RuntimeError, match="fp32"):
+        trunk(*trunk.condition(x, None, None))

@@ -363,11 +363,15 @@ def test_packed_rows_forward_matches_padded(device):
         trunk(*trunk.condition(flat(raw), flat(ple_l), flat(ve_l)), bounds.flip(0).to(device))
 
 
-def test_forward_with_grad_enabled_raises(device):
+def test_forward_with_grad_enabled_is_differentiable(device):
+    """Under autograd, Trunk.forward takes the training path (its gradients are checked in
+    tests/test_gpu_train.py); without it, the inference path, with the same values."""
+
     config = TrunkConfig(d_model=64, n_layers=1, n_heads=4, n_kv_heads=2, d_ff=128)
     trunk = Trunk(config).to(device)
     x = torch.randn(2, 3, 64, device=device)
-    with pytest.raises(RuntimeError, match="inference-only"):
-        trunk(*trunk.condition(x, None, None))
+    out = trunk(*trunk.condition(x, None, None))
+    assert out.requires_grad and out.shape == (2, 3, 64)
     with torch.no_grad():
-        assert trunk(*trunk.condition(x, None, None)).shape == (2, 3, 64)
+        plain = trunk(*trunk.condition(x, None, None))
+    torch.testing.assert_close(out.detach(), plain, rtol=1e-4, atol=1e-4)
