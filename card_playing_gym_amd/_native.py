@@ -101,6 +101,28 @@ class AttnTrain(ctypes.Structure):
     ]
 
 
+class TrainConfig(ctypes.Structure):
+    _fields_ = [(name, c_int32) for name in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff", "per_layer_dim",
+                                             "ple_width", "value_width")] + [("eps", c_float),
+                                                                             ("value_index", ctypes.POINTER(c_int32))]
+
+
+_TRAIN_BLOCK_FIELDS = ("ln_attn_w", "ln_attn_b", "qkv_w", "out_w", "ln_mlp_w", "ln_mlp_b", "up_w", "up_b", "down_w",
+                       "down_b")
+
+
+class TrainBlock(ctypes.Structure):
+    _fields_ = [(name, c_void_p) for name in _TRAIN_BLOCK_FIELDS]
+
+
+class TrainBlockGrads(ctypes.Structure):
+    _fields_ = [(name, c_void_p) for name in _TRAIN_BLOCK_FIELDS]
+
+
+class TrainGrads(ctypes.Structure):
+    _fields_ = [("blocks", ctypes.POINTER(TrainBlockGrads)), ("final_dw", c_void_p), ("final_db", c_void_p)]
+
+
 class LayerParams(ctypes.Structure):
     _fields_ = [
         ("ln_attn_w", c_void_p),
@@ -188,10 +210,11 @@ _SIGNATURES = {
          c_void_p, P(c_void_p)],
     ),
     "cg_piquet_refresh": (c_int32, [c_void_p, c_void_p]),
+    "cg_gemm_workspace_size": (c_size_t, [c_int32, c_int32, c_int32]),
     "cg_gemm_strided": (
         c_int32,
         [c_int32, c_int32, c_int32, c_float, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_float,
-         c_void_p, c_int64, c_void_p],
+         c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
     ),
     "cg_layernorm_fwd": (
         c_int32, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p],
@@ -202,13 +225,26 @@ _SIGNATURES = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
          c_void_p, c_size_t, c_int32, c_void_p],
     ),
-    "cg_column_sum": (c_int32, [c_void_p, c_int32, c_int32, c_int64, c_void_p, c_int32, c_void_p]),
+    "cg_column_sum_workspace_size": (c_size_t, [c_int32, c_int32]),
+    "cg_column_sum": (c_int32, [c_void_p, c_int32, c_int32, c_int64, c_void_p, c_int32, c_void_p, c_size_t, c_void_p]),
     "cg_gelu_fwd": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
     "cg_gelu_bwd": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "cg_add_strided": (c_int32, [c_int32, c_int32, c_float, c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "cg_rmsnorm_fwd": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "cg_seq_of": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p]),
     "cg_attn_train_fwd": (c_int32, [P(AttnTrain), c_void_p]),
+    "cg_train_saved_size": (c_size_t, [P(TrainConfig), c_int32]),
+    "cg_train_scratch_size": (c_size_t, [P(TrainConfig), c_int32]),
+    "cg_trunk_train_forward": (
+        c_int32,
+        [P(TrainConfig), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+         c_void_p, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p],
+    ),
+    "cg_trunk_train_backward": (
+        c_int32,
+        [P(TrainConfig), c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p, c_size_t,
+         P(TrainGrads), c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
     "cg_attn_train_bwd": (c_int32, [P(AttnTrain), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "cg_piquet_destroy": (c_int32, [c_void_p]),
     "cg_piquet_embed": (

@@ -35,13 +35,19 @@ def _ptr(t: torch.Tensor, offset: int = 0) -> int:
     return t.data_ptr() + 4 * offset
 
 
+def _gemm(m, n, k, alpha, a, sam, sak, b, sbk, sbn, beta, out, device) -> None:
+    size = nat.lib().cg_gemm_workspace_size(m, n, k)
+    ws = torch.empty(max(size // 4, 1), device=device) if size else None
+    nat.call("cg_gemm_strided", m, n, k, float(alpha), a, sam, sak, b, sbk, sbn, float(beta), out.data_ptr(),
+             out.stride(0), None if ws is None else ws.data_ptr(), size, stream_handle(device))
+
+
 def linear_nt(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0) -> None:
     """out[M, N] = alpha * x[M, K] @ w[N, K]^T + beta * out (contiguous rows)."""
 
     m, k = x.shape
     n = w.shape[0]
-    nat.call("cg_gemm_strided", m, n, k, float(alpha), x.data_ptr(), k, 1, w.data_ptr(), 1, k, float(beta),
-             out.data_ptr(), out.stride(0), _s(x))
+    _gemm(m, n, k, alpha, x.data_ptr(), k, 1, w.data_ptr(), 1, k, beta, out, x.device)
 
 
 def matmul_nn(dy: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0) -> None:
@@ -49,8 +55,7 @@ def matmul_nn(dy: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, b
 
     m, n = dy.shape
     k = w.shape[1]
-    nat.call("cg_gemm_strided", m, k, n, float(alpha), dy.data_ptr(), dy.stride(0), 1, w.data_ptr(), k, 1,
-             float(beta), out.data_ptr(), out.stride(0), _s(dy))
+    _gemm(m, k, n, alpha, dy.data_ptr(), dy.stride(0), 1, w.data_ptr(), k, 1, beta, out, dy.device)
 
 
 def matmul_tn(dy: torch.Tensor, x: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0) -> None:
@@ -58,8 +63,7 @@ def matmul_tn(dy: torch.Tensor, x: torch.Tensor, out: torch.Tensor, alpha=1.0, b
 
     m, n = dy.shape
     k = x.shape[1]
-    nat.call("cg_gemm_strided", n, k, m, float(alpha), dy.data_ptr(), 1, dy.stride(0), x.data_ptr(), x.stride(0), 1,
-             float(beta), out.data_ptr(), out.stride(0), _s(dy))
+    _gemm(n, k, m, alpha, dy.data_ptr(), 1, dy.stride(0), x.data_ptr(), x.stride(0), 1, beta, out, dy.device)
 
 
 def add_(dst: torch.Tensor, src: torch.Tensor, alpha=1.0, rows=None, cols=None, ld_src=None) -> None:
@@ -77,8 +81,10 @@ def add_bias_(dst: torch.Tensor, bias: torch.Tensor) -> None:
 
 
 def column_sum(x: torch.Tensor, out: torch.Tensor, accumulate: bool = False) -> None:
+    size = nat.lib().cg_column_sum_workspace_size(x.shape[0], x.shape[1])
+    ws = torch.empty(max(size // 4, 1), device=x.device) if size else None
     nat.call("cg_column_sum", x.data_ptr(), x.shape[0], x.shape[1], x.stride(0), out.data_ptr(), int(accumulate),
-             _s(x))
+             None if ws is None else ws.data_ptr(), size, _s(x))
 
 
 def layernorm_fwd(x, w, b, eps):
@@ -186,129 +192,74 @@ def block_params(trunk) -> list[torch.Tensor]:
     return out + [trunk.final_norm.weight, trunk.final_norm.bias]
 
 
-def _ple_slices(d: int, pd: int):
-    """(column offset, width, scale) of each repeat of a per-layer embedding (trunk.py:318-333)."""
+class _Native:
+    """ctypes views of a trunk's configuration and parameters for the training entry points."""
 
-    if pd == d:
-        return [(0, d, 1.0)]
-    repeats = d // pd if d % pd == 0 else math.ceil(d / pd)
-    scale = 1.0 / math.sqrt(repeats)
-    return [(r * pd, min(pd, d - r * pd), scale) for r in range(repeats)]
+    def __init__(self, trunk, params: list[torch.Tensor]) -> None:
+        c = trunk.config
+        self.value_index = (ctypes.c_int32 * max(c.n_layers, 1))(
+            *[trunk._value_index.get(layer, -1) for layer in range(c.n_layers)]
+        )
+        eps = trunk.blocks[0].ln_attn.eps if len(trunk.blocks) else 1e-5
+        self.config = nat.TrainConfig(c.d_model, c.n_layers, c.n_heads, c.n_kv_heads, c.d_ff, c.per_layer_dim,
+                                      c.ple_width, c.value_width, eps, self.value_index)
+        self.blocks = (nat.TrainBlock * max(c.n_layers, 1))()
+        for layer in range(c.n_layers):
+            self.blocks[layer] = nat.TrainBlock(*(t.data_ptr() for t in params[10 * layer : 10 * layer + 10]))
 
 
 class TrunkFunction(torch.autograd.Function):
-    """Packed-row trunk forward (blocks + final norm) and its backward."""
+    """Packed-row trunk forward (blocks + final norm) and its backward: two calls of
+    cg_trunk_train_forward / cg_trunk_train_backward."""
 
     @staticmethod
     def forward(ctx, trunk, seq_start, x, ple, values, *params):
         c = trunk.config
         device = x.device
-        n, d = x.shape
-        H, KVH, D = c.n_heads, c.n_kv_heads, c.head_dim
-        Q, KVW = H * D, KVH * D
-        n_seqs = seq_start.numel() - 1
-        seq_of = torch.empty(n, dtype=torch.int32, device=device)
-        nat.call("cg_seq_of", seq_start.data_ptr(), n_seqs, seq_of.data_ptr(), _s(x))
-        eps = trunk.blocks[0].ln_attn.eps if len(trunk.blocks) else 1e-5
-        value_index = trunk._value_index
-        saved = []
-        xl = x.float().contiguous()
-        for layer in range(c.n_layers):
-            w = params[10 * layer : 10 * layer + 10]
-            h1, m1, r1 = layernorm_fwd(xl, w[0], w[1], eps)
-            qkv = torch.empty((n, Q + 2 * KVW), device=device)
-            linear_nt(h1, w[2], qkv)
-            if layer in value_index:
-                ve = values[:, value_index[layer] * KVW : (value_index[layer] + 1) * KVW]
-                add_(qkv[:, Q + KVW :], ve, rows=n, cols=KVW)
-            o = torch.empty((n, Q), device=device)
-            lse = torch.empty((n, H), device=device)
-            at = nat.AttnTrain(n, H, KVH, D, 1.0 / math.sqrt(D), seq_start.data_ptr(), seq_of.data_ptr(),
-                               qkv.data_ptr(), _ptr(qkv, Q), _ptr(qkv, Q + KVW), Q + 2 * KVW, Q + 2 * KVW,
-                               Q + 2 * KVW, o.data_ptr(), lse.data_ptr())
-            nat.call("cg_attn_train_fwd", ctypes.byref(at), _s(x))
-            x1 = xl.clone()
-            linear_nt(o, w[3], x1, beta=1.0)
-            h2, m2, r2 = layernorm_fwd(x1, w[4], w[5], eps)
-            u = torch.empty((n, w[6].shape[0]), device=device)
-            linear_nt(h2, w[6], u)
-            add_bias_(u, w[7])
-            g = gelu_fwd(u)
-            x2 = x1.clone()
-            linear_nt(g, w[8], x2, beta=1.0)
-            add_bias_(x2, w[9])
-            if ple is not None:
-                pd = c.per_layer_dim
-                for off, width, scale in _ple_slices(d, pd):
-                    add_(x2[:, off:], ple[:, layer * pd :], alpha=scale, rows=n, cols=width)
-            saved += [xl, h1, m1, r1, qkv, o, lse, x1, h2, m2, r2, u]
-            xl = x2
-        fw, fb = params[10 * c.n_layers], params[10 * c.n_layers + 1]
-        hidden, mf, rf = layernorm_fwd(xl, fw, fb, eps)
-        ctx.trunk, ctx.eps = trunk, eps
+        n = x.shape[0]
+        native = _Native(trunk, list(params))
+        saved_size = nat.lib().cg_train_saved_size(ctypes.byref(native.config), n)
+        scratch_size = nat.lib().cg_train_scratch_size(ctypes.byref(native.config), n)
+        saved = torch.empty(saved_size, dtype=torch.uint8, device=device)
+        scratch = torch.empty(scratch_size, dtype=torch.uint8, device=device)
+        hidden = torch.empty((n, c.d_model), device=device)
+        L = c.n_layers
+        nat.call(
+            "cg_trunk_train_forward", ctypes.byref(native.config), native.blocks, params[10 * L].data_ptr(),
+            params[10 * L + 1].data_ptr(), x.data_ptr(), None if ple is None else ple.data_ptr(),
+            None if values is None else values.data_ptr(), seq_start.data_ptr(), seq_start.numel() - 1, n,
+            hidden.data_ptr(), saved.data_ptr(), saved_size, scratch.data_ptr(), scratch_size, _s(x),
+        )
+        ctx.trunk = trunk
         ctx.has_ple, ctx.has_values = ple is not None, values is not None
-        ctx.save_for_backward(seq_start, seq_of, xl, mf, rf, *saved, *params)
-        ctx.n_saved = len(saved)
+        ctx.save_for_backward(seq_start, saved, *params)
         return hidden
 
     @staticmethod
     def backward(ctx, dh):
         trunk = ctx.trunk
         c = trunk.config
-        t = ctx.saved_tensors
-        seq_start, seq_of, x_last, mf, rf = t[:5]
-        saved = t[5 : 5 + ctx.n_saved]
-        params = t[5 + ctx.n_saved :]
+        seq_start, saved, *params = ctx.saved_tensors
         device = dh.device
-        n, d = x_last.shape
-        H, KVH, D = c.n_heads, c.n_kv_heads, c.head_dim
-        Q, KVW = H * D, KVH * D
-        value_index = trunk._value_index
+        n = dh.shape[0]
+        native = _Native(trunk, params)
         grads = [torch.empty_like(p) for p in params]
         L = c.n_layers
-        dx = norm_bwd(x_last, dh.float().contiguous(), params[10 * L], mf, rf, grads[10 * L], grads[10 * L + 1])
-        dple = torch.zeros((n, c.ple_width), device=device) if ctx.has_ple else None
-        dvalues = torch.zeros((n, c.value_width), device=device) if ctx.has_values else None
-        for layer in reversed(range(L)):
-            xl, h1, m1, r1, qkv, o, lse, x1, h2, m2, r2, u = saved[12 * layer : 12 * layer + 12]
-            w = params[10 * layer : 10 * layer + 10]
-            gw = grads[10 * layer : 10 * layer + 10]
-            if dple is not None:
-                pd = c.per_layer_dim
-                for off, width, scale in _ple_slices(d, pd):
-                    add_(dple[:, layer * pd :], dx[:, off:], alpha=scale, rows=n, cols=width)
-            # x2 = x1 + GELU(u) W2^T + b2
-            g = gelu_fwd(u)
-            matmul_tn(dx, g, gw[8])
-            column_sum(dx, gw[9])
-            dg = torch.empty_like(u)
-            matmul_nn(dx, w[8], dg)
-            du = gelu_bwd(u, dg)
-            matmul_tn(du, h2, gw[6])
-            column_sum(du, gw[7])
-            dh2 = torch.empty_like(h2)
-            matmul_nn(du, w[6], dh2)
-            dx1 = norm_bwd(x1, dh2, w[4], m2, r2, gw[4], gw[5])
-            add_(dx1, dx)
-            # x1 = xl + o Wo^T
-            matmul_tn(dx1, o, gw[3])
-            do = torch.empty_like(o)
-            matmul_nn(dx1, w[3], do)
-            dqkv = torch.empty_like(qkv)
-            dsum = torch.empty((n, H), device=device)
-            at = nat.AttnTrain(n, H, KVH, D, 1.0 / math.sqrt(D), seq_start.data_ptr(), seq_of.data_ptr(),
-                               qkv.data_ptr(), _ptr(qkv, Q), _ptr(qkv, Q + KVW), Q + 2 * KVW, Q + 2 * KVW,
-                               Q + 2 * KVW, o.data_ptr(), lse.data_ptr())
-            nat.call("cg_attn_train_bwd", ctypes.byref(at), do.data_ptr(), dsum.data_ptr(), dqkv.data_ptr(),
-                     _ptr(dqkv, Q), _ptr(dqkv, Q + KVW), _s(dh))
-            if dvalues is not None and layer in value_index:
-                col = value_index[layer] * KVW
-                add_(dvalues[:, col:], dqkv[:, Q + KVW :], rows=n, cols=KVW)
-            matmul_tn(dqkv, h1, gw[2])
-            dh1 = torch.empty_like(h1)
-            matmul_nn(dqkv, w[2], dh1)
-            dx = norm_bwd(xl, dh1, w[0], m1, r1, gw[0], gw[1])
-            add_(dx, dx1)
+        block_grads = (nat.TrainBlockGrads * max(L, 1))()
+        for layer in range(L):
+            block_grads[layer] = nat.TrainBlockGrads(*(g.data_ptr() for g in grads[10 * layer : 10 * layer + 10]))
+        tg = nat.TrainGrads(block_grads, grads[10 * L].data_ptr(), grads[10 * L + 1].data_ptr())
+        dx = torch.empty((n, c.d_model), device=device)
+        dple = torch.empty((n, c.ple_width), device=device) if ctx.has_ple else None
+        dvalues = torch.empty((n, c.value_width), device=device) if ctx.has_values else None
+        scratch_size = nat.lib().cg_train_scratch_size(ctypes.byref(native.config), n)
+        scratch = torch.empty(scratch_size, dtype=torch.uint8, device=device)
+        nat.call(
+            "cg_trunk_train_backward", ctypes.byref(native.config), native.blocks, params[10 * L].data_ptr(),
+            seq_start.data_ptr(), n, dh.float().contiguous().data_ptr(), saved.data_ptr(), saved.numel(),
+            scratch.data_ptr(), scratch_size, ctypes.byref(tg), dx.data_ptr(),
+            None if dple is None else dple.data_ptr(), None if dvalues is None else dvalues.data_ptr(), _s(dh),
+        )
         return (None, None, dx, dple, dvalues, *grads)
 
 
@@ -330,5 +281,6 @@ def trunk_train_forward(trunk, x, ple, values, bounds=None):
     n = flat.shape[0]
     ple_flat = None if ple is None else ple.reshape(n, -1).float().contiguous()
     values_flat = None if values is None else values.reshape(n, -1).float().contiguous()
-    hidden = TrunkFunction.apply(trunk, seq_start, flat, ple_flat, values_flat, *block_params(trunk))
+    hidden = TrunkFunction.apply(trunk, seq_start, flat.float().contiguous(), ple_flat, values_flat,
+                                 *block_params(trunk))
     return hidden.view(*lead, c.d_model)

@@ -348,8 +348,10 @@ int cg_piquet_embed(const cg_piquet *embedder, const int64_t *tokens, int64_t ld
 
 /* C = alpha op(A) op(B) + beta C with A(i, k) = a[i * sam + k * sak] and B(k, j) =
  * b[k * sbk + j * sbn]: every projection's forward, input gradient and weight gradient. */
+size_t cg_gemm_workspace_size(int32_t m, int32_t n, int32_t k); /* split-K partials, 0 if none */
 int cg_gemm_strided(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
-                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *stream);
+                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *workspace,
+                    size_t workspace_size, void *stream);
 
 /* nn.LayerNorm forward keeping (mean, rstd) per row. */
 int cg_layernorm_fwd(const float *x, const float *w, const float *b, float eps, float *y, float *mean, float *rstd,
@@ -362,9 +364,10 @@ int cg_norm_bwd(const float *x, const float *dy, const float *w, const float *me
                 float *dw, float *db, int32_t n, int32_t d, void *workspace, size_t workspace_size,
                 int32_t accumulate, void *stream);
 
-/* out[c] (+)= sum_r x[r * ld + c]: bias gradients. */
+/* out[c] (+)= sum_r x[r * ld + c]: bias gradients (two passes over long columns). */
+size_t cg_column_sum_workspace_size(int32_t rows, int32_t cols);
 int cg_column_sum(const float *x, int32_t rows, int32_t cols, int64_t ld, float *out, int32_t accumulate,
-                  void *stream);
+                  void *workspace, size_t workspace_size, void *stream);
 
 /* nn.GELU() (erf) and its backward du = dg * GELU'(u). */
 int cg_gelu_fwd(const float *u, float *g, int64_t n, void *stream);
@@ -398,6 +401,42 @@ typedef struct {
 int cg_attn_train_fwd(const cg_attn_train *p, void *stream);
 int cg_attn_train_bwd(const cg_attn_train *p, const float *dout, float *dsum, float *dq, float *dk, float *dv,
                       void *stream);
+
+/* The whole trunk under autograd (what card_playing_gym_amd/nn/train.py's TrunkFunction
+ * runs): the forward keeps, per layer, the input, both norms' outputs and statistics, q / k /
+ * v, the attention output and log-sum-exp, the residual after attention and the MLP's
+ * pre-activation in `saved`; the backward reads them and writes every gradient.  x, ple,
+ * values and the gradients are fp32 [n, width] rows of sequences packed back to back
+ * (seq_start [n_seqs + 1]). */
+typedef struct {
+  int32_t d_model, n_layers, n_heads, n_kv_heads, d_ff, per_layer_dim, ple_width, value_width;
+  float eps;
+  const int32_t *value_index; /* host [n_layers]: the layer's slot in the value lookup, -1 none */
+} cg_train_config;
+
+typedef struct { /* DecoderBlock parameters (trunk.py:124-139), fp32 */
+  const float *ln_attn_w, *ln_attn_b, *qkv_w, *out_w, *ln_mlp_w, *ln_mlp_b, *up_w, *up_b, *down_w, *down_b;
+} cg_train_block;
+
+typedef struct {
+  float *ln_attn_w, *ln_attn_b, *qkv_w, *out_w, *ln_mlp_w, *ln_mlp_b, *up_w, *up_b, *down_w, *down_b;
+} cg_train_block_grads;
+
+typedef struct {
+  cg_train_block_grads *blocks; /* host array [n_layers] */
+  float *final_dw, *final_db;
+} cg_train_grads;
+
+size_t cg_train_saved_size(const cg_train_config *c, int32_t n);
+size_t cg_train_scratch_size(const cg_train_config *c, int32_t n);
+int cg_trunk_train_forward(const cg_train_config *c, const cg_train_block *blocks, const float *final_w,
+                           const float *final_b, const float *x, const float *ple, const float *values,
+                           const int64_t *seq_start, int32_t n_seqs, int32_t n, float *hidden, void *saved,
+                           size_t saved_size, void *scratch, size_t scratch_size, void *stream);
+int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *blocks, const float *final_w,
+                            const int64_t *seq_start, int32_t n, const float *dhidden, void *saved,
+                            size_t saved_size, void *scratch, size_t scratch_size, const cg_train_grads *grads,
+                            float *dx, float *dple, float *dvalues, void *stream);
 
 #ifdef __cplusplus
 }
