@@ -222,8 +222,8 @@ _SIGNATURES = {
     "cg_norm_bwd_workspace_size": (c_size_t, [c_int32, c_int32]),
     "cg_norm_bwd": (
         c_int32,
-        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
-         c_void_p, c_size_t, c_int32, c_void_p],
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
+         c_int32, c_void_p, c_size_t, c_int32, c_void_p],
     ),
     "cg_column_sum_workspace_size": (c_size_t, [c_int32, c_int32]),
     "cg_column_sum": (c_int32, [c_void_p, c_int32, c_int32, c_int64, c_void_p, c_int32, c_void_p, c_size_t, c_void_p]),

@@ -26,6 +26,37 @@ namespace {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
+// erf GELU and its derivative Phi(u) + u phi(u).
+__device__ __forceinline__ float gelu_exact(float u) { return 0.5f * u * (1.0f + erff(u * 0.70710678118654752f)); }
+__device__ __forceinline__ float gelu_grad(float u) {
+  const float cdf = 0.5f * (1.0f + erff(u * 0.70710678118654752f));
+  const float pdf = 0.3989422804014327f * expf(-0.5f * u * u);
+  return cdf + u * pdf;
+}
+
+// What a GEMM does with each result v = alpha (A B)[m, n] on its way out: add beta times the
+// prior value (read from `cin` when set, else from C itself), add bias[n], then either
+// multiply by gelu'(aux_in[m, n]) (GELU_GRAD: the MLP's backward) or also write gelu(v) to
+// aux_out[m, n] (GELU: the MLP's forward).  aux_in / aux_out / cin share C's row stride.
+enum EpiMode : int32_t { EPI_PLAIN = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2 };
+struct Epi {
+  const float *bias = nullptr;
+  const float *cin = nullptr;
+  const float *aux_in = nullptr;
+  float *aux_out = nullptr;
+  int32_t mode = EPI_PLAIN;
+};
+
+__device__ __forceinline__ void epilogue(const Epi &e, float v, float beta, float *__restrict__ C, int64_t ldc,
+                                         int64_t m, int64_t n) {
+  const int64_t i = m * ldc + n;
+  if (beta != 0.f) v += beta * (e.cin ? e.cin[i] : C[i]);
+  if (e.bias) v += e.bias[n];
+  if (e.mode == EPI_GELU_GRAD) v *= gelu_grad(e.aux_in[i]);
+  C[i] = v;
+  if (e.mode == EPI_GELU) e.aux_out[i] = gelu_exact(v);
+}
+
 // ---- strided GEMM ---------------------------------------------------------------------
 // Tile 128 x 128, four waves (2 x 2, each 64 x 64 = 4 x 4 MFMA tiles), 16 k per LDS stage,
 // double-buffered.  A(m, k) = A[m * sam + k * sak], B(k, n) = B[k * sbk + n * sbn]; tiles are
@@ -113,7 +144,7 @@ __global__ __launch_bounds__(256) void gemm_strided_kernel(int32_t M, int32_t N,
                                                            const float *__restrict__ A, int64_t sam, int64_t sak,
                                                            const float *__restrict__ B, int64_t sbk, int64_t sbn,
                                                            float beta, float *__restrict__ C, int64_t ldc,
-                                                           float *__restrict__ part) {
+                                                           float *__restrict__ part, const Epi epi) {
   __shared__ __align__(16) float as[2][GT_K * GT_LD];
   __shared__ __align__(16) float bs[2][GT_K * GT_LD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -169,24 +200,21 @@ __global__ __launch_bounds__(256) void gemm_strided_kernel(int32_t M, int32_t N,
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm * 64 + i * 16 + 4 * lg + r, n = n0 + wn * 64 + j * 16 + li;
         if (m >= M || n >= N) continue;
-        if (part) {
+        if (part)
           part[(int64_t(blockIdx.z) * M + m) * N + n] = acc[i][j][r];
-        } else {
-          float *c = C + int64_t(m) * ldc + n;
-          *c = alpha * acc[i][j][r] + (beta != 0.f ? beta * *c : 0.f);
-        }
+        else
+          epilogue(epi, alpha * acc[i][j][r], beta, C, ldc, m, n);
       }
 }
 
-// C[m, n] = alpha * sum_z part[z][m, n] + beta * C[m, n].
+// C[m, n] = epilogue(alpha * sum_z part[z][m, n]).
 __global__ void gemm_reduce_kernel(int32_t M, int32_t N, int32_t slices, float alpha, const float *__restrict__ part,
-                                   float beta, float *__restrict__ C, int64_t ldc) {
+                                   float beta, float *__restrict__ C, int64_t ldc, const Epi epi) {
   const int64_t total = int64_t(M) * N;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
     float s = 0.f;
     for (int z = 0; z < slices; ++z) s += part[int64_t(z) * total + i];
-    float *c = C + (i / N) * ldc + i % N;
-    *c = alpha * s + (beta != 0.f ? beta * *c : 0.f);
+    epilogue(epi, alpha * s, beta, C, ldc, i / N, i % N);
   }
 }
 
@@ -232,13 +260,15 @@ __global__ void layernorm_fwd_kernel(const float *__restrict__ x, const float *_
   }
 }
 
-// dx = rstd (g - mean(g) - xhat mean(g xhat)), g = dy * w; per block of `rows_per_block`
-// rows, partial dw = sum dy xhat and db = sum dy into part[blockIdx][0 / 1][d].  A NULL
-// mean selects RMSNorm (no centring, no bias).
+// dx = rstd (g - mean(g) - xhat mean(g xhat)) (+ residual), g = dy * w; per block of
+// `rows_per_block` rows, partial dw = sum dy xhat and db = sum dy into part[blockIdx][0 / 1][d].
+// A NULL mean selects RMSNorm (no centring, no bias).  Any d (norm_bwd_rows_kernel takes the
+// common shapes).
 __global__ void norm_bwd_kernel(const float *__restrict__ x, const float *__restrict__ dy,
                                 const float *__restrict__ w, const float *__restrict__ mean,
-                                const float *__restrict__ rstd, float *__restrict__ dx, float *__restrict__ part,
-                                int32_t n, int32_t d, int32_t rows_per_block) {
+                                const float *__restrict__ rstd, const float *__restrict__ residual,
+                                float *__restrict__ dx, float *__restrict__ part, int32_t n, int32_t d,
+                                int32_t rows_per_block) {
   extern __shared__ float acc_lds[];  // [2][d]
   const int waves = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int k = threadIdx.x; k < 2 * d; k += blockDim.x) acc_lds[k] = 0.f;
@@ -257,13 +287,141 @@ __global__ void norm_bwd_kernel(const float *__restrict__ x, const float *__rest
     float *dxr = dx + int64_t(row) * d;
     for (int k = lane; k < d; k += 64) {
       const float xh = (xr[k] - mu) * r;
-      dxr[k] = r * (gr[k] * w[k] - mg - xh * mgx);
+      dxr[k] = r * (gr[k] * w[k] - mg - xh * mgx) + (residual ? residual[int64_t(row) * d + k] : 0.f);
       atomicAdd(&acc_lds[k], gr[k] * xh);  // LDS atomics: order within a block only
       atomicAdd(&acc_lds[d + k], gr[k]);
     }
   }
   __syncthreads();
   for (int k = threadIdx.x; k < 2 * d; k += blockDim.x) part[int64_t(blockIdx.x) * 2 * d + k] = acc_lds[k];
+}
+
+// The same for d <= 256 NV, d a multiple of 4, 16-byte aligned rows: lane l owns the float4
+// columns 4 l + 256 v (v < NV) and keeps them, the gain and its dw / db partials in registers;
+// wave w of a block takes rows r0 + w, r0 + w + 4, ... of its NORM_ROWS, loading the next row
+// while it reduces the current one.
+constexpr int NORM_ROWS = 16;
+
+__device__ __forceinline__ float4 f4_fma(float4 a, float4 b, float4 c) {
+  return float4{fmaf(a.x, b.x, c.x), fmaf(a.y, b.y, c.y), fmaf(a.z, b.z, c.z), fmaf(a.w, b.w, c.w)};
+}
+
+template <int NV>
+__global__ __launch_bounds__(256) void norm_bwd_rows_kernel(const float *__restrict__ x, const float *__restrict__ dy,
+                                                            const float *__restrict__ w, const float *__restrict__ mean,
+                                                            const float *__restrict__ rstd,
+                                                            const float *__restrict__ residual, float *__restrict__ dx,
+                                                            float *__restrict__ part, int32_t n, int32_t d) {
+  __shared__ float4 red[4][2 * 64 * NV];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r0 = blockIdx.x * NORM_ROWS, r1 = min(n, r0 + NORM_ROWS);
+  const float4 zero = {0.f, 0.f, 0.f, 0.f};
+  float4 wv[NV], pw[NV], pb[NV], xa[NV], ga[NV];
+  bool in[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = 4 * lane + 256 * v;
+    in[v] = c < d;
+    wv[v] = in[v] ? *reinterpret_cast<const float4 *>(w + c) : zero;
+    pw[v] = zero;
+    pb[v] = zero;
+  }
+  auto load = [&](int row, float4 (&xs)[NV], float4 (&gs)[NV]) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int64_t i = int64_t(row) * d + 4 * lane + 256 * v;
+      xs[v] = in[v] ? *reinterpret_cast<const float4 *>(x + i) : zero;
+      gs[v] = in[v] ? *reinterpret_cast<const float4 *>(dy + i) : zero;
+    }
+  };
+  int row = r0 + wave;
+  float mu_n = 0.f, r_n = 0.f;
+  if (row < r1) {
+    load(row, xa, ga);
+    mu_n = mean ? mean[row] : 0.f;
+    r_n = rstd[row];
+  }
+  for (; row < r1; row += 4) {
+    float4 xc[NV], gc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      xc[v] = xa[v];
+      gc[v] = ga[v];
+    }
+    const float mu = mu_n, r = r_n;
+    if (row + 4 < r1) {
+      load(row + 4, xa, ga);
+      mu_n = mean ? mean[row + 4] : 0.f;
+      r_n = rstd[row + 4];
+    }
+    float4 xh[NV], g[NV];
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      xh[v] = float4{(xc[v].x - mu) * r, (xc[v].y - mu) * r, (xc[v].z - mu) * r, (xc[v].w - mu) * r};
+      g[v] = float4{gc[v].x * wv[v].x, gc[v].y * wv[v].y, gc[v].z * wv[v].z, gc[v].w * wv[v].w};
+      sg += (g[v].x + g[v].y) + (g[v].z + g[v].w);
+      sgx += (g[v].x * xh[v].x + g[v].y * xh[v].y) + (g[v].z * xh[v].z + g[v].w * xh[v].w);
+    }
+    const float mg = mean ? wave_sum(sg) / float(d) : 0.f, mgx = wave_sum(sgx) / float(d);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (!in[v]) continue;
+      const int64_t i = int64_t(row) * d + 4 * lane + 256 * v;
+      float4 o = {r * (g[v].x - mg - xh[v].x * mgx), r * (g[v].y - mg - xh[v].y * mgx),
+                  r * (g[v].z - mg - xh[v].z * mgx), r * (g[v].w - mg - xh[v].w * mgx)};
+      if (residual) {
+        const float4 a = *reinterpret_cast<const float4 *>(residual + i);
+        o = float4{o.x + a.x, o.y + a.y, o.z + a.z, o.w + a.w};
+      }
+      *reinterpret_cast<float4 *>(dx + i) = o;
+      pw[v] = f4_fma(gc[v], xh[v], pw[v]);
+      pb[v] = float4{pb[v].x + gc[v].x, pb[v].y + gc[v].y, pb[v].z + gc[v].z, pb[v].w + gc[v].w};
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    red[wave][v * 64 + lane] = pw[v];
+    red[wave][(NV + v) * 64 + lane] = pb[v];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * 64 * NV; i += 256) {
+    const int which = i / (64 * NV), v = (i / 64) % NV, c = 4 * (i % 64) + 256 * v;
+    if (c >= d) continue;
+    const float4 a = red[0][i], b = red[1][i], e = red[2][i], f = red[3][i];
+    *reinterpret_cast<float4 *>(part + int64_t(blockIdx.x) * 2 * d + which * d + c) =
+        float4{(a.x + b.x) + (e.x + f.x), (a.y + b.y) + (e.y + f.y), (a.z + b.z) + (e.z + f.z),
+               (a.w + b.w) + (e.w + f.w)};
+  }
+}
+
+// dw[c] (+)= sum_p part[p][0][c] and db[c] (+)= sum_p part[p][1][c] (db NULL: RMSNorm): 64 of
+// the 2 d columns per block, its 16 waves splitting the partial rows.
+__global__ __launch_bounds__(1024) void norm_params_kernel(const float *__restrict__ part, int32_t parts, int32_t d,
+                                                           float *__restrict__ dw, float *__restrict__ db,
+                                                           int32_t accumulate) {
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (c < 2 * d) {
+    int p = wave;
+    for (; p + 48 < parts; p += 64) {
+      s0 += part[int64_t(p) * 2 * d + c];
+      s1 += part[int64_t(p + 16) * 2 * d + c];
+      s2 += part[int64_t(p + 32) * 2 * d + c];
+      s3 += part[int64_t(p + 48) * 2 * d + c];
+    }
+    for (; p < parts; p += 16) s0 += part[int64_t(p) * 2 * d + c];
+  }
+  red[wave][lane] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (wave != 0 || c >= 2 * d) return;
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) s += red[q][lane];
+  float *o = c < d ? dw + c : (db ? db + (c - d) : nullptr);
+  if (o) *o = accumulate ? *o + s : s;
 }
 
 // out[c] = sum_r in[r * ld + c] (+ out[c] when accumulate): column sums of per-block
@@ -298,7 +456,6 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float *__restrict
 }
 
 // ---- GELU -------------------------------------------------------------------------------
-__device__ __forceinline__ float gelu_exact(float u) { return 0.5f * u * (1.0f + erff(u * 0.70710678118654752f)); }
 
 __global__ void gelu_fwd_kernel(const float *__restrict__ u, float *__restrict__ g, int64_t n) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
@@ -309,10 +466,7 @@ __global__ void gelu_fwd_kernel(const float *__restrict__ u, float *__restrict__
 __global__ void gelu_bwd_kernel(const float *__restrict__ u, const float *__restrict__ dg, float *__restrict__ du,
                                 int64_t n) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
-    const float x = u[i];
-    const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
-    const float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
-    du[i] = dg[i] * (cdf + x * pdf);
+    du[i] = dg[i] * gelu_grad(u[i]);
   }
 }
 
@@ -333,246 +487,439 @@ struct AttnTrain {
   float *out, *lse_out, *dsum, *dq, *dk, *dv;
 };
 
-// One lane per (token, head): a block is 64 consecutive tokens x up to four heads of one KV
-// head's group (wave w = head hk G + 4 blockIdx.z + w), so every K / V tile staged in LDS
-// serves up to 256 queries, and each lane runs its own softmax over the keys its token sees
-// (no cross-lane reductions).
-constexpr int AT = 32;  // keys per LDS tile
+// The three kernels work on 16 x 16 tiles of (query, key) pairs with v_mfma_f32_16x16x4_f32.
+// A contraction over head_dim gives lane (li, lg) the d slice [lg DC, (lg + 1) DC) (DC =
+// D / 4), one MFMA per d of the slice (the sum over d is the same whichever lane adds which
+// term).  A score tile leaves its MFMA with lane (li, lg) holding rows 4 lg + r, column li;
+// a contraction over those rows (keys or queries) is the four MFMAs r = 0..3, MFMA r taking
+// rows {4 lg + r} from the lane's own registers, so scores never leave the lane.  Outputs
+// over d come out transposed ([d][row]) so that each lane stores four consecutive d.
+constexpr int KT = 64;  // keys per staged K / V tile (forward and dQ)
 
 template <int D>
-__device__ __forceinline__ float dot_lds(const float (&q)[D], const float *row) {
-  float s = 0.f;
+struct AttnDims {
+  static constexpr int DC = D / 4;                      // d per lane in a contraction over d
+  static constexpr int DT = (D + 15) / 16;              // 16-wide d tiles of an output
+  static constexpr int LD = DT * 16 + 4;                // LDS row, floats; d in [D, 16 DT) hold 0
+  static constexpr int C4 = D / 4;                      // float4 per row
+  static constexpr int PER_KV = (2 * KT * C4 + 255) / 256;  // float4 per thread, one K + V tile
+  static constexpr int PER_Q = (2 * 16 * C4 + 255) / 256;   // float4 per thread, one Q + dO tile
+};
+
+template <int DC>
+__device__ __forceinline__ void lds_slice(const float *p, float (&out)[DC]) {
+  if constexpr (DC % 4 == 0) {
 #pragma unroll
-  for (int d = 0; d < D; d += 4) {
-    const float4 k = *reinterpret_cast<const float4 *>(row + d);
-    s = fmaf(q[d], k.x, s);
-    s = fmaf(q[d + 1], k.y, s);
-    s = fmaf(q[d + 2], k.z, s);
-    s = fmaf(q[d + 3], k.w, s);
-  }
-  return s;
-}
-
-// Stages keys [j0, j0 + AT) of KV head hk (rows past n read as 0) into kt / vt.
-template <int D>
-__device__ __forceinline__ void stage_kv(const AttnTrain &a, int hk, int64_t j0, float *kt, float *vt) {
-  for (int i = threadIdx.x; i < AT * D / 4; i += blockDim.x) {
-    const int r = i / (D / 4), c = (i % (D / 4)) * 4;
-    const int64_t j = j0 + r;
-    float4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-    if (j < a.n) {
-      const float *kp = a.k + j * a.ldk + hk * D + c, *vp = a.v + j * a.ldv + hk * D + c;
-      kv = float4{kp[0], kp[1], kp[2], kp[3]};
-      vv = float4{vp[0], vp[1], vp[2], vp[3]};
+    for (int i = 0; i < DC; i += 4) {
+      const float4 v = *reinterpret_cast<const float4 *>(p + i);
+      out[i] = v.x;
+      out[i + 1] = v.y;
+      out[i + 2] = v.z;
+      out[i + 3] = v.w;
     }
-    *reinterpret_cast<float4 *>(kt + r * D + c) = kv;
-    *reinterpret_cast<float4 *>(vt + r * D + c) = vv;
+  } else {
+    static_assert(DC % 2 == 0, "head_dim a multiple of 8");
+#pragma unroll
+    for (int i = 0; i < DC; i += 2) {
+      const float2 v = *reinterpret_cast<const float2 *>(p + i);
+      out[i] = v.x;
+      out[i + 1] = v.y;
+    }
   }
 }
 
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float max_over_rows(float x) {  // over lanes li, li + 16, li + 32, li + 48
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+
+__device__ __forceinline__ float sum_over_rows(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+// Zeroes the d >= D columns of `rows` LDS rows (they feed output rows that are never stored).
+template <int D>
+__device__ __forceinline__ void zero_pad(float *t, int rows) {
+  using S = AttnDims<D>;
+  constexpr int W = S::DT * 16 - D;
+  if constexpr (W > 0)
+    for (int i = threadIdx.x; i < rows * W; i += blockDim.x) t[(i / W) * S::LD + D + i % W] = 0.f;
+}
+
+// K / V tile of keys [j0, j0 + KT) of KV head hk (rows past n read 0), global -> registers -> LDS.
+template <int D>
+__device__ __forceinline__ void kv_load(const AttnTrain &a, int hk, int64_t j0, float4 (&r)[AttnDims<D>::PER_KV]) {
+  using S = AttnDims<D>;
+#pragma unroll
+  for (int e = 0; e < S::PER_KV; ++e) {
+    const int i = threadIdx.x + 256 * e;
+    float4 x = {0.f, 0.f, 0.f, 0.f};
+    if (i < 2 * KT * S::C4) {
+      const bool isv = i >= KT * S::C4;
+      const int ii = isv ? i - KT * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
+      const int64_t j = j0 + row;
+      if (j < a.n) x = *reinterpret_cast<const float4 *>((isv ? a.v + j * a.ldv : a.k + j * a.ldk) + hk * D + c);
+    }
+    r[e] = x;
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void kv_store(float *kt, float *vt, const float4 (&r)[AttnDims<D>::PER_KV]) {
+  using S = AttnDims<D>;
+#pragma unroll
+  for (int e = 0; e < S::PER_KV; ++e) {
+    const int i = threadIdx.x + 256 * e;
+    if (i < 2 * KT * S::C4) {
+      const bool isv = i >= KT * S::C4;
+      const int ii = isv ? i - KT * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
+      *reinterpret_cast<float4 *>((isv ? vt : kt) + row * S::LD + c) = r[e];
+    }
+  }
+}
+
+// Block of the forward and dQ kernels: 256 threads; wave w takes a strip of 16 tokens
+// (strip w / gpb) of head g = gpb blockIdx.z + w % gpb of KV head blockIdx.y, gpb =
+// min(G, 4) heads and 4 / gpb strips per block, so all waves share every staged K / V tile.
+struct QueryStrip {
+  int h;
+  bool active;     // the wave has a head and tokens
+  int64_t t0;      // first token of the wave's strip
+  int64_t base;    // first token of the block
+  int64_t b_last;  // last token of the block
+};
+
+__device__ __forceinline__ QueryStrip query_strip(const AttnTrain &a) {
+  const int G = a.H / a.KVH, gpb = min(G, 4), tpb = 4 / gpb, wave = threadIdx.x >> 6;
+  const int strip = wave / gpb, g = blockIdx.z * gpb + wave % gpb;
+  QueryStrip q;
+  q.base = int64_t(blockIdx.x) * 16 * tpb;
+  q.b_last = min<int64_t>(a.n - 1, q.base + 16 * tpb - 1);
+  q.t0 = q.base + 16 * strip;
+  q.active = strip < tpb && g < G && q.t0 < a.n;
+  q.h = blockIdx.y * G + min(g, G - 1);
+  return q;
+}
+
+// Forward: online softmax over K / V tiles staged KT keys at a time.  S^T = K Q^T (keys on
+// the rows, the lane's query li on the column), row statistics per query across the four
+// lanes li + 16 lg, O^T += V^T P^T.
 template <int D>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnTrain a) {
-  __shared__ __align__(16) float kt[AT * D], vt[AT * D];
-  const int G = a.H / a.KVH, hk = blockIdx.y;
-  const int lane = threadIdx.x & 63, g = blockIdx.z * 4 + (threadIdx.x >> 6);
-  const int64_t t0 = int64_t(blockIdx.x) * 64, t = t0 + lane;
-  const int64_t t_last = min(int64_t(a.n) - 1, t0 + 63);
-  const bool live = t < a.n && g < G;
-  const int h = hk * G + min(g, G - 1);
+  using S = AttnDims<D>;
+  __shared__ __align__(16) float kt[2][KT * S::LD], vt[2][KT * S::LD];
+  const int hk = blockIdx.y, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const QueryStrip w = query_strip(a);
+  const int64_t t = w.t0 + li, w_last = min<int64_t>(a.n - 1, w.t0 + 15);
+  const bool live = w.active && t < a.n;
   const int64_t start = live ? a.seq_start[a.seq_of[t]] : 0;
-  const int64_t k_lo = a.seq_start[a.seq_of[t0]];
-  float q[D], acc[D];
+  const int64_t w_first = w.active ? a.seq_start[a.seq_of[w.t0]] : 0;  // first key any query of the strip sees
+  const int64_t k_lo = a.seq_start[a.seq_of[w.base]];
+  zero_pad<D>(kt[0], 2 * KT);
+  zero_pad<D>(vt[0], 2 * KT);
+  float qf[S::DC];
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    q[d] = live ? a.q[t * a.ldq + h * D + d] * a.scale : 0.f;
-    acc[d] = 0.f;
-  }
-  float m = -INFINITY, l = 0.f;
-  for (int64_t j0 = k_lo; j0 <= t_last; j0 += AT) {
-    __syncthreads();
-    stage_kv<D>(a, hk, j0, kt, vt);
-    __syncthreads();
-    float sc[AT];
-    float mt = -INFINITY;
+  for (int kk = 0; kk < S::DC; ++kk) qf[kk] = live ? a.q[t * a.ldq + w.h * D + lg * S::DC + kk] * a.scale : 0.f;
+  f32x4 acc[S::DT];
 #pragma unroll
-    for (int i = 0; i < AT; ++i) {
-      const int64_t j = j0 + i;
-      const bool ok = live && j >= start && j <= t;
-      sc[i] = ok ? dot_lds<D>(q, kt + i * D) : -INFINITY;
-      mt = fmaxf(mt, sc[i]);
-    }
-    if (mt == -INFINITY) continue;  // no key of this tile for this query
-    const float mn = fmaxf(m, mt);
-    const float corr = expf(m - mn);
-    l *= corr;
+  for (int dt = 0; dt < S::DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -1e30f, l = 0.f;
+  float4 pre[S::PER_KV];
+  kv_load<D>(a, hk, k_lo, pre);
+  kv_store<D>(kt[0], vt[0], pre);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t j0 = k_lo; j0 <= w.b_last; j0 += KT) {
+    const bool more = j0 + KT <= w.b_last;
+    if (more) kv_load<D>(a, hk, j0 + KT, pre);  // the next tile's loads fly during this one's MFMAs
+    if (w.active && j0 <= w_last && j0 + KT - 1 >= w_first) {
+      const float *K = kt[buf], *V = vt[buf];
+      f32x4 s[4];
+      bool any[4];
+      float mt = -INFINITY;
 #pragma unroll
-    for (int d = 0; d < D; ++d) acc[d] *= corr;
+      for (int sub = 0; sub < 4; ++sub) {
+        const int64_t jb = j0 + 16 * sub;
+        any[sub] = jb <= w_last && jb + 15 >= w_first;
+        s[sub] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        if (any[sub]) {
+          float kf[S::DC];
+          lds_slice<S::DC>(K + (16 * sub + li) * S::LD + lg * S::DC, kf);
+          f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < AT; ++i) {
-      const float p = expf(sc[i] - mn);
-      l += p;
-      const float *vr = vt + i * D;
+          for (int kk = 0; kk < S::DC; ++kk) c = mfma4(kf[kk], qf[kk], c);
 #pragma unroll
-      for (int d = 0; d < D; d += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(vr + d);
-        acc[d] = fmaf(p, v.x, acc[d]);
-        acc[d + 1] = fmaf(p, v.y, acc[d + 1]);
-        acc[d + 2] = fmaf(p, v.z, acc[d + 2]);
-        acc[d + 3] = fmaf(p, v.w, acc[d + 3]);
+          for (int r = 0; r < 4; ++r) {
+            const int64_t j = jb + 4 * lg + r;
+            s[sub][r] = (live && j >= start && j <= t) ? c[r] : -INFINITY;
+            mt = fmaxf(mt, s[sub][r]);
+          }
+        }
+      }
+      mt = max_over_rows(mt);
+      const float mn = fmaxf(m, mt);
+      const float corr = __expf(m - mn);
+      m = mn;
+      l *= corr;
+#pragma unroll
+      for (int dt = 0; dt < S::DT; ++dt) acc[dt] *= corr;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        if (!any[sub]) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[sub][r] = __expf(s[sub][r] - mn);
+          l += s[sub][r];
+        }
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[dt] = mfma4(V[(16 * sub + 4 * lg + r) * S::LD + dt * 16 + li], s[sub][r], acc[dt]);
       }
     }
-    m = mn;
+    if (more) kv_store<D>(kt[buf ^ 1], vt[buf ^ 1], pre);
+    __syncthreads();
+    buf ^= 1;
   }
+  l = sum_over_rows(l);
   if (!live) return;
   const float inv = 1.0f / l;
-  float *orow = a.out + (t * a.H + h) * D;
+  float *orow = a.out + (t * a.H + w.h) * D;
 #pragma unroll
-  for (int d = 0; d < D; ++d) orow[d] = acc[d] * inv;
-  a.lse_out[t * a.H + h] = m + logf(l);
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = dt * 16 + 4 * lg + r;
+      if (d < D) orow[d] = acc[dt][r] * inv;
+    }
+  if (lg == 0) a.lse_out[t * a.H + w.h] = m + logf(l);
 }
 
-// dQ (and D = rowsum(dO * O)) per (token, head), with the forward's block layout.
+// dQ (and D = rowsum(dO * O)) with the forward's blocks: S^T = K Q^T and dP^T = V dO^T per
+// 16-key tile, P from the saved log-sum-exp, dS = P (dP - D), dQ^T += K^T dS^T.
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnTrain a) {
-  __shared__ __align__(16) float kt[AT * D], vt[AT * D];
-  const int G = a.H / a.KVH, hk = blockIdx.y;
-  const int lane = threadIdx.x & 63, g = blockIdx.z * 4 + (threadIdx.x >> 6);
-  const int64_t t0 = int64_t(blockIdx.x) * 64, t = t0 + lane;
-  const int64_t t_last = min(int64_t(a.n) - 1, t0 + 63);
-  const bool live = t < a.n && g < G;
-  const int h = hk * G + min(g, G - 1);
-  const int64_t row = t * a.H + h;
+  using S = AttnDims<D>;
+  __shared__ __align__(16) float kt[2][KT * S::LD], vt[2][KT * S::LD];
+  const int hk = blockIdx.y, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const QueryStrip w = query_strip(a);
+  const int64_t t = w.t0 + li, w_last = min<int64_t>(a.n - 1, w.t0 + 15);
+  const bool live = w.active && t < a.n;
+  const int64_t row = t * a.H + w.h;
   const int64_t start = live ? a.seq_start[a.seq_of[t]] : 0;
-  const int64_t k_lo = a.seq_start[a.seq_of[t0]];
-  float q[D], go[D], dq[D];
-  float dsum = 0.f;
+  const int64_t w_first = w.active ? a.seq_start[a.seq_of[w.t0]] : 0;
+  const int64_t k_lo = a.seq_start[a.seq_of[w.base]];
+  zero_pad<D>(kt[0], 2 * KT);
+  zero_pad<D>(vt[0], 2 * KT);
+  float qf[S::DC], gf[S::DC];
+  float part = 0.f;
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    q[d] = live ? a.q[t * a.ldq + h * D + d] * a.scale : 0.f;
-    go[d] = live ? a.dout[row * D + d] : 0.f;
-    dsum = fmaf(go[d], live ? a.o[row * D + d] : 0.f, dsum);
-    dq[d] = 0.f;
+  for (int kk = 0; kk < S::DC; ++kk) {
+    const int d = lg * S::DC + kk;
+    qf[kk] = live ? a.q[t * a.ldq + w.h * D + d] * a.scale : 0.f;
+    gf[kk] = live ? a.dout[row * D + d] : 0.f;
+    part = fmaf(gf[kk], live ? a.o[row * D + d] : 0.f, part);
   }
+  const float dsum = sum_over_rows(part);
   const float lse = live ? a.lse[row] : 0.f;
-  for (int64_t j0 = k_lo; j0 <= t_last; j0 += AT) {
-    __syncthreads();
-    stage_kv<D>(a, hk, j0, kt, vt);
-    __syncthreads();
-#pragma unroll 2
-    for (int i = 0; i < AT; ++i) {
-      const int64_t j = j0 + i;
-      if (!(live && j >= start && j <= t)) continue;
-      float kr[D];  // the key row once from LDS, for the score and the dQ update
+  f32x4 acc[S::DT];
 #pragma unroll
-      for (int d = 0; d < D; d += 4) {
-        const float4 k = *reinterpret_cast<const float4 *>(kt + i * D + d);
-        kr[d] = k.x;
-        kr[d + 1] = k.y;
-        kr[d + 2] = k.z;
-        kr[d + 3] = k.w;
+  for (int dt = 0; dt < S::DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float4 pre[S::PER_KV];
+  kv_load<D>(a, hk, k_lo, pre);
+  kv_store<D>(kt[0], vt[0], pre);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t j0 = k_lo; j0 <= w.b_last; j0 += KT) {
+    const bool more = j0 + KT <= w.b_last;
+    if (more) kv_load<D>(a, hk, j0 + KT, pre);
+    if (w.active && j0 <= w_last && j0 + KT - 1 >= w_first) {
+      const float *K = kt[buf], *V = vt[buf];
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int64_t jb = j0 + 16 * sub;
+        if (!(jb <= w_last && jb + 15 >= w_first)) continue;
+        float kf[S::DC], vf[S::DC];
+        lds_slice<S::DC>(K + (16 * sub + li) * S::LD + lg * S::DC, kf);
+        lds_slice<S::DC>(V + (16 * sub + li) * S::LD + lg * S::DC, vf);
+        f32x4 st = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < S::DC; ++kk) {
+          st = mfma4(kf[kk], qf[kk], st);
+          dp = mfma4(vf[kk], gf[kk], dp);
+        }
+        f32x4 ds;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t j = jb + 4 * lg + r;
+          const float p = (live && j >= start && j <= t) ? __expf(st[r] - lse) : 0.f;
+          ds[r] = p * (dp[r] - dsum);
+        }
+#pragma unroll
+        for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[dt] = mfma4(K[(16 * sub + 4 * lg + r) * S::LD + dt * 16 + li], ds[r], acc[dt]);
       }
-      float sc = 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) sc = fmaf(q[d], kr[d], sc);
-      const float p = expf(sc - lse);
-      const float ds = p * (dot_lds<D>(go, vt + i * D) - dsum);
-#pragma unroll
-      for (int d = 0; d < D; ++d) dq[d] = fmaf(ds, kr[d], dq[d]);
     }
+    if (more) kv_store<D>(kt[buf ^ 1], vt[buf ^ 1], pre);
+    __syncthreads();
+    buf ^= 1;
   }
   if (!live) return;
+  float *dqrow = a.dq + t * a.ldq + w.h * D;
 #pragma unroll
-  for (int d = 0; d < D; ++d) a.dq[t * a.ldq + h * D + d] = dq[d] * a.scale;
-  a.dsum[row] = dsum;
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = dt * 16 + 4 * lg + r;
+      if (d < D) dqrow[d] = acc[dt][r] * a.scale;
+    }
+  if (lg == 0) a.dsum[row] = dsum;
 }
 
-// dK / dV: one lane per key of a 64-key block of KV head blockIdx.y; the queries (token, head
-// of the group) that can see those keys are staged in LDS QT tokens at a time.
-constexpr int QT = 8;
+// One staged query unit of the dK / dV kernel: 16 tokens of one head (q scaled, dO, lse, D).
+template <int D>
+struct QueryUnit {
+  float4 v[AttnDims<D>::PER_Q];
+  float s;
+};
 
 template <int D>
-__global__ __launch_bounds__(64) void attn_bwd_dkv_kernel(const AttnTrain a) {
-  const int G = a.H / a.KVH, hk = blockIdx.y;
-  extern __shared__ __align__(16) float qs[];  // [QT * G][2 D + 2]: q (scaled), dO, lse, D
-  const int stride = 2 * D + 4;
-  const int lane = threadIdx.x;
-  const int64_t j0 = int64_t(blockIdx.x) * 64, j = j0 + lane;
-  const bool live = j < a.n;
-  const int64_t end = live ? a.seq_start[a.seq_of[j] + 1] : 0;
-  const int64_t j_last = min(int64_t(a.n) - 1, j0 + 63);
-  const int64_t q_hi = a.seq_start[a.seq_of[j_last] + 1];  // queries past it see none of these keys
-  float kr[D], vr[D], dk[D], dv[D];
+__device__ __forceinline__ QueryUnit<D> unit_load(const AttnTrain &a, int h, int64_t t0) {
+  using S = AttnDims<D>;
+  QueryUnit<D> u;
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    kr[d] = live ? a.k[j * a.ldk + hk * D + d] : 0.f;
-    vr[d] = live ? a.v[j * a.ldv + hk * D + d] : 0.f;
-    dk[d] = 0.f;
-    dv[d] = 0.f;
-  }
-  for (int64_t t0 = j0; t0 < q_hi; t0 += QT) {
-    __syncthreads();
-    for (int i = lane; i < QT * G * (D / 4); i += 64) {
-      const int r = i / (D / 4), c = (i % (D / 4)) * 4;
-      const int64_t t = t0 + r / G;
-      const int h = hk * G + r % G;
-      float *dst = qs + r * stride;
+  for (int e = 0; e < S::PER_Q; ++e) {
+    const int i = threadIdx.x + 256 * e;
+    float4 x = {0.f, 0.f, 0.f, 0.f};
+    if (i < 2 * 16 * S::C4) {
+      const bool isg = i >= 16 * S::C4;
+      const int ii = isg ? i - 16 * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
+      const int64_t t = t0 + row;
       if (t < a.n) {
-        const float *qp = a.q + t * a.ldq + h * D + c, *gp = a.dout + (t * a.H + h) * D + c;
-        *reinterpret_cast<float4 *>(dst + c) = float4{qp[0] * a.scale, qp[1] * a.scale, qp[2] * a.scale, qp[3] * a.scale};
-        *reinterpret_cast<float4 *>(dst + D + c) = float4{gp[0], gp[1], gp[2], gp[3]};
-        if (c == 0) {
-          dst[2 * D] = a.lse[t * a.H + h];
-          dst[2 * D + 1] = a.dsum[t * a.H + h];
-        }
-      } else {
-        *reinterpret_cast<float4 *>(dst + c) = float4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<float4 *>(dst + D + c) = float4{0.f, 0.f, 0.f, 0.f};
-        if (c == 0) {
-          dst[2 * D] = 0.f;
-          dst[2 * D + 1] = 0.f;
+        if (isg) {
+          x = *reinterpret_cast<const float4 *>(a.dout + (t * a.H + h) * D + c);
+        } else {
+          x = *reinterpret_cast<const float4 *>(a.q + t * a.ldq + h * D + c);
+          x.x *= a.scale;
+          x.y *= a.scale;
+          x.z *= a.scale;
+          x.w *= a.scale;
         }
       }
     }
+    u.v[e] = x;
+  }
+  u.s = 0.f;
+  const int64_t t = t0 + (threadIdx.x & 15);
+  if (threadIdx.x < 32 && t < a.n) u.s = threadIdx.x < 16 ? a.lse[t * a.H + h] : a.dsum[t * a.H + h];
+  return u;
+}
+
+template <int D>
+__device__ __forceinline__ void unit_store(float *qs, float *gs, float *ls, const QueryUnit<D> &u) {
+  using S = AttnDims<D>;
+#pragma unroll
+  for (int e = 0; e < S::PER_Q; ++e) {
+    const int i = threadIdx.x + 256 * e;
+    if (i < 2 * 16 * S::C4) {
+      const bool isg = i >= 16 * S::C4;
+      const int ii = isg ? i - 16 * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
+      *reinterpret_cast<float4 *>((isg ? gs : qs) + row * S::LD + c) = u.v[e];
+    }
+  }
+  if (threadIdx.x < 32) ls[threadIdx.x] = u.s;  // [0, 16) lse, [16, 32) D
+}
+
+// dK / dV: a block holds 64 keys of KV head blockIdx.y, wave w keys j0 + 16 w + li in
+// registers, and walks the units (16-token tile, head of the group) that can see them,
+// staged through LDS.  S = Q K^T and dP = dO V^T (queries on the rows), P and dS per lane,
+// dV^T += dO^T P and dK^T += Q^T dS (q staged scaled, so dK needs no further scale).
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
+  using S = AttnDims<D>;
+  __shared__ __align__(16) float qs[2][16 * S::LD], gs[2][16 * S::LD], ls[2][32];
+  const int G = a.H / a.KVH, hk = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const int64_t j0 = int64_t(blockIdx.x) * 64, jw = j0 + 16 * wave, j = jw + li;
+  const bool live = j < a.n, wave_live = jw < a.n;
+  const int64_t end = live ? a.seq_start[a.seq_of[j] + 1] : 0;
+  const int64_t w_hi = wave_live ? a.seq_start[a.seq_of[min<int64_t>(a.n - 1, jw + 15)] + 1] : 0;
+  const int64_t q_hi = a.seq_start[a.seq_of[min<int64_t>(a.n - 1, j0 + 63)] + 1];
+  const int units = int((q_hi - j0 + 15) / 16) * G;
+  zero_pad<D>(qs[0], 32);
+  zero_pad<D>(gs[0], 32);
+  float kf[S::DC], vf[S::DC];
+#pragma unroll
+  for (int kk = 0; kk < S::DC; ++kk) {
+    const int d = lg * S::DC + kk;
+    kf[kk] = live ? a.k[j * a.ldk + hk * D + d] : 0.f;
+    vf[kk] = live ? a.v[j * a.ldv + hk * D + d] : 0.f;
+  }
+  f32x4 dk[S::DT], dv[S::DT];
+#pragma unroll
+  for (int dt = 0; dt < S::DT; ++dt) {
+    dk[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  unit_store<D>(qs[0], gs[0], ls[0], unit_load<D>(a, hk * G, j0));
+  __syncthreads();
+  int buf = 0;
+  for (int u = 0; u < units; ++u) {
+    const bool more = u + 1 < units;
+    QueryUnit<D> next;
+    if (more) next = unit_load<D>(a, hk * G + (u + 1) % G, j0 + 16 * ((u + 1) / G));
+    const int64_t t0 = j0 + 16 * (u / G);
+    if (wave_live && t0 + 15 >= jw && t0 < w_hi) {
+      const float *Q = qs[buf], *GO = gs[buf], *L = ls[buf];
+      float qa[S::DC], ga[S::DC];
+      lds_slice<S::DC>(Q + li * S::LD + lg * S::DC, qa);
+      lds_slice<S::DC>(GO + li * S::LD + lg * S::DC, ga);
+      f32x4 sc = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < S::DC; ++kk) {
+        sc = mfma4(qa[kk], kf[kk], sc);
+        dp = mfma4(ga[kk], vf[kk], dp);
+      }
+      const float4 lse4 = *reinterpret_cast<const float4 *>(L + 4 * lg);
+      const float4 dsum4 = *reinterpret_cast<const float4 *>(L + 16 + 4 * lg);
+      const float lse[4] = {lse4.x, lse4.y, lse4.z, lse4.w}, dsm[4] = {dsum4.x, dsum4.y, dsum4.z, dsum4.w};
+      f32x4 p, ds;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = t0 + 4 * lg + r;
+        p[r] = (live && t >= j && t < end) ? __expf(sc[r] - lse[r]) : 0.f;
+        ds[r] = p[r] * (dp[r] - dsm[r]);
+      }
+#pragma unroll
+      for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dv[dt] = mfma4(GO[(4 * lg + r) * S::LD + dt * 16 + li], p[r], dv[dt]);
+          dk[dt] = mfma4(Q[(4 * lg + r) * S::LD + dt * 16 + li], ds[r], dk[dt]);
+        }
+    }
+    if (more) unit_store<D>(qs[buf ^ 1], gs[buf ^ 1], ls[buf ^ 1], next);
     __syncthreads();
-    for (int r = 0; r < QT * G; ++r) {
-      const int64_t t = t0 + r / G;
-      if (!(live && t >= j && t < end)) continue;
-      const float *qrow = qs + r * stride;
-      float qv[D], gv[D];  // the query and dO rows once from LDS, for the products and updates
-#pragma unroll
-      for (int d = 0; d < D; d += 4) {
-        const float4 a4 = *reinterpret_cast<const float4 *>(qrow + d);
-        const float4 g4 = *reinterpret_cast<const float4 *>(qrow + D + d);
-        qv[d] = a4.x;
-        qv[d + 1] = a4.y;
-        qv[d + 2] = a4.z;
-        qv[d + 3] = a4.w;
-        gv[d] = g4.x;
-        gv[d + 1] = g4.y;
-        gv[d + 2] = g4.z;
-        gv[d + 3] = g4.w;
-      }
-      float sc = 0.f, dp = 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        sc = fmaf(kr[d], qv[d], sc);
-        dp = fmaf(vr[d], gv[d], dp);
-      }
-      const float p = expf(sc - qrow[2 * D]);
-      const float ds = p * (dp - qrow[2 * D + 1]);
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        dk[d] = fmaf(ds, qv[d], dk[d]);
-        dv[d] = fmaf(p, gv[d], dv[d]);
-      }
-    }
+    buf ^= 1;
   }
   if (!live) return;
+  float *dkrow = a.dk + j * a.ldk + hk * D, *dvrow = a.dv + j * a.ldv + hk * D;
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    a.dk[j * a.ldk + hk * D + d] = dk[d];  // q was staged scaled: dK = sum ds q scale
-    a.dv[j * a.ldv + hk * D + d] = dv[d];
-  }
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = dt * 16 + 4 * lg + r;
+      if (d < D) {
+        dkrow[d] = dk[dt][r];
+        dvrow[d] = dv[dt][r];
+      }
+    }
 }
 
 // dst[r, c] += alpha * src[r * ld_src + c] (ld_src 0 broadcasts one row: bias adds).
@@ -610,6 +957,59 @@ __global__ void seq_of_kernel(const int64_t *__restrict__ seq_start, int32_t n_s
 unsigned blocks_of(int64_t items, int per_block) { return unsigned((items + per_block - 1) / per_block); }
 unsigned grid_1d(int64_t n) { return unsigned(std::min<int64_t>((n + 255) / 256, 8192)); }
 
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Operand checks shared by the attention launchers: the kernels load rows of q / k / v as
+// float4, so rows start 16-byte aligned.
+void check_attn_train(const cg_attn_train *p) {
+  CG_REQUIRE(p && p->H > 0 && p->KVH > 0 && p->H % p->KVH == 0 && p->H / p->KVH <= 16, CG_ERR_INVALID,
+             "training attention: H a multiple of KVH, at most 16 heads per KV head");
+  CG_REQUIRE(p->q && p->k && p->v && p->seq_start && p->seq_of, CG_ERR_INVALID,
+             "attention q, k, v, seq_start and seq_of are required");
+  CG_REQUIRE(aligned16(p->q) && aligned16(p->k) && aligned16(p->v) && p->ldq % 4 == 0 && p->ldk % 4 == 0 &&
+                 p->ldv % 4 == 0,
+             CG_ERR_INVALID, "attention q / k / v: 16-byte aligned rows (pointers and row strides)");
+}
+
+size_t gemm_workspace_bytes(int32_t m, int32_t n, int32_t k);
+
+void gemm_launch(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
+                 const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *workspace,
+                 size_t workspace_size, const Epi &epi, void *stream) {
+  CG_REQUIRE(m >= 0 && n >= 0 && k >= 0, CG_ERR_INVALID, "negative GEMM size");
+  if (m == 0 || n == 0) return;
+  CG_REQUIRE(a && b && c, CG_ERR_INVALID, "a, b and c are required");
+  CG_REQUIRE((epi.mode != EPI_GELU || epi.aux_out) && (epi.mode != EPI_GELU_GRAD || epi.aux_in), CG_ERR_INVALID,
+             "GEMM epilogue: GELU needs its second output, GELU' its pre-activation");
+  const SplitK sk = split_k(m, n, k);
+  const size_t need = gemm_workspace_bytes(m, n, k);
+  CG_REQUIRE(need == 0 || (workspace && workspace_size >= need), CG_ERR_INVALID,
+             "GEMM: workspace too small, need " + std::to_string(need) + " bytes");
+  const dim3 grid(unsigned((n + GT_N - 1) / GT_N), unsigned((m + GT_M - 1) / GT_M), unsigned(sk.slices));
+  CG_REQUIRE(grid.y <= 65535, CG_ERR_UNSUPPORTED, "GEMM: too many row tiles");
+  hipStream_t s = as_stream(stream);
+  float *part = sk.slices > 1 ? static_cast<float *>(workspace) : nullptr;
+  gemm_strided_kernel<<<grid, 256, 0, s>>>(m, n, k, sk.kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, part, epi);
+  CG_LAUNCHED();
+  if (part) {
+    gemm_reduce_kernel<<<grid_1d(int64_t(m) * n), 256, 0, s>>>(m, n, sk.slices, alpha, part, beta, c, ldc, epi);
+    CG_LAUNCHED();
+  }
+}
+
+size_t gemm_workspace_bytes(int32_t m, int32_t n, int32_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  const SplitK sk = split_k(m, n, k);
+  return sk.slices > 1 ? size_t(sk.slices) * size_t(m) * size_t(n) * 4 : 0;
+}
+
+// Grid of the forward and dQ kernels: blocks of 16 tokens x four heads of a group, or more
+// tokens per block when the group has fewer heads.
+dim3 query_grid(const cg_attn_train &p) {
+  const int G = p.H / p.KVH, gpb = std::min(G, 4), tpb = 4 / gpb;
+  return dim3(blocks_of(p.n, 16 * tpb), unsigned(p.KVH), unsigned((G + gpb - 1) / gpb));
+}
+
 
 }  // namespace
 }  // namespace cg
@@ -618,33 +1018,13 @@ using namespace cg;
 
 extern "C" {
 
-size_t cg_gemm_workspace_size(int32_t m, int32_t n, int32_t k) {
-  if (m <= 0 || n <= 0 || k <= 0) return 0;
-  const SplitK sk = split_k(m, n, k);
-  return sk.slices > 1 ? size_t(sk.slices) * size_t(m) * size_t(n) * 4 : 0;
-}
+size_t cg_gemm_workspace_size(int32_t m, int32_t n, int32_t k) { return gemm_workspace_bytes(m, n, k); }
 
 int cg_gemm_strided(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
                     const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *workspace,
                     size_t workspace_size, void *stream) {
   return guarded([&] {
-    CG_REQUIRE(m >= 0 && n >= 0 && k >= 0, CG_ERR_INVALID, "negative GEMM size");
-    if (m == 0 || n == 0) return;
-    CG_REQUIRE(a && b && c, CG_ERR_INVALID, "a, b and c are required");
-    const SplitK sk = split_k(m, n, k);
-    const size_t need = cg_gemm_workspace_size(m, n, k);
-    CG_REQUIRE(need == 0 || (workspace && workspace_size >= need), CG_ERR_INVALID,
-               "GEMM: workspace too small, need " + std::to_string(need) + " bytes");
-    const dim3 grid(unsigned((n + GT_N - 1) / GT_N), unsigned((m + GT_M - 1) / GT_M), unsigned(sk.slices));
-    CG_REQUIRE(grid.y <= 65535, CG_ERR_UNSUPPORTED, "GEMM: too many row tiles");
-    hipStream_t s = as_stream(stream);
-    float *part = sk.slices > 1 ? static_cast<float *>(workspace) : nullptr;
-    gemm_strided_kernel<<<grid, 256, 0, s>>>(m, n, k, sk.kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, part);
-    CG_LAUNCHED();
-    if (part) {
-      gemm_reduce_kernel<<<grid_1d(int64_t(m) * n), 256, 0, s>>>(m, n, sk.slices, alpha, part, beta, c, ldc);
-      CG_LAUNCHED();
-    }
+    gemm_launch(m, n, k, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, workspace, workspace_size, Epi{}, stream);
   });
 }
 
@@ -659,13 +1039,12 @@ int cg_layernorm_fwd(const float *x, const float *w, const float *b, float eps, 
 }
 
 size_t cg_norm_bwd_workspace_size(int32_t n, int32_t d) {
-  const int64_t blocks = (int64_t(n) + 63) / 64;
-  return size_t(std::max<int64_t>(blocks, 1)) * 2 * size_t(d) * 4;
+  return n > 0 && d > 0 ? size_t((int64_t(n) + NORM_ROWS - 1) / NORM_ROWS) * 2 * size_t(d) * 4 : 0;
 }
 
 int cg_norm_bwd(const float *x, const float *dy, const float *w, const float *mean, const float *rstd, float *dx,
-                float *dw, float *db, int32_t n, int32_t d, void *workspace, size_t workspace_size,
-                int32_t accumulate, void *stream) {
+                const float *residual, float *dw, float *db, int32_t n, int32_t d, void *workspace,
+                size_t workspace_size, int32_t accumulate, void *stream) {
   return guarded([&] {
     if (n == 0) return;
     CG_REQUIRE(x && dy && w && rstd && dx && dw && d > 0, CG_ERR_INVALID, "norm backward operands are required");
@@ -673,19 +1052,29 @@ int cg_norm_bwd(const float *x, const float *dy, const float *w, const float *me
     CG_REQUIRE(workspace && workspace_size >= cg_norm_bwd_workspace_size(n, d), CG_ERR_INVALID,
                "norm backward: workspace too small");
     hipStream_t s = as_stream(stream);
-    const int rows = 64;
-    const unsigned blocks = unsigned((int64_t(n) + rows - 1) / rows);
     float *part = static_cast<float *>(workspace);
-    norm_bwd_kernel<<<blocks, 256, 2 * d * sizeof(float), s>>>(x, dy, w, mean, rstd, dx, part, n, d, rows);
-    CG_LAUNCHED();
-    column_sum_kernel<<<dim3(blocks_of(d, 64), 1), 256, 0, s>>>(part, int32_t(blocks), d, 2 * d, dw, accumulate,
-                                                                int32_t(blocks));
-    CG_LAUNCHED();
-    if (db) {
-      column_sum_kernel<<<dim3(blocks_of(d, 64), 1), 256, 0, s>>>(part + d, int32_t(blocks), d, 2 * d, db,
-                                                                  accumulate, int32_t(blocks));
-      CG_LAUNCHED();
+    const bool vec = d % 4 == 0 && d <= 1024 && aligned16(x) && aligned16(dy) && aligned16(w) && aligned16(dx) &&
+                     (residual == nullptr || aligned16(residual)) && aligned16(part);
+    const int32_t parts = int32_t((int64_t(n) + NORM_ROWS - 1) / NORM_ROWS);
+    if (vec) {
+      switch ((d + 255) / 256) {
+#define CG_NORM_CASE(NV)                                                                                        \
+  case NV:                                                                                                      \
+    norm_bwd_rows_kernel<NV><<<unsigned(parts), 256, 0, s>>>(x, dy, w, mean, rstd, residual, dx, part, n, d); \
+    break;
+        CG_NORM_CASE(1)
+        CG_NORM_CASE(2)
+        CG_NORM_CASE(3)
+        CG_NORM_CASE(4)
+#undef CG_NORM_CASE
+      }
+    } else {
+      norm_bwd_kernel<<<unsigned(parts), 256, 2 * d * sizeof(float), s>>>(x, dy, w, mean, rstd, residual, dx, part, n,
+                                                                         d, NORM_ROWS);
     }
+    CG_LAUNCHED();
+    norm_params_kernel<<<blocks_of(2 * int64_t(d), 64), 1024, 0, s>>>(part, parts, d, dw, db, accumulate);
+    CG_LAUNCHED();
   });
 }
 
@@ -765,23 +1154,20 @@ int cg_seq_of(const int64_t *seq_start, int32_t n_seqs, int32_t *seq_of, void *s
 
 int cg_attn_train_fwd(const cg_attn_train *p, void *stream) {
   return guarded([&] {
-    CG_REQUIRE(p && p->H > 0 && p->KVH > 0 && p->H % p->KVH == 0 && p->H / p->KVH <= 16, CG_ERR_INVALID,
-               "training attention: H a multiple of KVH, at most 16 heads per KV head");
+    check_attn_train(p);
     if (p->n == 0) return;
     AttnTrain a{p->n, p->H, p->KVH, p->scale, p->seq_start, p->seq_of, p->q, p->k, p->v, p->ldq, p->ldk, p->ldv,
                 nullptr, nullptr, nullptr, p->o, p->lse, nullptr, nullptr, nullptr, nullptr};
-    CG_REQUIRE(a.q && a.k && a.v && a.out && a.lse_out && a.seq_start && a.seq_of, CG_ERR_INVALID,
-               "attention forward operands are required");
-    const int G = p->H / p->KVH;
-    const dim3 grid(blocks_of(p->n, 64), unsigned(p->KVH), unsigned((G + 3) / 4));
-    const unsigned threads = 64u * unsigned(std::min(G, 4));
+    CG_REQUIRE(a.out && a.lse_out, CG_ERR_INVALID, "attention forward outputs are required");
+    CG_REQUIRE(aligned16(a.out), CG_ERR_INVALID, "attention output: 16-byte aligned");
     hipStream_t s = as_stream(stream);
+    const dim3 grid = query_grid(*p);
     switch (p->head_dim) {
-      case 8: attn_fwd_kernel<8><<<grid, threads, 0, s>>>(a); break;
-      case 16: attn_fwd_kernel<16><<<grid, threads, 0, s>>>(a); break;
-      case 24: attn_fwd_kernel<24><<<grid, threads, 0, s>>>(a); break;
-      case 32: attn_fwd_kernel<32><<<grid, threads, 0, s>>>(a); break;
-      case 64: attn_fwd_kernel<64><<<grid, threads, 0, s>>>(a); break;
+      case 8: attn_fwd_kernel<8><<<grid, 256, 0, s>>>(a); break;
+      case 16: attn_fwd_kernel<16><<<grid, 256, 0, s>>>(a); break;
+      case 24: attn_fwd_kernel<24><<<grid, 256, 0, s>>>(a); break;
+      case 32: attn_fwd_kernel<32><<<grid, 256, 0, s>>>(a); break;
+      case 64: attn_fwd_kernel<64><<<grid, 256, 0, s>>>(a); break;
       default: throw Error(CG_ERR_UNSUPPORTED, "training attention: head_dim 8, 16, 24, 32 or 64");
     }
     CG_LAUNCHED();
@@ -791,25 +1177,21 @@ int cg_attn_train_fwd(const cg_attn_train *p, void *stream) {
 int cg_attn_train_bwd(const cg_attn_train *p, const float *dout, float *dsum, float *dq, float *dk, float *dv,
                       void *stream) {
   return guarded([&] {
-    CG_REQUIRE(p && p->H > 0 && p->KVH > 0 && p->H % p->KVH == 0 && p->H / p->KVH <= 16, CG_ERR_INVALID,
-               "training attention: H a multiple of KVH, at most 16 heads per KV head");
+    check_attn_train(p);
     if (p->n == 0) return;
     AttnTrain a{p->n, p->H, p->KVH, p->scale, p->seq_start, p->seq_of, p->q, p->k, p->v, p->ldq, p->ldk, p->ldv,
                 p->o, dout, p->lse, nullptr, nullptr, dsum, dq, dk, dv};
-    CG_REQUIRE(a.q && a.k && a.v && a.o && a.dout && a.lse && dsum && dq && dk && dv, CG_ERR_INVALID,
+    CG_REQUIRE(a.o && a.dout && a.lse && dsum && dq && dk && dv, CG_ERR_INVALID,
                "attention backward operands are required");
+    CG_REQUIRE(aligned16(dout), CG_ERR_INVALID, "attention dO: 16-byte aligned");
     hipStream_t s = as_stream(stream);
-    const int G = p->H / p->KVH;
-    const dim3 grid(blocks_of(p->n, 64), unsigned(p->KVH), unsigned((G + 3) / 4));
-    const dim3 grid_kv(blocks_of(p->n, 64), unsigned(p->KVH));
-    const unsigned threads = 64u * unsigned(std::min(G, 4));
-    const size_t dkv_lds = size_t(QT) * G * (2 * p->head_dim + 4) * sizeof(float);
+    const dim3 grid = query_grid(*p), grid_kv(blocks_of(p->n, 64), unsigned(p->KVH));
     switch (p->head_dim) {
-#define CG_BWD_CASE(DD)                                                  \
-  case DD:                                                               \
-    attn_bwd_dq_kernel<DD><<<grid, threads, 0, s>>>(a);                  \
-    CG_LAUNCHED();                                                       \
-    attn_bwd_dkv_kernel<DD><<<grid_kv, 64, dkv_lds, s>>>(a);             \
+#define CG_BWD_CASE(DD)                                  \
+  case DD:                                               \
+    attn_bwd_dq_kernel<DD><<<grid, 256, 0, s>>>(a);      \
+    CG_LAUNCHED();                                       \
+    attn_bwd_dkv_kernel<DD><<<grid_kv, 256, 0, s>>>(a);  \
     break;
       CG_BWD_CASE(8)
       CG_BWD_CASE(16)
@@ -858,19 +1240,26 @@ TrainDims dims_of(const cg_train_config &c, int32_t n) {
 }
 
 // Per layer, in floats of n rows: xl, h1 (d), m1, r1 (1), qkv (QKV), o (Q), lse (H), x1, h2 (d),
-// m2, r2 (1), u (F); then x_last (d), mf, rf (1) and seq_of (n int32).
+// m2, r2 (1), u, g (F: the MLP's pre-activation and its GELU); then x_last (d), mf, rf (1) and
+// seq_of (n int32).  Every array starts on a
+// 256-byte boundary (the attention kernels load rows of qkv as float4).
 struct SavedLayer {
-  float *xl, *h1, *m1, *r1, *qkv, *o, *lse, *x1, *h2, *m2, *r2, *u;
+  float *xl, *h1, *m1, *r1, *qkv, *o, *lse, *x1, *h2, *m2, *r2, *u, *g;
 };
 
-int64_t layer_floats(const TrainDims &t) { return t.n * (4 * t.d + 4 + t.QKV + t.Q + t.H + t.F); }
+int64_t span_of(const TrainDims &t, int64_t cols) { return (t.n * cols + 63) / 64 * 64; }
+
+int64_t layer_floats(const TrainDims &t) {
+  return 4 * span_of(t, t.d) + 4 * span_of(t, 1) + span_of(t, t.QKV) + span_of(t, t.Q) + span_of(t, t.H) +
+         2 * span_of(t, t.F);
+}
 
 SavedLayer saved_layer(const TrainDims &t, void *saved, int64_t l) {
   float *p = static_cast<float *>(saved) + l * layer_floats(t);
   SavedLayer s{};
   auto take = [&](int64_t cols) {
     float *q = p;
-    p += t.n * cols;
+    p += span_of(t, cols);
     return q;
   };
   s.xl = take(t.d);
@@ -885,6 +1274,7 @@ SavedLayer saved_layer(const TrainDims &t, void *saved, int64_t l) {
   s.m2 = take(1);
   s.r2 = take(1);
   s.u = take(t.F);
+  s.g = take(t.F);
   return s;
 }
 
@@ -894,7 +1284,8 @@ struct SavedTail {
 };
 SavedTail saved_tail(const TrainDims &t, void *saved) {
   float *p = static_cast<float *>(saved) + t.L * layer_floats(t);
-  return {p, p + t.n * t.d, p + t.n * t.d + t.n, reinterpret_cast<int32_t *>(p + t.n * t.d + 2 * t.n)};
+  float *mf = p + span_of(t, t.d), *rf = mf + span_of(t, 1);
+  return {p, mf, rf, reinterpret_cast<int32_t *>(rf + span_of(t, 1))};
 }
 
 size_t max_gemm_ws(const TrainDims &t) {
@@ -906,12 +1297,12 @@ size_t max_gemm_ws(const TrainDims &t) {
   return m;
 }
 
-// Scratch of one call: GEMM split-K partials, then (backward) dx, dx1, dh (d each), g, dg, du (F),
-// do (Q), dqkv (QKV), dsum (H), norm / column-sum partials.
+// Scratch of one call: GEMM split-K partials, then (backward) dx, dx1, dh (d each), du (F), do (Q),
+// dqkv (QKV), dsum (H), norm / column-sum partials.
 struct Scratch {
   float *gemm_ws;
   size_t gemm_bytes;
-  float *dx, *dx1, *dh, *g, *dg, *du, *dout, *dqkv, *dsum, *red;
+  float *dx, *dx1, *dh, *du, *dout, *dqkv, *dsum, *red;
   size_t red_bytes;
 };
 
@@ -936,8 +1327,6 @@ Scratch scratch_of(const TrainDims &t, void *base) {
   s.dx = take(t.d);
   s.dx1 = take(t.d);
   s.dh = take(t.d);
-  s.g = take(t.F);
-  s.dg = take(t.F);
   s.du = take(t.F);
   s.dout = take(t.Q);
   s.dqkv = take(t.QKV);
@@ -948,28 +1337,28 @@ Scratch scratch_of(const TrainDims &t, void *base) {
 }
 
 size_t scratch_bytes(const TrainDims &t) {
-  const int64_t cols = 3 * t.d + 3 * t.F + t.Q + t.QKV + t.H;
-  return (max_gemm_ws(t) + 255) / 256 * 256 + size_t(t.n * cols + 64 * 9) * 4 + red_bytes_of(t) + 256;
+  const int64_t cols = 3 * t.d + t.F + t.Q + t.QKV + t.H;
+  return (max_gemm_ws(t) + 255) / 256 * 256 + size_t(t.n * cols + 64 * 7) * 4 + red_bytes_of(t) + 256;
 }
 
 struct Gemm {
   const Scratch &s;
   hipStream_t st;
-  // out[M, N] = alpha x[M, K] W[N, K]^T + beta out
+  // out[M, N] = alpha x[M, K] W[N, K]^T (+ the epilogue's terms)
   void nt(int64_t M, int64_t N, int64_t K, const float *x, const float *w, float *out, float beta = 0.f,
-          float alpha = 1.f) const {
-    ok(cg_gemm_strided(int32_t(M), int32_t(N), int32_t(K), alpha, x, K, 1, w, 1, K, beta, out, N, s.gemm_ws,
-                       s.gemm_bytes, st));
+          const Epi &e = Epi{}) const {
+    gemm_launch(int32_t(M), int32_t(N), int32_t(K), 1.f, x, K, 1, w, 1, K, beta, out, N, s.gemm_ws, s.gemm_bytes, e,
+                st);
   }
   // out[M, K] = dy[M, N] W[N, K]
-  void nn(int64_t M, int64_t N, int64_t K, const float *dy, const float *w, float *out) const {
-    ok(cg_gemm_strided(int32_t(M), int32_t(K), int32_t(N), 1.f, dy, N, 1, w, K, 1, 0.f, out, K, s.gemm_ws,
-                       s.gemm_bytes, st));
+  void nn(int64_t M, int64_t N, int64_t K, const float *dy, const float *w, float *out, const Epi &e = Epi{}) const {
+    gemm_launch(int32_t(M), int32_t(K), int32_t(N), 1.f, dy, N, 1, w, K, 1, 0.f, out, K, s.gemm_ws, s.gemm_bytes, e,
+                st);
   }
   // out[N, K] = dy[M, N]^T x[M, K]
   void tn(int64_t M, int64_t N, int64_t K, const float *dy, const float *x, float *out) const {
-    ok(cg_gemm_strided(int32_t(N), int32_t(K), int32_t(M), 1.f, dy, 1, N, x, K, 1, 0.f, out, K, s.gemm_ws,
-                       s.gemm_bytes, st));
+    gemm_launch(int32_t(N), int32_t(K), int32_t(M), 1.f, dy, 1, N, x, K, 1, 0.f, out, K, s.gemm_ws, s.gemm_bytes,
+                Epi{}, st);
   }
 };
 
@@ -1011,7 +1400,7 @@ extern "C" {
 size_t cg_train_saved_size(const cg_train_config *c, int32_t n) {
   if (!c || n <= 0) return 0;
   const TrainDims t = dims_of(*c, n);
-  return size_t(t.L * layer_floats(t) + t.n * t.d + 2 * t.n) * 4 + size_t(t.n) * 4 + 256;
+  return size_t(t.L * layer_floats(t) + span_of(t, t.d) + 2 * span_of(t, 1)) * 4 + size_t(t.n) * 4 + 256;
 }
 
 size_t cg_train_scratch_size(const cg_train_config *c, int32_t n) {
@@ -1029,6 +1418,7 @@ int cg_trunk_train_forward(const cg_train_config *c, const cg_train_block *block
     CG_REQUIRE(n > 0 && n_seqs > 0, CG_ERR_INVALID, "training forward: empty batch");
     CG_REQUIRE(saved_size >= cg_train_saved_size(c, n) && scratch_size >= cg_train_scratch_size(c, n),
                CG_ERR_INVALID, "training forward: buffers too small");
+    CG_REQUIRE(aligned16(saved) && aligned16(scratch), CG_ERR_INVALID, "training forward: saved / scratch 16-byte aligned");
     CG_REQUIRE((c->ple_width == 0 || ple) && (c->value_width == 0 || values), CG_ERR_INVALID,
                "training forward: ple / values lookups are required");
     const TrainDims t = dims_of(*c, n);
@@ -1049,15 +1439,19 @@ int cg_trunk_train_forward(const cg_train_config *c, const cg_train_block *block
         ok(cg_add_strided(int32_t(t.n), int32_t(t.KVW), 1.f, values + vi * t.KVW, t.V, a.qkv + t.Q + t.KVW, t.QKV, st));
       const cg_attn_train at = attn_args(t, seq_start, tail.seq_of, a.qkv, a.o, a.lse);
       ok(cg_attn_train_fwd(&at, st));
-      CG_HIP(hipMemcpyAsync(a.x1, a.xl, size_t(t.n * t.d) * 4, hipMemcpyDeviceToDevice, st));
-      gm.nt(t.n, t.d, t.Q, a.o, w.out_w, a.x1, 1.f);
+      Epi res;  // x1 = xl + o W_out^T
+      res.cin = a.xl;
+      gm.nt(t.n, t.d, t.Q, a.o, w.out_w, a.x1, 1.f, res);
       ok(cg_layernorm_fwd(a.x1, w.ln_mlp_w, w.ln_mlp_b, c->eps, a.h2, a.m2, a.r2, int32_t(t.n), int32_t(t.d), st));
-      gm.nt(t.n, t.F, t.d, a.h2, w.up_w, a.u);
-      ok(cg_add_strided(int32_t(t.n), int32_t(t.F), 1.f, w.up_b, 0, a.u, t.F, st));
-      ok(cg_gelu_fwd(a.u, s.g, t.n * t.F, st));
-      CG_HIP(hipMemcpyAsync(x_next, a.x1, size_t(t.n * t.d) * 4, hipMemcpyDeviceToDevice, st));
-      gm.nt(t.n, t.d, t.F, s.g, w.down_w, x_next, 1.f);
-      ok(cg_add_strided(int32_t(t.n), int32_t(t.d), 1.f, w.down_b, 0, x_next, t.d, st));
+      Epi up;  // u = h2 W_up^T + b_up, g = gelu(u)
+      up.bias = w.up_b;
+      up.aux_out = a.g;
+      up.mode = EPI_GELU;
+      gm.nt(t.n, t.F, t.d, a.h2, w.up_w, a.u, 0.f, up);
+      Epi down;  // x_next = x1 + g W_down^T + b_down
+      down.cin = a.x1;
+      down.bias = w.down_b;
+      gm.nt(t.n, t.d, t.F, a.g, w.down_w, x_next, 1.f, down);
       if (ple)
         ple_slices(t.d, t.pd, [&](int64_t off, int64_t width, float scale) {
           ok(cg_add_strided(int32_t(t.n), int32_t(width), scale, ple + l * t.pd, t.P, x_next + off, t.d, st));
@@ -1078,14 +1472,15 @@ int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *bloc
     CG_REQUIRE(n > 0, CG_ERR_INVALID, "training backward: empty batch");
     CG_REQUIRE(saved_size >= cg_train_saved_size(c, n) && scratch_size >= cg_train_scratch_size(c, n),
                CG_ERR_INVALID, "training backward: buffers too small");
+    CG_REQUIRE(aligned16(saved) && aligned16(scratch), CG_ERR_INVALID, "training backward: saved / scratch 16-byte aligned");
     const TrainDims t = dims_of(*c, n);
     hipStream_t st = as_stream(stream);
     const Scratch s = scratch_of(t, scratch);
     const Gemm gm{s, st};
     const SavedTail tail = saved_tail(t, saved);
     const int32_t N = int32_t(t.n);
-    ok(cg_norm_bwd(tail.x_last, dhidden, final_w, tail.mf, tail.rf, s.dx, grads->final_dw, grads->final_db, N,
-                   int32_t(t.d), s.red, s.red_bytes, 0, st));
+    ok(cg_norm_bwd(tail.x_last, dhidden, final_w, tail.mf, tail.rf, s.dx, nullptr, grads->final_dw,
+                   grads->final_db, N, int32_t(t.d), s.red, s.red_bytes, 0, st));
     if (dple) CG_HIP(hipMemsetAsync(dple, 0, size_t(t.n * t.P) * 4, st));
     if (dvalues) CG_HIP(hipMemsetAsync(dvalues, 0, size_t(t.n * t.V) * 4, st));
     for (int64_t l = t.L - 1; l >= 0; --l) {
@@ -1096,17 +1491,17 @@ int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *bloc
         ple_slices(t.d, t.pd, [&](int64_t off, int64_t width, float scale) {
           ok(cg_add_strided(N, int32_t(width), scale, s.dx + off, t.d, dple + l * t.pd, t.P, st));
         });
-      ok(cg_gelu_fwd(a.u, s.g, t.n * t.F, st));
-      gm.tn(t.n, t.d, t.F, s.dx, s.g, gw.down_w);
+      gm.tn(t.n, t.d, t.F, s.dx, a.g, gw.down_w);
       ok(cg_column_sum(s.dx, N, int32_t(t.d), t.d, gw.down_b, 0, s.red, s.red_bytes, st));
-      gm.nn(t.n, t.d, t.F, s.dx, w.down_w, s.dg);
-      ok(cg_gelu_bwd(a.u, s.dg, s.du, t.n * t.F, st));
+      Epi dgelu;  // du = (dx W_down) gelu'(u)
+      dgelu.aux_in = a.u;
+      dgelu.mode = EPI_GELU_GRAD;
+      gm.nn(t.n, t.d, t.F, s.dx, w.down_w, s.du, dgelu);
       gm.tn(t.n, t.F, t.d, s.du, a.h2, gw.up_w);
       ok(cg_column_sum(s.du, N, int32_t(t.F), t.F, gw.up_b, 0, s.red, s.red_bytes, st));
       gm.nn(t.n, t.F, t.d, s.du, w.up_w, s.dh);
-      ok(cg_norm_bwd(a.x1, s.dh, w.ln_mlp_w, a.m2, a.r2, s.dx1, gw.ln_mlp_w, gw.ln_mlp_b, N, int32_t(t.d), s.red,
-                     s.red_bytes, 0, st));
-      ok(cg_add_strided(N, int32_t(t.d), 1.f, s.dx, t.d, s.dx1, t.d, st));
+      ok(cg_norm_bwd(a.x1, s.dh, w.ln_mlp_w, a.m2, a.r2, s.dx1, s.dx, gw.ln_mlp_w, gw.ln_mlp_b, N, int32_t(t.d),
+                     s.red, s.red_bytes, 0, st));
       gm.tn(t.n, t.d, t.Q, s.dx1, a.o, gw.out_w);
       gm.nn(t.n, t.d, t.Q, s.dx1, w.out_w, s.dout);
       const cg_attn_train at = attn_args(t, seq_start, tail.seq_of, a.qkv, a.o, a.lse);
@@ -1116,9 +1511,8 @@ int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *bloc
         ok(cg_add_strided(N, int32_t(t.KVW), 1.f, s.dqkv + t.Q + t.KVW, t.QKV, dvalues + vi * t.KVW, t.V, st));
       gm.tn(t.n, t.QKV, t.d, s.dqkv, a.h1, gw.qkv_w);
       gm.nn(t.n, t.QKV, t.d, s.dqkv, w.qkv_w, s.dh);
-      ok(cg_norm_bwd(a.xl, s.dh, w.ln_attn_w, a.m1, a.r1, s.dx, gw.ln_attn_w, gw.ln_attn_b, N, int32_t(t.d), s.red,
-                     s.red_bytes, 0, st));
-      ok(cg_add_strided(N, int32_t(t.d), 1.f, s.dx1, t.d, s.dx, t.d, st));
+      ok(cg_norm_bwd(a.xl, s.dh, w.ln_attn_w, a.m1, a.r1, s.dx, s.dx1, gw.ln_attn_w, gw.ln_attn_b, N, int32_t(t.d),
+                     s.red, s.red_bytes, 0, st));
     }
     CG_HIP(hipMemcpyAsync(dx, s.dx, size_t(t.n * t.d) * 4, hipMemcpyDeviceToDevice, st));
   });

@@ -97,16 +97,17 @@ def layernorm_fwd(x, w, b, eps):
     return y, mean, rstd
 
 
-def norm_bwd(x, dy, w, mean, rstd, dw, db) -> torch.Tensor:
-    """dx of LayerNorm (mean given) or RMSNorm (mean None); dw / db receive the sums."""
+def norm_bwd(x, dy, w, mean, rstd, dw, db, residual=None) -> torch.Tensor:
+    """dx of LayerNorm (mean given) or RMSNorm (mean None), plus `residual` when given; dw / db
+    receive the sums."""
 
     n, d = x.shape
     dx = torch.empty_like(x)
     size = nat.lib().cg_norm_bwd_workspace_size(n, d)
     ws = torch.empty(max(size // 4, 1), device=x.device)
     nat.call("cg_norm_bwd", x.data_ptr(), dy.data_ptr(), w.data_ptr(), None if mean is None else mean.data_ptr(),
-             rstd.data_ptr(), dx.data_ptr(), dw.data_ptr(), None if db is None else db.data_ptr(), n, d,
-             ws.data_ptr(), size, 0, _s(x))
+             rstd.data_ptr(), dx.data_ptr(), None if residual is None else residual.data_ptr(), dw.data_ptr(),
+             None if db is None else db.data_ptr(), n, d, ws.data_ptr(), size, 0, _s(x))
     return dx
 
 

@@ -358,11 +358,12 @@ int cg_layernorm_fwd(const float *x, const float *w, const float *b, float eps, 
                      int32_t n, int32_t d, void *stream);
 
 /* LayerNorm (mean != NULL) or gain-only RMSNorm (mean == NULL, db ignored) backward: dx per
- * row; dw (and db) summed over the rows, added to dw / db when accumulate != 0. */
+ * row, plus residual (a gradient arriving around the norm, e.g. the residual stream's) when
+ * not NULL; dw (and db) summed over the rows, added to dw / db when accumulate != 0. */
 size_t cg_norm_bwd_workspace_size(int32_t n, int32_t d);
 int cg_norm_bwd(const float *x, const float *dy, const float *w, const float *mean, const float *rstd, float *dx,
-                float *dw, float *db, int32_t n, int32_t d, void *workspace, size_t workspace_size,
-                int32_t accumulate, void *stream);
+                const float *residual, float *dw, float *db, int32_t n, int32_t d, void *workspace,
+                size_t workspace_size, int32_t accumulate, void *stream);
 
 /* out[c] (+)= sum_r x[r * ld + c]: bias gradients (two passes over long columns). */
 size_t cg_column_sum_workspace_size(int32_t rows, int32_t cols);
@@ -387,7 +388,8 @@ int cg_seq_of(const int64_t *seq_start, int32_t n_seqs, int32_t *seq_of, void *s
 /* Causal attention inside each packed sequence with GQA (F.scaled_dot_product_attention,
  * is_causal, enable_gqa: trunk.py:159-164).  q [n, H, D] at row stride ldq, k / v [n, KVH, D]
  * at ldk / ldv; o [n, H, D] dense; lse [n, H].  Forward writes o and lse; backward reads
- * them and writes dq / dk / dv at the strides of q / k / v (and dsum [n, H]). */
+ * them and writes dq / dk / dv at the strides of q / k / v (and dsum [n, H]).  q, k, v, o and
+ * dout start 16-byte aligned and ldq / ldk / ldv are multiples of 4. */
 typedef struct {
   int32_t n, H, KVH, head_dim;
   float scale;
@@ -407,7 +409,7 @@ int cg_attn_train_bwd(const cg_attn_train *p, const float *dout, float *dsum, fl
  * v, the attention output and log-sum-exp, the residual after attention and the MLP's
  * pre-activation in `saved`; the backward reads them and writes every gradient.  x, ple,
  * values and the gradients are fp32 [n, width] rows of sequences packed back to back
- * (seq_start [n_seqs + 1]). */
+ * (seq_start [n_seqs + 1]); saved and scratch start 16-byte aligned. */
 typedef struct {
   int32_t d_model, n_layers, n_heads, n_kv_heads, d_ff, per_layer_dim, ple_width, value_width;
   float eps;

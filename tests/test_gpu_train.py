@@ -53,7 +53,7 @@ def test_gemm_layouts(device):
     close(out, dy.double().T @ x.double(), what="tn")
 
 
-@pytest.mark.parametrize("d", [64, 240, 256])
+@pytest.mark.parametrize("d", [64, 66, 240, 256, 600])
 def test_norms_and_gelu(device, d):
     g = torch.Generator().manual_seed(d)
     n = 131
@@ -70,6 +70,10 @@ def test_norms_and_gelu(device, d):
     dw, db = torch.empty_like(wd), torch.empty_like(bd)
     dx = T.norm_bwd(xd, dy.float().to(device), wd, mean, rstd, dw, db)
     close(dx, x.grad, what="ln dx")
+    residual = torch.randn(n, d, generator=g)
+    dx = T.norm_bwd(xd, dy.float().to(device), wd, mean, rstd, torch.empty_like(wd), torch.empty_like(bd),
+                    residual=residual.to(device))
+    close(dx, x.grad + residual.double(), what="ln dx + residual")
     close(dw, w.grad, what="ln dw")
     close(db, b.grad, what="ln db")
     # RMSNorm (gain only) through the autograd function
@@ -144,11 +148,14 @@ CONFIGS = [
     dict(d_model=64, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=128, per_layer_dim=16, value_embeddings="alternating"),
     dict(d_model=96, n_layers=1, n_heads=3, n_kv_heads=1, d_ff=160, per_layer_dim=0, value_embeddings="all"),
     dict(d_model=64, n_layers=2, n_heads=2, n_kv_heads=2, d_ff=64, per_layer_dim=64, value_embeddings="off"),
+    # long reductions (d_model, d_ff >= 1024): split-K GEMMs whose second pass applies the
+    # residual / bias / GELU' epilogues
+    dict(d_model=1024, n_layers=1, n_heads=16, n_kv_heads=4, d_ff=1024, per_layer_dim=0, value_embeddings="off"),
 ]
 
 
 @pytest.mark.parametrize("packed", [False, True])
-@pytest.mark.parametrize("shape", CONFIGS, ids=["ple16-ve-alt", "ve-all", "ple-full"])
+@pytest.mark.parametrize("shape", CONFIGS, ids=["ple16-ve-alt", "ve-all", "ple-full", "wide"])
 def test_trunk_gradients_match_autograd(device, shape, packed):
     config = TrunkConfig(**shape)
     state = random_trunk(config, seed=31)
