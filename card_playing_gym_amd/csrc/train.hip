@@ -60,134 +60,141 @@ __device__ __forceinline__ void epilogue(const Epi &e, float v, float beta, floa
 // ---- strided GEMM ---------------------------------------------------------------------
 // Tile 128 x 128, four waves (2 x 2, each 64 x 64 = 4 x 4 MFMA tiles), 16 k per LDS stage,
 // double-buffered.  A(m, k) = A[m * sam + k * sak], B(k, n) = B[k * sbk + n * sbn]; tiles are
-// staged through LDS with 16-byte loads along whichever index has stride 1.  MFMA 16x16x4
-// f32: lane (li, lg) gives A(row li, k lg) and B(k lg, col li); the result sits in lane
-// (li, lg) as rows 4 lg + r, column li.  Split K (grid.z > 1): slice z covers k in [z kc,
-// (z + 1) kc) and writes its partial product to part[z] ([m, n]); a second pass sums them.
+// staged through LDS with 16-byte loads along whichever index has stride 1, and sit there as
+// [row][16 k] (row pitch GT_LDK).  MFMA 16x16x4 f32: lane (li, lg) gives A(row li, k) and
+// B(k, col li) for the instruction's k index lg; the result sits in lane (li, lg) as rows
+// 4 lg + r, column li.  The four MFMAs s = 0..3 of a stage give lane group lg the stage's k
+// = 4 lg + s (the sum over k does not depend on which instruction adds which term), so a
+// lane's fragments for a whole stage are one 16-byte LDS read per 16-row block.  Split K
+// (grid.z > 1): slice z covers k in [z kc, (z + 1) kc) and writes its partial product to
+// part[z] ([m, n]); a second pass sums them.
 constexpr int GT_M = 128, GT_N = 128, GT_K = 16;
-constexpr int GT_LD = GT_M + 4;  // LDS row (one k) of a staged operand tile, floats
+constexpr int GT_LDK = GT_K + 4;  // LDS row pitch, floats: 16-lane groups of 16-byte reads hit 64 banks once
 
-// Loads a 128 x 16 (rows x k) operand tile with element (r, k) at p[r * sr + k * sk] into
-// registers (`v`, two float4 per thread); rows >= rows_left or k >= k_left read 0.
+// A 128 x 16 (rows x k) operand tile with element (r, k) at p[r * sr + k * sk], two float4
+// per thread.  MODE 1: k contiguous (float4 = 4 k of a row; k extent a multiple of 4); MODE 2:
+// rows contiguous (float4 = 4 rows at one k; row extent a multiple of 4); MODE 0: any strides.
+// Loads go to clamped, always valid addresses with no branches (so the next stage's loads all
+// fly at once during this stage's MFMAs); rows >= rows_left or k >= k_left are zeroed when the
+// tile is written to LDS, after the MFMAs.
 struct TileRegs {
   float4 v[2];
 };
 
+template <int MODE>
 __device__ __forceinline__ TileRegs load_tile(const float *__restrict__ p, int64_t sr, int64_t sk, int rows_left,
-                                              int k_left, int tid, int mode) {
+                                              int k_left, int tid) {
   TileRegs t;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int idx = tid + e * 256;  // 512 float4 = 2048 floats
-    float4 v = {0.f, 0.f, 0.f, 0.f};
-    if (mode == 1) {  // k contiguous: 128 rows x 4 groups of 4 k
+    if constexpr (MODE == 2) {      // 32 groups of 4 rows x 16 k (k fastest across lanes)
+      const int k = idx & 15, r = (idx >> 4) * 4;
+      const int rc = max(0, min(r, rows_left - 4)), kc = min(k, k_left - 1);
+      t.v[e] = *reinterpret_cast<const float4 *>(p + int64_t(kc) * sk + rc);
+    } else if constexpr (MODE == 1) {  // 128 rows x 4 groups of 4 k
       const int r = idx >> 2, k = (idx & 3) * 4;
-      if (r < rows_left) {
-        const float *q = p + int64_t(r) * sr + k;
-        if (k + 3 < k_left) {
-          v = *reinterpret_cast<const float4 *>(q);
-        } else {
-          if (k < k_left) v.x = q[0];
-          if (k + 1 < k_left) v.y = q[1];
-          if (k + 2 < k_left) v.z = q[2];
-        }
-      }
-    } else if (mode == 2) {  // rows contiguous: 16 k x 32 groups of 4 rows
-      const int k = idx >> 5, r = (idx & 31) * 4;
-      if (k < k_left) {
-        const float *q = p + int64_t(k) * sk + r;
-        if (r + 3 < rows_left) {
-          v = *reinterpret_cast<const float4 *>(q);
-        } else {
-          if (r < rows_left) v.x = q[0];
-          if (r + 1 < rows_left) v.y = q[1];
-          if (r + 2 < rows_left) v.z = q[2];
-        }
-      }
-    } else {  // general strides: element by element, same slots as mode 1
+      const int rc = min(r, rows_left - 1), kc = max(0, min(k, k_left - 4));
+      t.v[e] = *reinterpret_cast<const float4 *>(p + int64_t(rc) * sr + kc);
+    } else {  // same slots as MODE 1, element by element
       const int r = idx >> 2, k = (idx & 3) * 4;
-      float x[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) x[c] = (r < rows_left && k + c < k_left) ? p[int64_t(r) * sr + int64_t(k + c) * sk] : 0.f;
-      v = float4{x[0], x[1], x[2], x[3]};
+      const int64_t base = int64_t(min(r, rows_left - 1)) * sr;
+      t.v[e] = float4{p[base + int64_t(min(k, k_left - 1)) * sk], p[base + int64_t(min(k + 1, k_left - 1)) * sk],
+                      p[base + int64_t(min(k + 2, k_left - 1)) * sk], p[base + int64_t(min(k + 3, k_left - 1)) * sk]};
     }
-    t.v[e] = v;
   }
   return t;
 }
 
-__device__ __forceinline__ void store_tile(float *lds, const TileRegs &t, int tid, int mode) {
+template <int MODE>
+__device__ __forceinline__ void store_tile(float *lds, const TileRegs &t, int tid, int rows_left, int k_left) {
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int idx = tid + e * 256;
-    if (mode == 2) {
-      const int k = idx >> 5, r = (idx & 31) * 4;
-      *reinterpret_cast<float4 *>(lds + k * GT_LD + r) = t.v[e];
+    const float4 v = t.v[e];
+    if constexpr (MODE == 2) {
+      const int k = idx & 15, r = (idx >> 4) * 4;
+      const bool ok = k < k_left && r < rows_left;  // row extent a multiple of 4: all four rows or none
+      lds[(r + 0) * GT_LDK + k] = ok ? v.x : 0.f;
+      lds[(r + 1) * GT_LDK + k] = ok ? v.y : 0.f;
+      lds[(r + 2) * GT_LDK + k] = ok ? v.z : 0.f;
+      lds[(r + 3) * GT_LDK + k] = ok ? v.w : 0.f;
     } else {
       const int r = idx >> 2, k = (idx & 3) * 4;
-      lds[(k + 0) * GT_LD + r] = t.v[e].x;
-      lds[(k + 1) * GT_LD + r] = t.v[e].y;
-      lds[(k + 2) * GT_LD + r] = t.v[e].z;
-      lds[(k + 3) * GT_LD + r] = t.v[e].w;
+      const bool row = r < rows_left;
+      float4 o;
+      if constexpr (MODE == 1) {
+        const bool ok = row && k < k_left;  // k extent a multiple of 4
+        o = ok ? v : float4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        o = float4{row && k < k_left ? v.x : 0.f, row && k + 1 < k_left ? v.y : 0.f, row && k + 2 < k_left ? v.z : 0.f,
+                   row && k + 3 < k_left ? v.w : 0.f};
+      }
+      *reinterpret_cast<float4 *>(lds + r * GT_LDK + k) = o;
     }
   }
 }
 
-__device__ __forceinline__ int tile_mode(const float *p, int64_t sr, int64_t sk) {
-  const bool al = (reinterpret_cast<uintptr_t>(p) & 15) == 0;
-  if (sk == 1 && (sr & 3) == 0 && al) return 1;
-  if (sr == 1 && (sk & 3) == 0 && al) return 2;
-  return 0;
-}
-
-__global__ __launch_bounds__(256) void gemm_strided_kernel(int32_t M, int32_t N, int32_t K, int32_t kc, float alpha,
+template <int AM, int BM>
+__global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t N, int32_t K, int32_t kc, float alpha,
                                                            const float *__restrict__ A, int64_t sam, int64_t sak,
                                                            const float *__restrict__ B, int64_t sbk, int64_t sbn,
                                                            float beta, float *__restrict__ C, int64_t ldc,
                                                            float *__restrict__ part, const Epi epi) {
-  __shared__ __align__(16) float as[2][GT_K * GT_LD];
-  __shared__ __align__(16) float bs[2][GT_K * GT_LD];
+  __shared__ __align__(16) float as[2][GT_M * GT_LDK];
+  __shared__ __align__(16) float bs[2][GT_N * GT_LDK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 15, lg = lane >> 4;
-  const int m0 = blockIdx.y * GT_M, n0 = blockIdx.x * GT_N;
+  int mt = blockIdx.y, nt = blockIdx.x;
+  if (gridDim.z == 1) {  // XCD-aware order: XCD k (block ids = k mod 8) takes a contiguous run of
+                         // tiles, N fastest, so the rows of A it reads stay in its own L2
+    const int tiles = gridDim.x * gridDim.y, b = blockIdx.x + gridDim.x * blockIdx.y;
+    const int xcd = b & 7, per = tiles >> 3, extra = tiles & 7;
+    const int t = xcd * per + min(xcd, extra) + (b >> 3);
+    mt = t / gridDim.x;
+    nt = t % gridDim.x;
+  }
+  const int m0 = mt * GT_M, n0 = nt * GT_N;
   const int kbeg = blockIdx.z * kc, kend = min(K, kbeg + kc);
   const float *a0 = A + int64_t(m0) * sam, *b0 = B + int64_t(n0) * sbn;
-  const int amode = tile_mode(a0, sam, sak), bmode = tile_mode(b0, sbn, sbk);
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   int buf = 0;
+  const int ma = M - m0, nb_ = N - n0;
   if (kbeg < kend) {
-    store_tile(as[0], load_tile(a0 + int64_t(kbeg) * sak, sam, sak, M - m0, kend - kbeg, tid, amode), tid, amode);
-    store_tile(bs[0], load_tile(b0 + int64_t(kbeg) * sbk, sbn, sbk, N - n0, kend - kbeg, tid, bmode), tid, bmode);
+    store_tile<AM>(as[0], load_tile<AM>(a0 + int64_t(kbeg) * sak, sam, sak, ma, kend - kbeg, tid), tid, ma,
+                   kend - kbeg);
+    store_tile<BM>(bs[0], load_tile<BM>(b0 + int64_t(kbeg) * sbk, sbn, sbk, nb_, kend - kbeg, tid), tid, nb_,
+                   kend - kbeg);
   }
   __syncthreads();
   for (int k0 = kbeg; k0 < kend; k0 += GT_K) {
     const bool more = k0 + GT_K < kend;
+    const int kl = kend - k0 - GT_K;  // k left after this stage
     TileRegs na, nb;
     if (more) {  // the next stage's loads fly during this stage's MFMAs
-      na = load_tile(a0 + int64_t(k0 + GT_K) * sak, sam, sak, M - m0, kend - k0 - GT_K, tid, amode);
-      nb = load_tile(b0 + int64_t(k0 + GT_K) * sbk, sbn, sbk, N - n0, kend - k0 - GT_K, tid, bmode);
+      na = load_tile<AM>(a0 + int64_t(k0 + GT_K) * sak, sam, sak, ma, kl, tid);
+      nb = load_tile<BM>(b0 + int64_t(k0 + GT_K) * sbk, sbn, sbk, nb_, kl, tid);
     }
     const float *ta = as[buf], *tb = bs[buf];
+    f32x4 bf[4];
 #pragma unroll
-    for (int ks = 0; ks < GT_K; ks += 4) {
-      float af[4], bf[4];
+    for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const f32x4 *>(tb + (wn * 64 + j * 16 + li) * GT_LDK + 4 * lg);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = ta[(ks + lg) * GT_LD + wm * 64 + i * 16 + li];
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 af = *reinterpret_cast<const f32x4 *>(ta + (wm * 64 + i * 16 + li) * GT_LDK + 4 * lg);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = tb[(ks + lg) * GT_LD + wn * 64 + j * 16 + li];
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[s], bf[j][s], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      store_tile(as[buf ^ 1], na, tid, amode);
-      store_tile(bs[buf ^ 1], nb, tid, bmode);
+      store_tile<AM>(as[buf ^ 1], na, tid, ma, kl);
+      store_tile<BM>(bs[buf ^ 1], nb, tid, nb_, kl);
     }
     __syncthreads();
     buf ^= 1;
@@ -989,7 +996,26 @@ void gemm_launch(int32_t m, int32_t n, int32_t k, float alpha, const float *a, i
   CG_REQUIRE(grid.y <= 65535, CG_ERR_UNSUPPORTED, "GEMM: too many row tiles");
   hipStream_t s = as_stream(stream);
   float *part = sk.slices > 1 ? static_cast<float *>(workspace) : nullptr;
-  gemm_strided_kernel<<<grid, 256, 0, s>>>(m, n, k, sk.kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, part, epi);
+  // Operand modes (rows, k): A is (m, k) with strides (sam, sak), B is (n, k) with (sbn, sbk).
+  auto mode_of = [](const float *p, int64_t sr, int64_t sk, int32_t rows, int32_t kk) {
+    if (!aligned16(p)) return 0;
+    if (sk == 1 && sr % 4 == 0 && kk % 4 == 0) return 1;
+    if (sr == 1 && sk % 4 == 0 && rows % 4 == 0) return 2;
+    return 0;
+  };
+  int am = mode_of(a, sam, sak, m, k), bm = mode_of(b, sbn, sbk, n, k);
+  if (am == 0 || bm == 0) am = bm = 0;
+  const int32_t kc = sk.kc;
+#define CG_GEMM_CASE(A_, B_)                                                                                    \
+  if (am == A_ && bm == B_)                                                                                     \
+    gemm_strided_kernel<A_, B_><<<grid, 256, 0, s>>>(m, n, k, kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, \
+                                                     part, epi);
+  CG_GEMM_CASE(1, 1)
+  CG_GEMM_CASE(1, 2)
+  CG_GEMM_CASE(2, 1)
+  CG_GEMM_CASE(2, 2)
+  CG_GEMM_CASE(0, 0)
+#undef CG_GEMM_CASE
   CG_LAUNCHED();
   if (part) {
     gemm_reduce_kernel<<<grid_1d(int64_t(m) * n), 256, 0, s>>>(m, n, sk.slices, alpha, part, beta, c, ldc, epi);
