@@ -71,23 +71,24 @@ __device__ __forceinline__ void epilogue(const Epi &e, float v, float beta, floa
 constexpr int GT_M = 128, GT_N = 128, GT_K = 16;
 constexpr int GT_LDK = GT_K + 4;  // LDS row pitch, floats: 16-lane groups of 16-byte reads hit 64 banks once
 
-// A 128 x 16 (rows x k) operand tile with element (r, k) at p[r * sr + k * sk], two float4
-// per thread.  MODE 1: k contiguous (float4 = 4 k of a row; k extent a multiple of 4); MODE 2:
+// A ROWS x 16 (rows x k) operand tile (ROWS 64 or 128) with element (r, k) at p[r * sr + k *
+// sk], ROWS / 64 float4 per thread.  MODE 1: k contiguous (float4 = 4 k of a row; k extent a multiple of 4); MODE 2:
 // rows contiguous (float4 = 4 rows at one k; row extent a multiple of 4); MODE 0: any strides.
 // Loads go to clamped, always valid addresses with no branches (so the next stage's loads all
 // fly at once during this stage's MFMAs); rows >= rows_left or k >= k_left are zeroed when the
 // tile is written to LDS, after the MFMAs.
+template <int ROWS>
 struct TileRegs {
-  float4 v[2];
+  float4 v[ROWS / 64];
 };
 
-template <int MODE>
-__device__ __forceinline__ TileRegs load_tile(const float *__restrict__ p, int64_t sr, int64_t sk, int rows_left,
-                                              int k_left, int tid) {
-  TileRegs t;
+template <int MODE, int ROWS>
+__device__ __forceinline__ TileRegs<ROWS> load_tile(const float *__restrict__ p, int64_t sr, int64_t sk, int rows_left,
+                                                    int k_left, int tid) {
+  TileRegs<ROWS> t;
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int idx = tid + e * 256;  // 512 float4 = 2048 floats
+  for (int e = 0; e < ROWS / 64; ++e) {
+    const int idx = tid + e * 256;  // ROWS x 16 floats = ROWS * 4 float4
     if constexpr (MODE == 2) {      // 32 groups of 4 rows x 16 k (k fastest across lanes)
       const int k = idx & 15, r = (idx >> 4) * 4;
       const int rc = max(0, min(r, rows_left - 4)), kc = min(k, k_left - 1);
@@ -106,10 +107,10 @@ __device__ __forceinline__ TileRegs load_tile(const float *__restrict__ p, int64
   return t;
 }
 
-template <int MODE>
-__device__ __forceinline__ void store_tile(float *lds, const TileRegs &t, int tid, int rows_left, int k_left) {
+template <int MODE, int ROWS>
+__device__ __forceinline__ void store_tile(float *lds, const TileRegs<ROWS> &t, int tid, int rows_left, int k_left) {
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
+  for (int e = 0; e < ROWS / 64; ++e) {
     const int idx = tid + e * 256;
     const float4 v = t.v[e];
     if constexpr (MODE == 2) {
@@ -135,13 +136,14 @@ __device__ __forceinline__ void store_tile(float *lds, const TileRegs &t, int ti
   }
 }
 
-template <int AM, int BM>
+template <int AM, int BM, int TM>
 __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t N, int32_t K, int32_t kc, float alpha,
                                                            const float *__restrict__ A, int64_t sam, int64_t sak,
                                                            const float *__restrict__ B, int64_t sbk, int64_t sbn,
                                                            float beta, float *__restrict__ C, int64_t ldc,
                                                            float *__restrict__ part, const Epi epi) {
-  __shared__ __align__(16) float as[2][GT_M * GT_LDK];
+  constexpr int FM = TM / 32;  // 16-row MFMA blocks per wave: a wave takes TM / 2 rows x 64 columns
+  __shared__ __align__(16) float as[2][TM * GT_LDK];
   __shared__ __align__(16) float bs[2][GT_N * GT_LDK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -155,57 +157,58 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
     mt = t / gridDim.x;
     nt = t % gridDim.x;
   }
-  const int m0 = mt * GT_M, n0 = nt * GT_N;
+  const int m0 = mt * TM, n0 = nt * GT_N;
   const int kbeg = blockIdx.z * kc, kend = min(K, kbeg + kc);
   const float *a0 = A + int64_t(m0) * sam, *b0 = B + int64_t(n0) * sbn;
-  f32x4 acc[4][4];
+  f32x4 acc[FM][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   int buf = 0;
   const int ma = M - m0, nb_ = N - n0;
   if (kbeg < kend) {
-    store_tile<AM>(as[0], load_tile<AM>(a0 + int64_t(kbeg) * sak, sam, sak, ma, kend - kbeg, tid), tid, ma,
-                   kend - kbeg);
-    store_tile<BM>(bs[0], load_tile<BM>(b0 + int64_t(kbeg) * sbk, sbn, sbk, nb_, kend - kbeg, tid), tid, nb_,
-                   kend - kbeg);
+    store_tile<AM, TM>(as[0], load_tile<AM, TM>(a0 + int64_t(kbeg) * sak, sam, sak, ma, kend - kbeg, tid), tid, ma,
+                       kend - kbeg);
+    store_tile<BM, GT_N>(bs[0], load_tile<BM, GT_N>(b0 + int64_t(kbeg) * sbk, sbn, sbk, nb_, kend - kbeg, tid), tid,
+                         nb_, kend - kbeg);
   }
   __syncthreads();
   for (int k0 = kbeg; k0 < kend; k0 += GT_K) {
     const bool more = k0 + GT_K < kend;
     const int kl = kend - k0 - GT_K;  // k left after this stage
-    TileRegs na, nb;
+    TileRegs<TM> na;
+    TileRegs<GT_N> nb;
     if (more) {  // the next stage's loads fly during this stage's MFMAs
-      na = load_tile<AM>(a0 + int64_t(k0 + GT_K) * sak, sam, sak, ma, kl, tid);
-      nb = load_tile<BM>(b0 + int64_t(k0 + GT_K) * sbk, sbn, sbk, nb_, kl, tid);
+      na = load_tile<AM, TM>(a0 + int64_t(k0 + GT_K) * sak, sam, sak, ma, kl, tid);
+      nb = load_tile<BM, GT_N>(b0 + int64_t(k0 + GT_K) * sbk, sbn, sbk, nb_, kl, tid);
     }
     const float *ta = as[buf], *tb = bs[buf];
     f32x4 bf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const f32x4 *>(tb + (wn * 64 + j * 16 + li) * GT_LDK + 4 * lg);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x4 af = *reinterpret_cast<const f32x4 *>(ta + (wm * 64 + i * 16 + li) * GT_LDK + 4 * lg);
+    for (int i = 0; i < FM; ++i) {
+      const f32x4 af = *reinterpret_cast<const f32x4 *>(ta + (wm * (TM / 2) + i * 16 + li) * GT_LDK + 4 * lg);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[s], bf[j][s], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      store_tile<AM>(as[buf ^ 1], na, tid, ma, kl);
-      store_tile<BM>(bs[buf ^ 1], nb, tid, nb_, kl);
+      store_tile<AM, TM>(as[buf ^ 1], na, tid, ma, kl);
+      store_tile<BM, GT_N>(bs[buf ^ 1], nb, tid, nb_, kl);
     }
     __syncthreads();
     buf ^= 1;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * lg + r, n = n0 + wn * 64 + j * 16 + li;
+        const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lg + r, n = n0 + wn * 64 + j * 16 + li;
         if (m >= M || n >= N) continue;
         if (part)
           part[(int64_t(blockIdx.z) * M + m) * N + n] = acc[i][j][r];
@@ -225,13 +228,18 @@ __global__ void gemm_reduce_kernel(int32_t M, int32_t N, int32_t slices, float a
   }
 }
 
-// Split-K plan: enough (tile, slice) blocks to fill the chip when the output has few tiles
-// and the reduction is long (weight gradients reduce over every token).
-struct SplitK {
-  int slices, kc;
+// Launch plan: row tile TM and split K.  A short reduction over few 128-row tiles takes
+// 64-row tiles (twice the blocks, no second pass); a long reduction into a small output (the
+// weight gradients reduce over every token) is split over k into enough (tile, slice) blocks
+// to fill the chip, and a second pass sums the slices.
+struct GemmPlan {
+  int tm, slices, kc;
 };
-SplitK split_k(int32_t m, int32_t n, int32_t k) {
-  const int64_t tiles = int64_t((m + GT_M - 1) / GT_M) * ((n + GT_N - 1) / GT_N);
+GemmPlan gemm_plan(int32_t m, int32_t n, int32_t k, bool generic) {
+  const int64_t nt = (n + GT_N - 1) / GT_N, tiles128 = int64_t((m + GT_M - 1) / GT_M) * nt;
+  int tm = GT_M;
+  if (!generic && m > 64 && tiles128 < 512 && !(k >= 1024 && tiles128 < 128)) tm = 64;
+  const int64_t tiles = int64_t((m + tm - 1) / tm) * nt;
   int slices = 1;
   if (tiles < 512 && k >= 4 * GT_K * 16) {
     slices = int(std::min<int64_t>((512 + tiles - 1) / tiles, k / (GT_K * 16)));
@@ -239,7 +247,7 @@ SplitK split_k(int32_t m, int32_t n, int32_t k) {
   }
   const int kc = ((k + slices - 1) / slices + GT_K - 1) / GT_K * GT_K;
   slices = (k + kc - 1) / kc;
-  return {slices, kc};
+  return {tm, slices, kc};
 }
 
 // ---- LayerNorm / RMSNorm -----------------------------------------------------------------
@@ -978,7 +986,21 @@ void check_attn_train(const cg_attn_train *p) {
              CG_ERR_INVALID, "attention q / k / v: 16-byte aligned rows (pointers and row strides)");
 }
 
-size_t gemm_workspace_bytes(int32_t m, int32_t n, int32_t k);
+// Operand mode (rows, k) of a GEMM input: 1 k contiguous, 2 rows contiguous, 0 any strides.
+int operand_mode(const float *p, int64_t sr, int64_t sk, int32_t rows, int32_t kk) {
+  if (!aligned16(p)) return 0;
+  if (sk == 1 && sr % 4 == 0 && kk % 4 == 0) return 1;
+  if (sr == 1 && sk % 4 == 0 && rows % 4 == 0) return 2;
+  return 0;
+}
+
+GemmPlan plan_of(int32_t m, int32_t n, int32_t k, const float *a, int64_t sam, int64_t sak, const float *b,
+                 int64_t sbk, int64_t sbn, int *am, int *bm) {
+  *am = operand_mode(a, sam, sak, m, k);
+  *bm = operand_mode(b, sbn, sbk, n, k);
+  if (*am == 0 || *bm == 0) *am = *bm = 0;
+  return gemm_plan(m, n, k, *am == 0);
+}
 
 void gemm_launch(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
                  const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *workspace,
@@ -988,45 +1010,47 @@ void gemm_launch(int32_t m, int32_t n, int32_t k, float alpha, const float *a, i
   CG_REQUIRE(a && b && c, CG_ERR_INVALID, "a, b and c are required");
   CG_REQUIRE((epi.mode != EPI_GELU || epi.aux_out) && (epi.mode != EPI_GELU_GRAD || epi.aux_in), CG_ERR_INVALID,
              "GEMM epilogue: GELU needs its second output, GELU' its pre-activation");
-  const SplitK sk = split_k(m, n, k);
-  const size_t need = gemm_workspace_bytes(m, n, k);
+  int am, bm;
+  const GemmPlan pl = plan_of(m, n, k, a, sam, sak, b, sbk, sbn, &am, &bm);
+  const size_t need = pl.slices > 1 ? size_t(pl.slices) * size_t(m) * size_t(n) * 4 : 0;
   CG_REQUIRE(need == 0 || (workspace && workspace_size >= need), CG_ERR_INVALID,
              "GEMM: workspace too small, need " + std::to_string(need) + " bytes");
-  const dim3 grid(unsigned((n + GT_N - 1) / GT_N), unsigned((m + GT_M - 1) / GT_M), unsigned(sk.slices));
+  const dim3 grid(unsigned((n + GT_N - 1) / GT_N), unsigned((m + pl.tm - 1) / pl.tm), unsigned(pl.slices));
   CG_REQUIRE(grid.y <= 65535, CG_ERR_UNSUPPORTED, "GEMM: too many row tiles");
   hipStream_t s = as_stream(stream);
-  float *part = sk.slices > 1 ? static_cast<float *>(workspace) : nullptr;
-  // Operand modes (rows, k): A is (m, k) with strides (sam, sak), B is (n, k) with (sbn, sbk).
-  auto mode_of = [](const float *p, int64_t sr, int64_t sk, int32_t rows, int32_t kk) {
-    if (!aligned16(p)) return 0;
-    if (sk == 1 && sr % 4 == 0 && kk % 4 == 0) return 1;
-    if (sr == 1 && sk % 4 == 0 && rows % 4 == 0) return 2;
-    return 0;
-  };
-  int am = mode_of(a, sam, sak, m, k), bm = mode_of(b, sbn, sbk, n, k);
-  if (am == 0 || bm == 0) am = bm = 0;
-  const int32_t kc = sk.kc;
-#define CG_GEMM_CASE(A_, B_)                                                                                    \
-  if (am == A_ && bm == B_)                                                                                     \
-    gemm_strided_kernel<A_, B_><<<grid, 256, 0, s>>>(m, n, k, kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, \
-                                                     part, epi);
-  CG_GEMM_CASE(1, 1)
-  CG_GEMM_CASE(1, 2)
-  CG_GEMM_CASE(2, 1)
-  CG_GEMM_CASE(2, 2)
-  CG_GEMM_CASE(0, 0)
+  float *part = pl.slices > 1 ? static_cast<float *>(workspace) : nullptr;
+  const int32_t kc = pl.kc;
+#define CG_GEMM_CASE(A_, B_, T_)                                                                             \
+  if (am == A_ && bm == B_ && pl.tm == T_)                                                                   \
+    gemm_strided_kernel<A_, B_, T_><<<grid, 256, 0, s>>>(m, n, k, kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, \
+                                                         ldc, part, epi);
+  CG_GEMM_CASE(1, 1, 128)
+  CG_GEMM_CASE(1, 2, 128)
+  CG_GEMM_CASE(2, 1, 128)
+  CG_GEMM_CASE(2, 2, 128)
+  CG_GEMM_CASE(1, 1, 64)
+  CG_GEMM_CASE(1, 2, 64)
+  CG_GEMM_CASE(2, 1, 64)
+  CG_GEMM_CASE(2, 2, 64)
+  CG_GEMM_CASE(0, 0, 128)
 #undef CG_GEMM_CASE
   CG_LAUNCHED();
   if (part) {
-    gemm_reduce_kernel<<<grid_1d(int64_t(m) * n), 256, 0, s>>>(m, n, sk.slices, alpha, part, beta, c, ldc, epi);
+    gemm_reduce_kernel<<<grid_1d(int64_t(m) * n), 256, 0, s>>>(m, n, pl.slices, alpha, part, beta, c, ldc, epi);
     CG_LAUNCHED();
   }
 }
 
+// Split-K partials of a GEMM (an upper bound over the operand layouts: the generic layout
+// never splits more than the others).
 size_t gemm_workspace_bytes(int32_t m, int32_t n, int32_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
-  const SplitK sk = split_k(m, n, k);
-  return sk.slices > 1 ? size_t(sk.slices) * size_t(m) * size_t(n) * 4 : 0;
+  size_t most = 0;
+  for (bool generic : {false, true}) {
+    const GemmPlan pl = gemm_plan(m, n, k, generic);
+    if (pl.slices > 1) most = std::max(most, size_t(pl.slices) * size_t(m) * size_t(n) * 4);
+  }
+  return most;
 }
 
 // Grid of the forward and dQ kernels: blocks of 16 tokens x four heads of a group, or more
