@@ -60,6 +60,11 @@ def parse() -> argparse.Namespace:
         help="run only the decode-attention launches of the timed steps and a 256 MiB calibration copy "
         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), then exit",
     )
+    p.add_argument(
+        "--train-probe", action="store_true",
+        help="run only the fp32 training step (our path, no reference) and print its timings, then exit "
+        "(for a rocprofv3 kernel trace of the training kernels)",
+    )
     return p.parse_args()
 
 
@@ -623,6 +628,9 @@ def main() -> int:
         print(json.dumps({"probe": "traffic", "kernel": roof["kernel"], "launches": roof["launches"],
                           "algorithmic_bytes_per_launch": roof["algorithmic_bytes_per_launch"],
                           "copy_bytes": src.numel(), "copy_launches": 4}), flush=True)
+        return 0
+    if args.train_probe:
+        print(json.dumps({"probe": "train_step", **train_step_time(bench, with_reference=False)}), flush=True)
         return 0
     with torch.no_grad():
         bench.load(0)

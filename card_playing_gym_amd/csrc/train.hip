@@ -26,12 +26,27 @@ namespace {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
-// erf GELU and its derivative Phi(u) + u phi(u).
-__device__ __forceinline__ float gelu_exact(float u) { return 0.5f * u * (1.0f + erff(u * 0.70710678118654752f)); }
+// erf by Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26:
+// erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-x^2), t = 1 / (1 + p x) for x >= 0
+// (odd in x), |error| <= 1.5e-7.  `gauss` receives e^(-x^2), which GELU's derivative reuses.
+__device__ __forceinline__ float erf_as(float x, float &gauss) {
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, ax, 1.0f));
+  const float poly =
+      t * fmaf(t, fmaf(t, fmaf(t, fmaf(t, 1.061405429f, -1.453152027f), 1.421413741f), -0.284496736f), 0.254829592f);
+  gauss = __expf(-ax * ax);
+  return copysignf(1.0f - poly * gauss, x);
+}
+
+// erf GELU, u Phi(u), and its derivative Phi(u) + u phi(u) (phi(u) = e^(-u^2 / 2) / sqrt(2 pi)).
+__device__ __forceinline__ float gelu_exact(float u) {
+  float gauss;
+  return 0.5f * u * (1.0f + erf_as(u * 0.70710678118654752f, gauss));
+}
 __device__ __forceinline__ float gelu_grad(float u) {
-  const float cdf = 0.5f * (1.0f + erff(u * 0.70710678118654752f));
-  const float pdf = 0.3989422804014327f * expf(-0.5f * u * u);
-  return cdf + u * pdf;
+  float gauss;
+  const float cdf = 0.5f * (1.0f + erf_as(u * 0.70710678118654752f, gauss));
+  return fmaf(u * 0.3989422804014327f, gauss, cdf);
 }
 
 // What a GEMM does with each result v = alpha (A B)[m, n] on its way out: add beta times the
@@ -202,19 +217,56 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
     __syncthreads();
     buf ^= 1;
   }
+  if (part) {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lg + r, n = n0 + wn * 64 + j * 16 + li;
+          if (m < M && n < N) part[(int64_t(blockIdx.z) * M + m) * N + n] = acc[i][j][r];
+        }
+    return;
+  }
+  // Epilogue: every operand it reads (prior C or cin, bias, aux_in) is loaded for a whole
+  // 16-row block at once from clamped, always valid addresses, and unused values are dropped by
+  // selects, so the loads overlap instead of waiting one by one behind per-element branches.
+  const bool prior = beta != 0.f, grad = epi.mode == EPI_GELU_GRAD, fwd_gelu = epi.mode == EPI_GELU;
+  const float *pin = epi.cin ? epi.cin : C, *ain = grad ? epi.aux_in : C;
+  float bj[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = min(n0 + wn * 64 + j * 16 + li, N - 1);
+    bj[j] = epi.bias ? epi.bias[n] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    float pv[4][4], av[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = min(m0 + wm * (TM / 2) + i * 16 + 4 * lg + r, M - 1), n = min(n0 + wn * 64 + j * 16 + li, N - 1);
+        pv[j][r] = pin[m * ldc + n];
+        av[j][r] = ain[m * ldc + n];
+      }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lg + r, n = n0 + wn * 64 + j * 16 + li;
-        if (m >= M || n >= N) continue;
-        if (part)
-          part[(int64_t(blockIdx.z) * M + m) * N + n] = acc[i][j][r];
-        else
-          epilogue(epi, alpha * acc[i][j][r], beta, C, ldc, m, n);
+        float v = alpha * acc[i][j][r];
+        if (prior) v += beta * pv[j][r];
+        v += bj[j];
+        if (grad) v *= gelu_grad(av[j][r]);
+        if (m < M && n < N) {
+          const int64_t o = int64_t(m) * ldc + n;
+          C[o] = v;
+          if (fwd_gelu) epi.aux_out[o] = gelu_exact(v);
+        }
       }
+  }
 }
 
 // C[m, n] = epilogue(alpha * sum_z part[z][m, n]).
