@@ -17,7 +17,7 @@ Also reported (one JSON line on stdout):
   * prefill: forward_prefill throughput at two shapes, beside the reference path on the GPU;
   * piquet_embed: the Piquet token embedder on one 4096-token wave, beside the reference path;
   * piquet_wave: a whole Piquet wave (embedder + 16-layer Piquet trunk step), graph-replayed;
-  * train_step: a fp32 training step (full causal forward + backward) of the 16-layer trunk.
+  * train_step: a training step (full causal forward + backward) of the 16-layer trunk, fp32 and bf16 autocast.
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 10]
 """
@@ -433,11 +433,12 @@ def piquet_wave_time(bench: Bench, with_reference: bool, steps: int = 20) -> dic
 
 
 def train_step_time(bench: Bench, with_reference: bool, warmup: int = 3, reps: int = 5) -> dict:
-    """One PPO-update-shaped training step of the 16-layer trunk in fp32 (the reference's
-    precision = "fp32"): a full causal forward over a batch of sequences, a loss on every
-    hidden state and the backward into every parameter and the input (trunk.py:348-374
-    under autograd).  Wall time per step after `warmup` steps; with `with_reference`, the
-    oracle's restated reference path (SDPA, autograd) on the same GPU."""
+    """One PPO-update-shaped training step of the 16-layer trunk: a full causal forward over a
+    batch of sequences, a loss on every hidden state and the backward into every parameter and
+    the input (trunk.py:348-374 under autograd), in fp32 (the reference's default precision)
+    and under bf16 autocast (its "bf16" precision, cardgym/core/devices.py:32-43).  Wall time
+    per step after `warmup` steps; with `with_reference`, the oracle's restatement of the
+    reference path (SDPA, autograd; under the same autocast) on the same GPU."""
 
     from card_playing_gym_amd.nn.trunk import Trunk
 
@@ -451,38 +452,44 @@ def train_step_time(bench: Bench, with_reference: bool, warmup: int = 3, reps: i
         from oracle.reference_path import RefTrunk, ref_config_of
 
         state = {"trunk." + k: v.detach().clone().requires_grad_() for k, v in trunk.state_dict().items()}
-        ref = RefTrunk(state, ref_config_of(cfg), "fp32")
-    out = {"precision": "fp32"}
-    for batch, length in ((256, 64), (64, 256)):
-        g = torch.Generator(device=dev).manual_seed(batch)
-        x = torch.randn((batch, length, cfg.d_model), generator=g, device=dev).requires_grad_()
-        w = torch.randn((batch, length, cfg.d_model), generator=g, device=dev)
+        ref = RefTrunk(state, ref_config_of(cfg), "fp32")  # autocast applies the bf16 policy itself
+    out = {}
+    for precision in ("fp32", "bf16"):
+        autocast = torch.autocast("cuda", dtype=torch.bfloat16, enabled=precision == "bf16")
+        result = {}
+        for batch, length in ((256, 64), (64, 256)):
+            g = torch.Generator(device=dev).manual_seed(batch)
+            x = torch.randn((batch, length, cfg.d_model), generator=g, device=dev).requires_grad_()
+            w = torch.randn((batch, length, cfg.d_model), generator=g, device=dev)
 
-        def ours():
-            h = trunk(*trunk.condition(x, None, None))
-            (h * w).sum().backward()
+            def ours():
+                with autocast:
+                    h = trunk(*trunk.condition(x, None, None))
+                (h * w).sum().backward()
 
-        def theirs():
-            h = ref.forward_full(*ref.condition(x, None, None))
-            (h * w).sum().backward()
+            def theirs():
+                with autocast:
+                    h = ref.forward_full(*ref.condition(x, None, None))
+                (h * w).sum().backward()
 
-        def wall(fn) -> float:
-            for _ in range(warmup):
-                fn()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                fn()
-            torch.cuda.synchronize()
-            return (time.perf_counter() - t0) / reps
+            def wall(fn) -> float:
+                for _ in range(warmup):
+                    fn()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    fn()
+                torch.cuda.synchronize()
+                return (time.perf_counter() - t0) / reps
 
-        entry = {"tokens": batch * length, "ms_per_step": round(wall(ours) * 1e3, 3)}
-        entry["tokens_per_s"] = round(batch * length / entry["ms_per_step"] * 1e3, 1)
-        if ref is not None:
-            entry["reference_gpu_ms_per_step"] = round(wall(theirs) * 1e3, 3)
-            entry["speedup"] = round(entry["reference_gpu_ms_per_step"] / entry["ms_per_step"], 2)
-        out[f"{batch}x{length}"] = entry
-        trunk.zero_grad(set_to_none=True)
+            entry = {"tokens": batch * length, "ms_per_step": round(wall(ours) * 1e3, 3)}
+            entry["tokens_per_s"] = round(batch * length / entry["ms_per_step"] * 1e3, 1)
+            if ref is not None:
+                entry["reference_gpu_ms_per_step"] = round(wall(theirs) * 1e3, 3)
+                entry["speedup"] = round(entry["reference_gpu_ms_per_step"] / entry["ms_per_step"], 2)
+            result[f"{batch}x{length}"] = entry
+            trunk.zero_grad(set_to_none=True)
+        out[precision] = result
     del trunk, ref
     torch.cuda.empty_cache()
     return out

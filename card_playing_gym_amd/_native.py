@@ -98,13 +98,15 @@ class AttnTrain(ctypes.Structure):
         ("n", c_int32), ("H", c_int32), ("KVH", c_int32), ("head_dim", c_int32), ("scale", c_float),
         ("seq_start", c_void_p), ("seq_of", c_void_p), ("q", c_void_p), ("k", c_void_p), ("v", c_void_p),
         ("ldq", c_int64), ("ldk", c_int64), ("ldv", c_int64), ("o", c_void_p), ("lse", c_void_p),
+        ("round_bf16", c_int32),
     ]
 
 
 class TrainConfig(ctypes.Structure):
     _fields_ = [(name, c_int32) for name in ("d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff", "per_layer_dim",
                                              "ple_width", "value_width")] + [("eps", c_float),
-                                                                             ("value_index", ctypes.POINTER(c_int32))]
+                                                                             ("value_index", ctypes.POINTER(c_int32)),
+                                                                             ("bf16", c_int32)]
 
 
 _TRAIN_BLOCK_FIELDS = ("ln_attn_w", "ln_attn_b", "qkv_w", "out_w", "ln_mlp_w", "ln_mlp_b", "up_w", "up_b", "down_w",
@@ -214,7 +216,7 @@ _SIGNATURES = {
     "cg_gemm_strided": (
         c_int32,
         [c_int32, c_int32, c_int32, c_float, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_float,
-         c_void_p, c_int64, c_void_p, c_size_t, c_void_p],
+         c_void_p, c_int64, c_int32, c_void_p, c_size_t, c_void_p],
     ),
     "cg_layernorm_fwd": (
         c_int32, [c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p],

@@ -25,6 +25,23 @@ namespace cg {
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+
+// bf16 (autocast) precision: values are kept in fp32 storage holding bf16 numbers.  A pair of
+// fp32 values to packed bf16, round to nearest even (v_cvt_pk_bf16_f32): a in the low half.
+__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+// Four consecutive k of an MFMA fragment as the bf16 operand of v_mfma_f32_16x16x16_bf16.
+__device__ __forceinline__ s16x4 bf16x4_of(f32x4 v) {
+  const u32x2 p = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+  return __builtin_bit_cast(s16x4, p);
+}
+// The bf16 value nearest x, as fp32.
+__device__ __forceinline__ float round_bf16(float x) { return __builtin_bit_cast(float, pack_bf16(0.f, x) & 0xffff0000u); }
 
 // erf by Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26:
 // erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-x^2), t = 1 / (1 + p x) for x >= 0
@@ -49,10 +66,12 @@ __device__ __forceinline__ float gelu_grad(float u) {
   return fmaf(u * 0.3989422804014327f, gauss, cdf);
 }
 
-// What a GEMM does with each result v = alpha (A B)[m, n] on its way out: add beta times the
-// prior value (read from `cin` when set, else from C itself), add bias[n], then either
-// multiply by gelu'(aux_in[m, n]) (GELU_GRAD: the MLP's backward) or also write gelu(v) to
-// aux_out[m, n] (GELU: the MLP's forward).  aux_in / aux_out / cin share C's row stride.
+// What a GEMM does with each result v = alpha (A B)[m, n] on its way out: add bias[n], round
+// to bf16 when `round` (autocast: a bf16 product's output), add beta times the prior value
+// (read from `cin` when set, else from C itself: the fp32 residual), then either multiply by
+// gelu'(aux_in[m, n]) (GELU_GRAD: the MLP's backward; rounded again under `round`) or also
+// write gelu(v) to aux_out[m, n] (GELU: the MLP's forward; rounded under `round`).
+// aux_in / aux_out / cin share C's row stride.
 enum EpiMode : int32_t { EPI_PLAIN = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2 };
 struct Epi {
   const float *bias = nullptr;
@@ -60,16 +79,27 @@ struct Epi {
   const float *aux_in = nullptr;
   float *aux_out = nullptr;
   int32_t mode = EPI_PLAIN;
+  int32_t round = 0;  // bf16 operands (the GEMM rounds them as it stages) and bf16 outputs
 };
+
+__device__ __forceinline__ float epi_value(const Epi &e, float v, float beta, float prior, float bias, float aux) {
+  v += bias;
+  if (e.round) v = round_bf16(v);
+  if (beta != 0.f) v += beta * prior;
+  if (e.mode == EPI_GELU_GRAD) {
+    v *= gelu_grad(aux);
+    if (e.round) v = round_bf16(v);
+  }
+  return v;
+}
 
 __device__ __forceinline__ void epilogue(const Epi &e, float v, float beta, float *__restrict__ C, int64_t ldc,
                                          int64_t m, int64_t n) {
   const int64_t i = m * ldc + n;
-  if (beta != 0.f) v += beta * (e.cin ? e.cin[i] : C[i]);
-  if (e.bias) v += e.bias[n];
-  if (e.mode == EPI_GELU_GRAD) v *= gelu_grad(e.aux_in[i]);
+  v = epi_value(e, v, beta, beta != 0.f ? (e.cin ? e.cin[i] : C[i]) : 0.f, e.bias ? e.bias[n] : 0.f,
+                e.mode == EPI_GELU_GRAD ? e.aux_in[i] : 0.f);
   C[i] = v;
-  if (e.mode == EPI_GELU) e.aux_out[i] = gelu_exact(v);
+  if (e.mode == EPI_GELU) e.aux_out[i] = e.round ? round_bf16(gelu_exact(v)) : gelu_exact(v);
 }
 
 // ---- strided GEMM ---------------------------------------------------------------------
@@ -151,7 +181,7 @@ __device__ __forceinline__ void store_tile(float *lds, const TileRegs<ROWS> &t, 
   }
 }
 
-template <int AM, int BM, int TM>
+template <int AM, int BM, int TM, bool BF>
 __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t N, int32_t K, int32_t kc, float alpha,
                                                            const float *__restrict__ A, int64_t sam, int64_t sak,
                                                            const float *__restrict__ B, int64_t sbk, int64_t sbn,
@@ -202,13 +232,27 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
     f32x4 bf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const f32x4 *>(tb + (wn * 64 + j * 16 + li) * GT_LDK + 4 * lg);
+    if constexpr (BF) {  // bf16 operands: the stage's 16 k in one v_mfma_f32_16x16x16_bf16 per tile,
+                         // lane group lg holding k = 4 lg .. 4 lg + 3 as the fp32 path does
+      s16x4 bb[4];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const f32x4 af = *reinterpret_cast<const f32x4 *>(ta + (wm * (TM / 2) + i * 16 + li) * GT_LDK + 4 * lg);
+      for (int j = 0; j < 4; ++j) bb[j] = bf16x4_of(bf[j]);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int i = 0; i < FM; ++i) {
+        const s16x4 ab = bf16x4_of(*reinterpret_cast<const f32x4 *>(ta + (wm * (TM / 2) + i * 16 + li) * GT_LDK + 4 * lg));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[s], bf[j][s], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ab, bb[j], acc[i][j], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const f32x4 af = *reinterpret_cast<const f32x4 *>(ta + (wm * (TM / 2) + i * 16 + li) * GT_LDK + 4 * lg);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[s], bf[j][s], acc[i][j], 0, 0, 0);
+      }
     }
     if (more) {
       store_tile<AM, TM>(as[buf ^ 1], na, tid, ma, kl);
@@ -232,8 +276,8 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
   // Epilogue: every operand it reads (prior C or cin, bias, aux_in) is loaded for a whole
   // 16-row block at once from clamped, always valid addresses, and unused values are dropped by
   // selects, so the loads overlap instead of waiting one by one behind per-element branches.
-  const bool prior = beta != 0.f, grad = epi.mode == EPI_GELU_GRAD, fwd_gelu = epi.mode == EPI_GELU;
-  const float *pin = epi.cin ? epi.cin : C, *ain = grad ? epi.aux_in : C;
+  const bool prior = beta != 0.f, fwd_gelu = epi.mode == EPI_GELU;
+  const float *pin = epi.cin ? epi.cin : C, *ain = epi.mode == EPI_GELU_GRAD ? epi.aux_in : C;
   float bj[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -256,14 +300,11 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m0 + wm * (TM / 2) + i * 16 + 4 * lg + r, n = n0 + wn * 64 + j * 16 + li;
-        float v = alpha * acc[i][j][r];
-        if (prior) v += beta * pv[j][r];
-        v += bj[j];
-        if (grad) v *= gelu_grad(av[j][r]);
+        const float v = epi_value(epi, alpha * acc[i][j][r], beta, prior ? pv[j][r] : 0.f, bj[j], av[j][r]);
         if (m < M && n < N) {
           const int64_t o = int64_t(m) * ldc + n;
           C[o] = v;
-          if (fwd_gelu) epi.aux_out[o] = gelu_exact(v);
+          if (fwd_gelu) epi.aux_out[o] = epi.round ? round_bf16(gelu_exact(v)) : gelu_exact(v);
         }
       }
   }
@@ -497,7 +538,7 @@ __global__ __launch_bounds__(1024) void norm_params_kernel(const float *__restri
 // chunk lands in out[y][c] (a second pass sums the chunks).
 __global__ __launch_bounds__(256) void column_sum_kernel(const float *__restrict__ in, int32_t rows, int32_t cols,
                                                          int64_t ld, float *__restrict__ out, int32_t accumulate,
-                                                         int32_t chunk) {
+                                                         int32_t chunk, int32_t round_in, int32_t round_out) {
   __shared__ float red[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
@@ -505,18 +546,23 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const float *__restrict
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
   if (c < cols) {
     int r = r0 + wave;
+    auto at = [&](int rr) {
+      const float v = in[int64_t(rr) * ld + c];
+      return round_in ? round_bf16(v) : v;
+    };
     for (; r + 12 < r1; r += 16) {
-      s0 += in[int64_t(r) * ld + c];
-      s1 += in[int64_t(r + 4) * ld + c];
-      s2 += in[int64_t(r + 8) * ld + c];
-      s3 += in[int64_t(r + 12) * ld + c];
+      s0 += at(r);
+      s1 += at(r + 4);
+      s2 += at(r + 8);
+      s3 += at(r + 12);
     }
-    for (; r < r1; r += 4) s0 += in[int64_t(r) * ld + c];
+    for (; r < r1; r += 4) s0 += at(r);
   }
   red[wave][lane] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (wave == 0 && c < cols) {
-    const float s = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    float s = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    if (round_out) s = round_bf16(s);
     float *o = out + int64_t(blockIdx.y) * cols + c;
     *o = accumulate ? *o + s : s;
   }
@@ -552,7 +598,10 @@ struct AttnTrain {
   int64_t ldq, ldk, ldv;
   const float *o, *dout, *lse;
   float *out, *lse_out, *dsum, *dq, *dk, *dv;
+  int32_t round;  // bf16 outputs (o, dq, dk, dv), as SDPA on bf16 operands returns them
 };
+
+__device__ __forceinline__ float attn_out(const AttnTrain &a, float v) { return a.round ? round_bf16(v) : v; }
 
 // The three kernels work on 16 x 16 tiles of (query, key) pairs with v_mfma_f32_16x16x4_f32.
 // A contraction over head_dim gives lane (li, lg) the d slice [lg DC, (lg + 1) DC) (DC =
@@ -762,7 +811,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnTrain a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int d = dt * 16 + 4 * lg + r;
-      if (d < D) orow[d] = acc[dt][r] * inv;
+      if (d < D) orow[d] = attn_out(a, acc[dt][r] * inv);
     }
   if (lg == 0) a.lse_out[t * a.H + w.h] = m + logf(l);
 }
@@ -844,7 +893,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnTrain a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int d = dt * 16 + 4 * lg + r;
-      if (d < D) dqrow[d] = acc[dt][r] * a.scale;
+      if (d < D) dqrow[d] = attn_out(a, acc[dt][r] * a.scale);
     }
   if (lg == 0) a.dsum[row] = dsum;
 }
@@ -983,8 +1032,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
     for (int r = 0; r < 4; ++r) {
       const int d = dt * 16 + 4 * lg + r;
       if (d < D) {
-        dkrow[d] = dk[dt][r];
-        dvrow[d] = dv[dt][r];
+        dkrow[d] = attn_out(a, dk[dt][r]);
+        dvrow[d] = attn_out(a, dv[dt][r]);
       }
     }
 }
@@ -1072,10 +1121,16 @@ void gemm_launch(int32_t m, int32_t n, int32_t k, float alpha, const float *a, i
   hipStream_t s = as_stream(stream);
   float *part = pl.slices > 1 ? static_cast<float *>(workspace) : nullptr;
   const int32_t kc = pl.kc;
-#define CG_GEMM_CASE(A_, B_, T_)                                                                             \
-  if (am == A_ && bm == B_ && pl.tm == T_)                                                                   \
-    gemm_strided_kernel<A_, B_, T_><<<grid, 256, 0, s>>>(m, n, k, kc, alpha, a, sam, sak, b, sbk, sbn, beta, c, \
-                                                         ldc, part, epi);
+  const bool bf = epi.round != 0;
+#define CG_GEMM_CASE(A_, B_, T_)                                                                                 \
+  if (am == A_ && bm == B_ && pl.tm == T_) {                                                                     \
+    if (bf)                                                                                                      \
+      gemm_strided_kernel<A_, B_, T_, true><<<grid, 256, 0, s>>>(m, n, k, kc, alpha, a, sam, sak, b, sbk, sbn, beta, \
+                                                                 c, ldc, part, epi);                             \
+    else                                                                                                         \
+      gemm_strided_kernel<A_, B_, T_, false><<<grid, 256, 0, s>>>(m, n, k, kc, alpha, a, sam, sak, b, sbk, sbn,    \
+                                                                  beta, c, ldc, part, epi);                      \
+  }
   CG_GEMM_CASE(1, 1, 128)
   CG_GEMM_CASE(1, 2, 128)
   CG_GEMM_CASE(2, 1, 128)
@@ -1105,6 +1160,47 @@ size_t gemm_workspace_bytes(int32_t m, int32_t n, int32_t k) {
   return most;
 }
 
+size_t column_sum_ws(int32_t rows, int32_t cols) {
+  return rows > 2048 ? size_t((rows + 255) / 256) * size_t(std::max(cols, 0)) * 4 : 0;
+}
+
+// out[c] (+)= sum_r x[r * ld + c]; with `bf16`, the sum of the bf16-rounded entries, rounded to
+// bf16 (a bias gradient under autocast: the sum of a bf16 gradient, returned in bf16).
+void column_sum_launch(const float *x, int32_t rows, int32_t cols, int64_t ld, float *out, int32_t accumulate,
+                       void *workspace, size_t workspace_size, bool bf16, void *stream) {
+  if (cols == 0) return;
+  CG_REQUIRE(x && out && rows >= 0, CG_ERR_INVALID, "column sum operands are required");
+  hipStream_t s = as_stream(stream);
+  const int32_t r = bf16 ? 1 : 0;
+  if (rows <= 2048) {
+    column_sum_kernel<<<dim3(blocks_of(cols, 64), 1), 256, 0, s>>>(x, rows, cols, ld, out, accumulate, rows, r, r);
+    CG_LAUNCHED();
+    return;
+  }
+  const size_t need = column_sum_ws(rows, cols);
+  CG_REQUIRE(workspace && workspace_size >= need, CG_ERR_INVALID, "column sum: workspace too small");
+  const int chunks = (rows + 255) / 256;
+  float *part = static_cast<float *>(workspace);
+  column_sum_kernel<<<dim3(blocks_of(cols, 64), unsigned(chunks)), 256, 0, s>>>(x, rows, cols, ld, part, 0, 256, r, 0);
+  CG_LAUNCHED();
+  column_sum_kernel<<<dim3(blocks_of(cols, 64), 1), 256, 0, s>>>(part, chunks, cols, cols, out, accumulate, chunks, 0,
+                                                                 r);
+  CG_LAUNCHED();
+}
+
+// dst[r, c] = bf16(dst[r, c] + src[r * ld_src + c]): the value embedding added to v in fp32 and
+// rounded once (the attention reads bf16 v).
+__global__ void add_round_kernel(int32_t rows, int32_t cols, const float *__restrict__ src, int64_t ld_src,
+                                 float *__restrict__ dst, int64_t ld_dst) {
+  const int64_t total = int64_t(rows) * cols;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = i / cols;
+    const int c = int(i % cols);
+    float *d = dst + r * ld_dst + c;
+    *d = round_bf16(*d + src[r * ld_src + c]);
+  }
+}
+
 // Grid of the forward and dQ kernels: blocks of 16 tokens x four heads of a group, or more
 // tokens per block when the group has fewer heads.
 dim3 query_grid(const cg_attn_train &p) {
@@ -1123,10 +1219,14 @@ extern "C" {
 size_t cg_gemm_workspace_size(int32_t m, int32_t n, int32_t k) { return gemm_workspace_bytes(m, n, k); }
 
 int cg_gemm_strided(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
-                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *workspace,
-                    size_t workspace_size, void *stream) {
+                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc,
+                    int32_t compute_dtype, void *workspace, size_t workspace_size, void *stream) {
   return guarded([&] {
-    gemm_launch(m, n, k, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, workspace, workspace_size, Epi{}, stream);
+    CG_REQUIRE(compute_dtype == CG_F32 || compute_dtype == CG_BF16, CG_ERR_UNSUPPORTED,
+               "GEMM compute dtype: CG_F32 or CG_BF16");
+    Epi e;
+    e.round = compute_dtype == CG_BF16;
+    gemm_launch(m, n, k, alpha, a, sam, sak, b, sbk, sbn, beta, c, ldc, workspace, workspace_size, e, stream);
   });
 }
 
@@ -1180,30 +1280,11 @@ int cg_norm_bwd(const float *x, const float *dy, const float *w, const float *me
   });
 }
 
-size_t cg_column_sum_workspace_size(int32_t rows, int32_t cols) {
-  return rows > 2048 ? size_t((rows + 255) / 256) * size_t(std::max(cols, 0)) * 4 : 0;
-}
+size_t cg_column_sum_workspace_size(int32_t rows, int32_t cols) { return column_sum_ws(rows, cols); }
 
 int cg_column_sum(const float *x, int32_t rows, int32_t cols, int64_t ld, float *out, int32_t accumulate,
                   void *workspace, size_t workspace_size, void *stream) {
-  return guarded([&] {
-    if (cols == 0) return;
-    CG_REQUIRE(x && out && rows >= 0, CG_ERR_INVALID, "column sum operands are required");
-    hipStream_t s = as_stream(stream);
-    if (rows <= 2048) {
-      column_sum_kernel<<<dim3(blocks_of(cols, 64), 1), 256, 0, s>>>(x, rows, cols, ld, out, accumulate, rows);
-      CG_LAUNCHED();
-      return;
-    }
-    const size_t need = cg_column_sum_workspace_size(rows, cols);
-    CG_REQUIRE(workspace && workspace_size >= need, CG_ERR_INVALID, "column sum: workspace too small");
-    const int chunks = (rows + 255) / 256;
-    float *part = static_cast<float *>(workspace);
-    column_sum_kernel<<<dim3(blocks_of(cols, 64), unsigned(chunks)), 256, 0, s>>>(x, rows, cols, ld, part, 0, 256);
-    CG_LAUNCHED();
-    column_sum_kernel<<<dim3(blocks_of(cols, 64), 1), 256, 0, s>>>(part, chunks, cols, cols, out, accumulate, chunks);
-    CG_LAUNCHED();
-  });
+  return guarded([&] { column_sum_launch(x, rows, cols, ld, out, accumulate, workspace, workspace_size, false, stream); });
 }
 
 int cg_gelu_fwd(const float *u, float *g, int64_t n, void *stream) {
@@ -1259,7 +1340,7 @@ int cg_attn_train_fwd(const cg_attn_train *p, void *stream) {
     check_attn_train(p);
     if (p->n == 0) return;
     AttnTrain a{p->n, p->H, p->KVH, p->scale, p->seq_start, p->seq_of, p->q, p->k, p->v, p->ldq, p->ldk, p->ldv,
-                nullptr, nullptr, nullptr, p->o, p->lse, nullptr, nullptr, nullptr, nullptr};
+                nullptr, nullptr, nullptr, p->o, p->lse, nullptr, nullptr, nullptr, nullptr, p->round_bf16};
     CG_REQUIRE(a.out && a.lse_out, CG_ERR_INVALID, "attention forward outputs are required");
     CG_REQUIRE(aligned16(a.out), CG_ERR_INVALID, "attention output: 16-byte aligned");
     hipStream_t s = as_stream(stream);
@@ -1282,7 +1363,7 @@ int cg_attn_train_bwd(const cg_attn_train *p, const float *dout, float *dsum, fl
     check_attn_train(p);
     if (p->n == 0) return;
     AttnTrain a{p->n, p->H, p->KVH, p->scale, p->seq_start, p->seq_of, p->q, p->k, p->v, p->ldq, p->ldk, p->ldv,
-                p->o, dout, p->lse, nullptr, nullptr, dsum, dq, dk, dv};
+                p->o, dout, p->lse, nullptr, nullptr, dsum, dq, dk, dv, p->round_bf16};
     CG_REQUIRE(a.o && a.dout && a.lse && dsum && dq && dk && dv, CG_ERR_INVALID,
                "attention backward operands are required");
     CG_REQUIRE(aligned16(dout), CG_ERR_INVALID, "attention dO: 16-byte aligned");
@@ -1321,11 +1402,13 @@ void ok(int status) {
 
 struct TrainDims {
   int64_t n, d, F, H, KVH, D, Q, KVW, QKV, L, P, V, pd;
+  bool bf;  // bf16 autocast precision
 };
 
 TrainDims dims_of(const cg_train_config &c, int32_t n) {
   TrainDims t{};
   t.n = n;
+  t.bf = c.bf16 != 0;
   t.d = c.d_model;
   t.F = c.d_ff;
   t.H = c.n_heads;
@@ -1446,21 +1529,26 @@ size_t scratch_bytes(const TrainDims &t) {
 struct Gemm {
   const Scratch &s;
   hipStream_t st;
+  bool bf;  // bf16 operands and outputs (autocast), else fp32
+  Epi with(Epi e) const {
+    e.round = bf ? 1 : 0;
+    return e;
+  }
   // out[M, N] = alpha x[M, K] W[N, K]^T (+ the epilogue's terms)
   void nt(int64_t M, int64_t N, int64_t K, const float *x, const float *w, float *out, float beta = 0.f,
           const Epi &e = Epi{}) const {
-    gemm_launch(int32_t(M), int32_t(N), int32_t(K), 1.f, x, K, 1, w, 1, K, beta, out, N, s.gemm_ws, s.gemm_bytes, e,
-                st);
+    gemm_launch(int32_t(M), int32_t(N), int32_t(K), 1.f, x, K, 1, w, 1, K, beta, out, N, s.gemm_ws, s.gemm_bytes,
+                with(e), st);
   }
   // out[M, K] = dy[M, N] W[N, K]
   void nn(int64_t M, int64_t N, int64_t K, const float *dy, const float *w, float *out, const Epi &e = Epi{}) const {
-    gemm_launch(int32_t(M), int32_t(K), int32_t(N), 1.f, dy, N, 1, w, K, 1, 0.f, out, K, s.gemm_ws, s.gemm_bytes, e,
-                st);
+    gemm_launch(int32_t(M), int32_t(K), int32_t(N), 1.f, dy, N, 1, w, K, 1, 0.f, out, K, s.gemm_ws, s.gemm_bytes,
+                with(e), st);
   }
   // out[N, K] = dy[M, N]^T x[M, K]
   void tn(int64_t M, int64_t N, int64_t K, const float *dy, const float *x, float *out) const {
     gemm_launch(int32_t(N), int32_t(K), int32_t(M), 1.f, dy, 1, N, x, K, 1, 0.f, out, K, s.gemm_ws, s.gemm_bytes,
-                Epi{}, st);
+                with(Epi{}), st);
   }
 };
 
@@ -1492,6 +1580,7 @@ cg_attn_train attn_args(const TrainDims &t, const int64_t *seq_start, const int3
   a.ldq = a.ldk = a.ldv = t.QKV;
   a.o = o;
   a.lse = lse;
+  a.round_bf16 = t.bf ? 1 : 0;
   return a;
 }
 
@@ -1526,7 +1615,7 @@ int cg_trunk_train_forward(const cg_train_config *c, const cg_train_block *block
     const TrainDims t = dims_of(*c, n);
     hipStream_t st = as_stream(stream);
     const Scratch s = scratch_of(t, scratch);
-    const Gemm gm{s, st};
+    const Gemm gm{s, st, t.bf};
     const SavedTail tail = saved_tail(t, saved);
     ok(cg_seq_of(seq_start, n_seqs, tail.seq_of, st));
     CG_HIP(hipMemcpyAsync(saved_layer(t, saved, 0).xl, x, size_t(t.n * t.d) * 4, hipMemcpyDeviceToDevice, st));
@@ -1537,8 +1626,16 @@ int cg_trunk_train_forward(const cg_train_config *c, const cg_train_block *block
       ok(cg_layernorm_fwd(a.xl, w.ln_attn_w, w.ln_attn_b, c->eps, a.h1, a.m1, a.r1, int32_t(t.n), int32_t(t.d), st));
       gm.nt(t.n, t.QKV, t.d, a.h1, w.qkv_w, a.qkv);
       const int32_t vi = c->value_index ? c->value_index[l] : -1;
-      if (vi >= 0)
-        ok(cg_add_strided(int32_t(t.n), int32_t(t.KVW), 1.f, values + vi * t.KVW, t.V, a.qkv + t.Q + t.KVW, t.QKV, st));
+      if (vi >= 0) {
+        if (t.bf) {  // v = bf16(v + value embedding): the attention reads bf16 v
+          add_round_kernel<<<grid_1d(t.n * t.KVW), 256, 0, st>>>(int32_t(t.n), int32_t(t.KVW), values + vi * t.KVW,
+                                                                 t.V, a.qkv + t.Q + t.KVW, t.QKV);
+          CG_LAUNCHED();
+        } else {
+          ok(cg_add_strided(int32_t(t.n), int32_t(t.KVW), 1.f, values + vi * t.KVW, t.V, a.qkv + t.Q + t.KVW, t.QKV,
+                            st));
+        }
+      }
       const cg_attn_train at = attn_args(t, seq_start, tail.seq_of, a.qkv, a.o, a.lse);
       ok(cg_attn_train_fwd(&at, st));
       Epi res;  // x1 = xl + o W_out^T
@@ -1578,7 +1675,7 @@ int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *bloc
     const TrainDims t = dims_of(*c, n);
     hipStream_t st = as_stream(stream);
     const Scratch s = scratch_of(t, scratch);
-    const Gemm gm{s, st};
+    const Gemm gm{s, st, t.bf};
     const SavedTail tail = saved_tail(t, saved);
     const int32_t N = int32_t(t.n);
     ok(cg_norm_bwd(tail.x_last, dhidden, final_w, tail.mf, tail.rf, s.dx, nullptr, grads->final_dw,
@@ -1594,13 +1691,13 @@ int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *bloc
           ok(cg_add_strided(N, int32_t(width), scale, s.dx + off, t.d, dple + l * t.pd, t.P, st));
         });
       gm.tn(t.n, t.d, t.F, s.dx, a.g, gw.down_w);
-      ok(cg_column_sum(s.dx, N, int32_t(t.d), t.d, gw.down_b, 0, s.red, s.red_bytes, st));
+      column_sum_launch(s.dx, N, int32_t(t.d), t.d, gw.down_b, 0, s.red, s.red_bytes, t.bf, st);
       Epi dgelu;  // du = (dx W_down) gelu'(u)
       dgelu.aux_in = a.u;
       dgelu.mode = EPI_GELU_GRAD;
       gm.nn(t.n, t.d, t.F, s.dx, w.down_w, s.du, dgelu);
       gm.tn(t.n, t.F, t.d, s.du, a.h2, gw.up_w);
-      ok(cg_column_sum(s.du, N, int32_t(t.F), t.F, gw.up_b, 0, s.red, s.red_bytes, st));
+      column_sum_launch(s.du, N, int32_t(t.F), t.F, gw.up_b, 0, s.red, s.red_bytes, t.bf, st);
       gm.nn(t.n, t.F, t.d, s.du, w.up_w, s.dh);
       ok(cg_norm_bwd(a.x1, s.dh, w.ln_mlp_w, a.m2, a.r2, s.dx1, s.dx, gw.ln_mlp_w, gw.ln_mlp_b, N, int32_t(t.d),
                      s.red, s.red_bytes, 0, st));

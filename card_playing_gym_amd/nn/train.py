@@ -1,5 +1,5 @@
-"""Training side of the trunk on the HIP path (fp32): autograd functions whose forward and
-backward run the kernels of csrc/train.hip.
+"""Training side of the trunk on the HIP path (fp32, or bf16 autocast): autograd functions
+whose forward and backward run the kernels of csrc/train.hip.
 
 What autograd records in the reference (cardgym/nn/trunk.py:104-181, 285-374) is, per
 block, LayerNorm -> fused QKV projection (+ value embedding) -> causal GQA attention
@@ -11,6 +11,14 @@ cardgym/nn/packing.py lays them out; a padded [B, T, d] batch is B sequences of 
 the activations the backward needs, and its backward produces the gradients of the
 input, of the per-layer and value lookups and of every trunk parameter.
 ``RMSNormFunction`` and ``PleContextFunction`` cover ``Trunk.condition``.
+
+Precision follows the caller's autocast as the reference's does (cardgym/core/devices.py:32-43,
+cardgym/rl/trainer.py): outside autocast everything is fp32; under bf16 autocast every
+projection takes bf16-rounded operands and returns a bf16-rounded product (fp32 accumulation),
+the attention returns bf16 outputs and gradients, the value embedding is added to v in fp32 and
+rounded once, and the residual stream, LayerNorm / RMSNorm and their statistics stay fp32
+(metal_trunk.py's statement of the same policy: cardgym/nn/metal_trunk.py:32-35).  Values are
+kept in fp32 storage holding bf16 numbers; the products run on bf16 MFMA.
 
 Only the elementwise bookkeeping (allocation, zero fills, copies) uses torch; every
 reduction, product, norm and attention is a HIP kernel.
@@ -35,35 +43,37 @@ def _ptr(t: torch.Tensor, offset: int = 0) -> int:
     return t.data_ptr() + 4 * offset
 
 
-def _gemm(m, n, k, alpha, a, sam, sak, b, sbk, sbn, beta, out, device) -> None:
+def _gemm(m, n, k, alpha, a, sam, sak, b, sbk, sbn, beta, out, device, bf16=False) -> None:
     size = nat.lib().cg_gemm_workspace_size(m, n, k)
     ws = torch.empty(max(size // 4, 1), device=device) if size else None
     nat.call("cg_gemm_strided", m, n, k, float(alpha), a, sam, sak, b, sbk, sbn, float(beta), out.data_ptr(),
-             out.stride(0), None if ws is None else ws.data_ptr(), size, stream_handle(device))
+             out.stride(0), nat.CG_BF16 if bf16 else nat.CG_F32, None if ws is None else ws.data_ptr(), size,
+             stream_handle(device))
 
 
-def linear_nt(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0) -> None:
-    """out[M, N] = alpha * x[M, K] @ w[N, K]^T + beta * out (contiguous rows)."""
+def linear_nt(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0, bf16=False) -> None:
+    """out[M, N] = alpha * x[M, K] @ w[N, K]^T + beta * out (contiguous rows); with ``bf16``
+    the operands and alpha * product are rounded to bf16 (autocast)."""
 
     m, k = x.shape
     n = w.shape[0]
-    _gemm(m, n, k, alpha, x.data_ptr(), k, 1, w.data_ptr(), 1, k, beta, out, x.device)
+    _gemm(m, n, k, alpha, x.data_ptr(), k, 1, w.data_ptr(), 1, k, beta, out, x.device, bf16)
 
 
-def matmul_nn(dy: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0) -> None:
+def matmul_nn(dy: torch.Tensor, w: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0, bf16=False) -> None:
     """out[M, K] = alpha * dy[M, N] @ w[N, K] + beta * out."""
 
     m, n = dy.shape
     k = w.shape[1]
-    _gemm(m, k, n, alpha, dy.data_ptr(), dy.stride(0), 1, w.data_ptr(), k, 1, beta, out, dy.device)
+    _gemm(m, k, n, alpha, dy.data_ptr(), dy.stride(0), 1, w.data_ptr(), k, 1, beta, out, dy.device, bf16)
 
 
-def matmul_tn(dy: torch.Tensor, x: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0) -> None:
+def matmul_tn(dy: torch.Tensor, x: torch.Tensor, out: torch.Tensor, alpha=1.0, beta=0.0, bf16=False) -> None:
     """out[N, K] = alpha * dy[M, N]^T @ x[M, K] + beta * out (weight gradients)."""
 
     m, n = dy.shape
     k = x.shape[1]
-    _gemm(n, k, m, alpha, dy.data_ptr(), 1, dy.stride(0), x.data_ptr(), x.stride(0), 1, beta, out, dy.device)
+    _gemm(n, k, m, alpha, dy.data_ptr(), 1, dy.stride(0), x.data_ptr(), x.stride(0), 1, beta, out, dy.device, bf16)
 
 
 def add_(dst: torch.Tensor, src: torch.Tensor, alpha=1.0, rows=None, cols=None, ld_src=None) -> None:
@@ -123,9 +133,15 @@ def gelu_bwd(u, dg):
     return du
 
 
-def _require_fp32(device: torch.device) -> None:
-    if torch.is_autocast_enabled(device.type):
-        raise RuntimeError("the HIP training path runs in fp32: leave autocast off for the update")
+def train_precision(device: torch.device) -> bool:
+    """Whether the update runs at bf16 autocast's rounding points (True) or in fp32 (False);
+    fp16 autocast is refused (the reference scales fp16 losses, cardgym/rl/trainer.py:409)."""
+
+    if not torch.is_autocast_enabled(device.type):
+        return False
+    if torch.get_autocast_dtype(device.type) != torch.bfloat16:
+        raise RuntimeError("the HIP training path runs in fp32 or under bf16 autocast, not fp16")
+    return True
 
 
 # ---- conditioning ---------------------------------------------------------------------------
@@ -155,17 +171,26 @@ class RMSNormFunction(torch.autograd.Function):
 
 
 class PleContextFunction(torch.autograd.Function):
-    """ple = (lookup + x @ W^T) / sqrt(2) (trunk.py:301-306)."""
+    """ple = (lookup + x @ W^T) / sqrt(2) (trunk.py:301-306); under bf16 autocast the product
+    is a bf16 projection of bf16-rounded operands, added to the fp32 lookup."""
 
     @staticmethod
-    def forward(ctx, lookup, x, w):
+    def forward(ctx, lookup, x, w, bf16=False):
         flat = x.reshape(-1, x.shape[-1]).float().contiguous()
         look = lookup.reshape(flat.shape[0], -1).float().contiguous()
         s = 1.0 / math.sqrt(2.0)
-        out = look.clone()
-        linear_nt(flat, w, out, alpha=s, beta=s)
+        if bf16:
+            proj = torch.empty_like(look)
+            linear_nt(flat, w, proj, bf16=True)
+            out = torch.zeros_like(look)
+            add_(out, look, alpha=s)
+            add_(out, proj, alpha=s)
+        else:
+            out = look.clone()
+            linear_nt(flat, w, out, alpha=s, beta=s)
         ctx.save_for_backward(flat, w)
         ctx.shapes = (lookup.shape, x.shape)
+        ctx.bf16 = bf16
         return out
 
     @staticmethod
@@ -176,10 +201,14 @@ class PleContextFunction(torch.autograd.Function):
         dlookup = torch.zeros_like(dple)
         add_(dlookup, dple, alpha=s)
         dx = torch.empty_like(flat)
-        matmul_nn(dple, w, dx, alpha=s)
         dw = torch.empty_like(w)
-        matmul_tn(dple, flat, dw, alpha=s)
-        return dlookup.view(ctx.shapes[0]), dx.view(ctx.shapes[1]), dw
+        if ctx.bf16:  # the projection's gradient s * dple enters both products rounded to bf16
+            matmul_nn(dlookup, w, dx, bf16=True)
+            matmul_tn(dlookup, flat, dw, bf16=True)
+        else:
+            matmul_nn(dple, w, dx, alpha=s)
+            matmul_tn(dple, flat, dw, alpha=s)
+        return dlookup.view(ctx.shapes[0]), dx.view(ctx.shapes[1]), dw, None
 
 
 # ---- the blocks ------------------------------------------------------------------------------
@@ -196,14 +225,14 @@ def block_params(trunk) -> list[torch.Tensor]:
 class _Native:
     """ctypes views of a trunk's configuration and parameters for the training entry points."""
 
-    def __init__(self, trunk, params: list[torch.Tensor]) -> None:
+    def __init__(self, trunk, params: list[torch.Tensor], bf16: bool) -> None:
         c = trunk.config
         self.value_index = (ctypes.c_int32 * max(c.n_layers, 1))(
             *[trunk._value_index.get(layer, -1) for layer in range(c.n_layers)]
         )
         eps = trunk.blocks[0].ln_attn.eps if len(trunk.blocks) else 1e-5
         self.config = nat.TrainConfig(c.d_model, c.n_layers, c.n_heads, c.n_kv_heads, c.d_ff, c.per_layer_dim,
-                                      c.ple_width, c.value_width, eps, self.value_index)
+                                      c.ple_width, c.value_width, eps, self.value_index, 1 if bf16 else 0)
         self.blocks = (nat.TrainBlock * max(c.n_layers, 1))()
         for layer in range(c.n_layers):
             self.blocks[layer] = nat.TrainBlock(*(t.data_ptr() for t in params[10 * layer : 10 * layer + 10]))
@@ -214,11 +243,11 @@ class TrunkFunction(torch.autograd.Function):
     cg_trunk_train_forward / cg_trunk_train_backward."""
 
     @staticmethod
-    def forward(ctx, trunk, seq_start, x, ple, values, *params):
+    def forward(ctx, trunk, bf16, seq_start, x, ple, values, *params):
         c = trunk.config
         device = x.device
         n = x.shape[0]
-        native = _Native(trunk, list(params))
+        native = _Native(trunk, list(params), bf16)
         saved_size = nat.lib().cg_train_saved_size(ctypes.byref(native.config), n)
         scratch_size = nat.lib().cg_train_scratch_size(ctypes.byref(native.config), n)
         saved = torch.empty(saved_size, dtype=torch.uint8, device=device)
@@ -232,6 +261,7 @@ class TrunkFunction(torch.autograd.Function):
             hidden.data_ptr(), saved.data_ptr(), saved_size, scratch.data_ptr(), scratch_size, _s(x),
         )
         ctx.trunk = trunk
+        ctx.bf16 = bf16
         ctx.has_ple, ctx.has_values = ple is not None, values is not None
         ctx.save_for_backward(seq_start, saved, *params)
         return hidden
@@ -243,7 +273,7 @@ class TrunkFunction(torch.autograd.Function):
         seq_start, saved, *params = ctx.saved_tensors
         device = dh.device
         n = dh.shape[0]
-        native = _Native(trunk, params)
+        native = _Native(trunk, params, ctx.bf16)
         grads = [torch.empty_like(p) for p in params]
         L = c.n_layers
         block_grads = (nat.TrainBlockGrads * max(L, 1))()
@@ -261,14 +291,14 @@ class TrunkFunction(torch.autograd.Function):
             scratch.data_ptr(), scratch_size, ctypes.byref(tg), dx.data_ptr(),
             None if dple is None else dple.data_ptr(), None if dvalues is None else dvalues.data_ptr(), _s(dh),
         )
-        return (None, None, dx, dple, dvalues, *grads)
+        return (None, None, None, dx, dple, dvalues, *grads)
 
 
 def trunk_train_forward(trunk, x, ple, values, bounds=None):
     """Trunk.forward under autograd: [B, T, d] (or packed rows [N, d] with ``bounds``) ->
     final-norm hidden states of the same leading shape, differentiable."""
 
-    _require_fp32(x.device)
+    bf16 = train_precision(x.device)
     c = trunk.config
     if bounds is None:
         batch, length = x.shape[0], x.shape[1]
@@ -282,6 +312,6 @@ def trunk_train_forward(trunk, x, ple, values, bounds=None):
     n = flat.shape[0]
     ple_flat = None if ple is None else ple.reshape(n, -1).float().contiguous()
     values_flat = None if values is None else values.reshape(n, -1).float().contiguous()
-    hidden = TrunkFunction.apply(trunk, seq_start, flat.float().contiguous(), ple_flat, values_flat,
+    hidden = TrunkFunction.apply(trunk, bf16, seq_start, flat.float().contiguous(), ple_flat, values_flat,
                                  *block_params(trunk))
     return hidden.view(*lead, c.d_model)

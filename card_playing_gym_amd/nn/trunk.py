@@ -320,9 +320,9 @@ class Trunk(nn.Module):
         return any(t is not None and t.requires_grad for t in inputs) or any(p.requires_grad for p in self.parameters())
 
     def _condition_train(self, x, ple_lookup, value_lookup):
-        from .train import PleContextFunction, RMSNormFunction, _require_fp32
+        from .train import PleContextFunction, RMSNormFunction, train_precision
 
-        _require_fp32(x.device)
+        bf16 = train_precision(x.device)
         if self.input_norm is not None:
             x = RMSNormFunction.apply(x, self.input_norm.weight, self.input_norm.eps)
         else:
@@ -332,7 +332,7 @@ class Trunk(nn.Module):
         if self.ple_context is not None:
             if ple_lookup is None:
                 raise ValueError("This trunk expects a per-layer embedding lookup.")
-            ple = PleContextFunction.apply(ple_lookup, x, self.ple_context.weight).view(
+            ple = PleContextFunction.apply(ple_lookup, x, self.ple_context.weight, bf16).view(
                 *lead, self.config.n_layers, self.config.per_layer_dim
             )
         values = None

@@ -341,17 +341,20 @@ int cg_piquet_destroy(cg_piquet *embedder);
 int cg_piquet_embed(const cg_piquet *embedder, const int64_t *tokens, int64_t ld_tokens, int32_t n, void *x,
                     void *ple, void *values, float *cards, int32_t *flag, void *stream);
 
-/* ---- training side (fp32): a packed-row trunk forward that keeps what its backward needs,
+/* ---- training side (fp32, or bf16 autocast): a packed-row trunk forward that keeps what its
+ * backward needs,
  * and that backward (cardgym/nn/trunk.py:124-181, 285-374 under autograd; packed rows as in
  * cardgym/nn/packing.py:36-40).  The composition (which buffers each layer keeps, the order
  * of the backward) is card_playing_gym_amd/nn/train.py; these are its kernels. ---------- */
 
 /* C = alpha op(A) op(B) + beta C with A(i, k) = a[i * sam + k * sak] and B(k, j) =
- * b[k * sbk + j * sbn]: every projection's forward, input gradient and weight gradient. */
+ * b[k * sbk + j * sbn]: every projection's forward, input gradient and weight gradient.
+ * compute_dtype CG_F32, or CG_BF16 as under autocast: A and B rounded to bf16, fp32
+ * accumulation, alpha op(A) op(B) rounded to bf16 before beta C is added. */
 size_t cg_gemm_workspace_size(int32_t m, int32_t n, int32_t k); /* split-K partials, 0 if none */
 int cg_gemm_strided(int32_t m, int32_t n, int32_t k, float alpha, const float *a, int64_t sam, int64_t sak,
-                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc, void *workspace,
-                    size_t workspace_size, void *stream);
+                    const float *b, int64_t sbk, int64_t sbn, float beta, float *c, int64_t ldc,
+                    int32_t compute_dtype, void *workspace, size_t workspace_size, void *stream);
 
 /* nn.LayerNorm forward keeping (mean, rstd) per row. */
 int cg_layernorm_fwd(const float *x, const float *w, const float *b, float eps, float *y, float *mean, float *rstd,
@@ -399,6 +402,7 @@ typedef struct {
   int64_t ldq, ldk, ldv;
   float *o;
   float *lse;
+  int32_t round_bf16; /* 1: o (forward) and dq / dk / dv (backward) rounded to bf16 */
 } cg_attn_train;
 int cg_attn_train_fwd(const cg_attn_train *p, void *stream);
 int cg_attn_train_bwd(const cg_attn_train *p, const float *dout, float *dsum, float *dq, float *dk, float *dv,
@@ -414,6 +418,7 @@ typedef struct {
   int32_t d_model, n_layers, n_heads, n_kv_heads, d_ff, per_layer_dim, ple_width, value_width;
   float eps;
   const int32_t *value_index; /* host [n_layers]: the layer's slot in the value lookup, -1 none */
+  int32_t bf16;               /* 1: bf16 autocast rounding points (GEMM operands and outputs, attention) */
 } cg_train_config;
 
 typedef struct { /* DecoderBlock parameters (trunk.py:124-139), fp32 */
