@@ -181,6 +181,40 @@ __device__ __forceinline__ void store_tile(float *lds, const TileRegs<ROWS> &t, 
   }
 }
 
+// bf16 operands: the same tile converted once as it is written to LDS, [row][16 k] bf16 at a
+// 40-byte row pitch (16-lane groups of 8-byte fragment reads hit distinct banks).
+constexpr int GT_LDKB = GT_K + 4;  // row pitch in bf16 elements
+
+template <int MODE, int ROWS>
+__device__ __forceinline__ void store_tile_bf16(unsigned short *lds, const TileRegs<ROWS> &t, int tid, int rows_left,
+                                                int k_left) {
+#pragma unroll
+  for (int e = 0; e < ROWS / 64; ++e) {
+    const int idx = tid + e * 256;
+    const float4 v = t.v[e];
+    if constexpr (MODE == 2) {
+      const int k = idx & 15, r = (idx >> 4) * 4;
+      const bool ok = k < k_left && r < rows_left;
+      const unsigned lo = pack_bf16(ok ? v.x : 0.f, ok ? v.y : 0.f), hi = pack_bf16(ok ? v.z : 0.f, ok ? v.w : 0.f);
+      lds[(r + 0) * GT_LDKB + k] = static_cast<unsigned short>(lo);
+      lds[(r + 1) * GT_LDKB + k] = static_cast<unsigned short>(lo >> 16);
+      lds[(r + 2) * GT_LDKB + k] = static_cast<unsigned short>(hi);
+      lds[(r + 3) * GT_LDKB + k] = static_cast<unsigned short>(hi >> 16);
+    } else {
+      const int r = idx >> 2, k = (idx & 3) * 4;
+      const bool row = r < rows_left;
+      float4 o;
+      if constexpr (MODE == 1) {
+        o = (row && k < k_left) ? v : float4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        o = float4{row && k < k_left ? v.x : 0.f, row && k + 1 < k_left ? v.y : 0.f, row && k + 2 < k_left ? v.z : 0.f,
+                   row && k + 3 < k_left ? v.w : 0.f};
+      }
+      *reinterpret_cast<u32x2 *>(lds + r * GT_LDKB + k) = u32x2{pack_bf16(o.x, o.y), pack_bf16(o.z, o.w)};
+    }
+  }
+}
+
 template <int AM, int BM, int TM, bool BF>
 __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t N, int32_t K, int32_t kc, float alpha,
                                                            const float *__restrict__ A, int64_t sam, int64_t sak,
@@ -188,8 +222,12 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
                                                            float beta, float *__restrict__ C, int64_t ldc,
                                                            float *__restrict__ part, const Epi epi) {
   constexpr int FM = TM / 32;  // 16-row MFMA blocks per wave: a wave takes TM / 2 rows x 64 columns
-  __shared__ __align__(16) float as[2][TM * GT_LDK];
-  __shared__ __align__(16) float bs[2][GT_N * GT_LDK];
+  // fp32 tiles [row][GT_LDK floats]; bf16 tiles [row][GT_LDKB halves] (half the storage)
+  constexpr int PITCH = BF ? GT_LDKB / 2 : GT_LDK;  // row pitch in 4-byte words
+  __shared__ __align__(16) float as[2][TM * PITCH];
+  __shared__ __align__(16) float bs[2][GT_N * PITCH];
+  auto as16 = [&](int b) { return reinterpret_cast<unsigned short *>(as[b]); };
+  auto bs16 = [&](int b) { return reinterpret_cast<unsigned short *>(bs[b]); };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 15, lg = lane >> 4;
@@ -213,10 +251,15 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
   int buf = 0;
   const int ma = M - m0, nb_ = N - n0;
   if (kbeg < kend) {
-    store_tile<AM, TM>(as[0], load_tile<AM, TM>(a0 + int64_t(kbeg) * sak, sam, sak, ma, kend - kbeg, tid), tid, ma,
-                       kend - kbeg);
-    store_tile<BM, GT_N>(bs[0], load_tile<BM, GT_N>(b0 + int64_t(kbeg) * sbk, sbn, sbk, nb_, kend - kbeg, tid), tid,
-                         nb_, kend - kbeg);
+    const auto ta0 = load_tile<AM, TM>(a0 + int64_t(kbeg) * sak, sam, sak, ma, kend - kbeg, tid);
+    const auto tb0 = load_tile<BM, GT_N>(b0 + int64_t(kbeg) * sbk, sbn, sbk, nb_, kend - kbeg, tid);
+    if constexpr (BF) {
+      store_tile_bf16<AM, TM>(as16(0), ta0, tid, ma, kend - kbeg);
+      store_tile_bf16<BM, GT_N>(bs16(0), tb0, tid, nb_, kend - kbeg);
+    } else {
+      store_tile<AM, TM>(as[0], ta0, tid, ma, kend - kbeg);
+      store_tile<BM, GT_N>(bs[0], tb0, tid, nb_, kend - kbeg);
+    }
   }
   __syncthreads();
   for (int k0 = kbeg; k0 < kend; k0 += GT_K) {
@@ -229,21 +272,23 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
       nb = load_tile<BM, GT_N>(b0 + int64_t(k0 + GT_K) * sbk, sbn, sbk, nb_, kl, tid);
     }
     const float *ta = as[buf], *tb = bs[buf];
-    f32x4 bf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const f32x4 *>(tb + (wn * 64 + j * 16 + li) * GT_LDK + 4 * lg);
     if constexpr (BF) {  // bf16 operands: the stage's 16 k in one v_mfma_f32_16x16x16_bf16 per tile,
                          // lane group lg holding k = 4 lg .. 4 lg + 3 as the fp32 path does
+      const unsigned short *ta16 = as16(buf), *tb16 = bs16(buf);
       s16x4 bb[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bb[j] = bf16x4_of(bf[j]);
+      for (int j = 0; j < 4; ++j)
+        bb[j] = *reinterpret_cast<const s16x4 *>(tb16 + (wn * 64 + j * 16 + li) * GT_LDKB + 4 * lg);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
-        const s16x4 ab = bf16x4_of(*reinterpret_cast<const f32x4 *>(ta + (wm * (TM / 2) + i * 16 + li) * GT_LDK + 4 * lg));
+        const s16x4 ab = *reinterpret_cast<const s16x4 *>(ta16 + (wm * (TM / 2) + i * 16 + li) * GT_LDKB + 4 * lg);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ab, bb[j], acc[i][j], 0, 0, 0);
       }
     } else {
+      f32x4 bf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const f32x4 *>(tb + (wn * 64 + j * 16 + li) * GT_LDK + 4 * lg);
 #pragma unroll
       for (int i = 0; i < FM; ++i) {
         const f32x4 af = *reinterpret_cast<const f32x4 *>(ta + (wm * (TM / 2) + i * 16 + li) * GT_LDK + 4 * lg);
@@ -255,8 +300,13 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
       }
     }
     if (more) {
-      store_tile<AM, TM>(as[buf ^ 1], na, tid, ma, kl);
-      store_tile<BM, GT_N>(bs[buf ^ 1], nb, tid, nb_, kl);
+      if constexpr (BF) {
+        store_tile_bf16<AM, TM>(as16(buf ^ 1), na, tid, ma, kl);
+        store_tile_bf16<BM, GT_N>(bs16(buf ^ 1), nb, tid, nb_, kl);
+      } else {
+        store_tile<AM, TM>(as[buf ^ 1], na, tid, ma, kl);
+        store_tile<BM, GT_N>(bs[buf ^ 1], nb, tid, nb_, kl);
+      }
     }
     __syncthreads();
     buf ^= 1;
