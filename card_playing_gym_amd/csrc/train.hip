@@ -360,14 +360,31 @@ __global__ __launch_bounds__(256, 3) void gemm_strided_kernel(int32_t M, int32_t
   }
 }
 
-// C[m, n] = epilogue(alpha * sum_z part[z][m, n]).
+// C[m, n] = epilogue(alpha * sum_z part[z][m, n]).  A thread takes four consecutive entries
+// (float4 loads when N is a multiple of 4) and keeps four slices in flight.
 __global__ void gemm_reduce_kernel(int32_t M, int32_t N, int32_t slices, float alpha, const float *__restrict__ part,
                                    float beta, float *__restrict__ C, int64_t ldc, const Epi epi) {
-  const int64_t total = int64_t(M) * N;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-    float s = 0.f;
-    for (int z = 0; z < slices; ++z) s += part[int64_t(z) * total + i];
-    epilogue(epi, alpha * s, beta, C, ldc, i / N, i % N);
+  const int64_t total = int64_t(M) * N, quads = (total + 3) / 4;
+  const bool vec = (N & 3) == 0;
+  for (int64_t q = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; q < quads; q += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i0 = 4 * q;
+    f32x4 s[4] = {};
+    if (vec) {
+      int z = 0;
+      for (; z + 3 < slices; z += 4)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s[u] += *reinterpret_cast<const f32x4 *>(part + int64_t(z + u) * total + i0);
+      for (; z < slices; ++z) s[0] += *reinterpret_cast<const f32x4 *>(part + int64_t(z) * total + i0);
+    } else {
+      for (int z = 0; z < slices; ++z)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (i0 + e < total) s[0][e] += part[int64_t(z) * total + i0 + e];
+    }
+    const f32x4 t = (s[0] + s[1]) + (s[2] + s[3]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (i0 + e < total) epilogue(epi, alpha * t[e], beta, C, ldc, (i0 + e) / N, (i0 + e) % N);
   }
 }
 
@@ -1193,7 +1210,8 @@ void gemm_launch(int32_t m, int32_t n, int32_t k, float alpha, const float *a, i
 #undef CG_GEMM_CASE
   CG_LAUNCHED();
   if (part) {
-    gemm_reduce_kernel<<<grid_1d(int64_t(m) * n), 256, 0, s>>>(m, n, pl.slices, alpha, part, beta, c, ldc, epi);
+    gemm_reduce_kernel<<<grid_1d((int64_t(m) * n + 3) / 4), 256, 0, s>>>(m, n, pl.slices, alpha, part, beta, c, ldc,
+                                                                        epi);
     CG_LAUNCHED();
   }
 }

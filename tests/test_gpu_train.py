@@ -35,9 +35,11 @@ def close(got, want, tol=1e-4, what=""):
     assert err <= tol * scale, (what, err, scale)
 
 
-def test_gemm_layouts(device):
+@pytest.mark.parametrize("size", [(70, 45, 133), (96, 45, 2048), (200, 136, 1040)],
+                         ids=["generic", "split-k-odd-n", "split-k"])
+def test_gemm_layouts(device, size):
     g = torch.Generator().manual_seed(1)
-    m, n, k = 70, 45, 133
+    m, n, k = size
     x = torch.randn(m, k, generator=g)
     w = torch.randn(n, k, generator=g)
     dy = torch.randn(m, n, generator=g)
