@@ -435,6 +435,64 @@ __global__ void layernorm_fwd_kernel(const float *__restrict__ x, const float *_
   }
 }
 
+// The same for d <= 256 NV, d a multiple of 4, 16-byte aligned rows: lane l owns the float4
+// columns 4 l + 256 v of a row (two-pass mean and variance from registers), wave w takes rows
+// r0 + w, r0 + w + 4, ... of its block's 16, loading the next row while it reduces this one.
+template <int NV>
+__global__ __launch_bounds__(256) void layernorm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                             const float *__restrict__ b, float eps,
+                                                             float *__restrict__ y, float *__restrict__ mean,
+                                                             float *__restrict__ rstd, int32_t n, int32_t d) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r0 = blockIdx.x * 16, r1 = min(n, r0 + 16);
+  const float4 zero = {0.f, 0.f, 0.f, 0.f};
+  float4 wv[NV], bv[NV], xa[NV];
+  bool in[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int c = 4 * lane + 256 * v;
+    in[v] = c < d;
+    wv[v] = in[v] ? *reinterpret_cast<const float4 *>(w + c) : zero;
+    bv[v] = in[v] ? *reinterpret_cast<const float4 *>(b + c) : zero;
+  }
+  auto load = [&](int row, float4 (&xs)[NV]) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      xs[v] = in[v] ? *reinterpret_cast<const float4 *>(x + int64_t(row) * d + 4 * lane + 256 * v) : zero;
+  };
+  int row = r0 + wave;
+  if (row < r1) load(row, xa);
+  for (; row < r1; row += 4) {
+    float4 xc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) xc[v] = xa[v];
+    if (row + 4 < r1) load(row + 4, xa);
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) s += (xc[v].x + xc[v].y) + (xc[v].z + xc[v].w);
+    const float mu = wave_sum(s) / float(d);
+    float q = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (!in[v]) continue;
+      const float a0 = xc[v].x - mu, a1 = xc[v].y - mu, a2 = xc[v].z - mu, a3 = xc[v].w - mu;
+      q += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+    }
+    const float r = 1.0f / sqrtf(wave_sum(q) / float(d) + eps);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (!in[v]) continue;
+      *reinterpret_cast<float4 *>(y + int64_t(row) * d + 4 * lane + 256 * v) =
+          float4{(xc[v].x - mu) * r * wv[v].x + bv[v].x, (xc[v].y - mu) * r * wv[v].y + bv[v].y,
+                 (xc[v].z - mu) * r * wv[v].z + bv[v].z, (xc[v].w - mu) * r * wv[v].w + bv[v].w};
+    }
+    if (lane == 0) {
+      mean[row] = mu;
+      rstd[row] = r;
+    }
+  }
+}
+
 // dx = rstd (g - mean(g) - xhat mean(g xhat)) (+ residual), g = dy * w; per block of
 // `rows_per_block` rows, partial dw = sum dy xhat and db = sum dy into part[blockIdx][0 / 1][d].
 // A NULL mean selects RMSNorm (no centring, no bias).  Any d (norm_bwd_rows_kernel takes the
@@ -1303,7 +1361,22 @@ int cg_layernorm_fwd(const float *x, const float *w, const float *b, float eps, 
   return guarded([&] {
     if (n == 0) return;
     CG_REQUIRE(x && w && b && y && mean && rstd && d > 0, CG_ERR_INVALID, "LayerNorm operands are required");
-    layernorm_fwd_kernel<<<blocks_of(n, 4), 256, 0, as_stream(stream)>>>(x, w, b, eps, y, mean, rstd, n, d);
+    hipStream_t s = as_stream(stream);
+    if (d % 4 == 0 && d <= 1024 && aligned16(x) && aligned16(w) && aligned16(b) && aligned16(y)) {
+      switch ((d + 255) / 256) {
+#define CG_LN_CASE(NV)                                                                                        \
+  case NV:                                                                                                    \
+    layernorm_rows_kernel<NV><<<blocks_of(n, 16), 256, 0, s>>>(x, w, b, eps, y, mean, rstd, n, d); \
+    break;
+        CG_LN_CASE(1)
+        CG_LN_CASE(2)
+        CG_LN_CASE(3)
+        CG_LN_CASE(4)
+#undef CG_LN_CASE
+      }
+    } else {
+      layernorm_fwd_kernel<<<blocks_of(n, 4), 256, 0, s>>>(x, w, b, eps, y, mean, rstd, n, d);
+    }
     CG_LAUNCHED();
   });
 }
