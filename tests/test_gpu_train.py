@@ -112,7 +112,7 @@ def packed_attention_reference(q, k, v, lengths, G):
     return torch.cat(outs)
 
 
-@pytest.mark.parametrize("D,H,KVH", [(32, 8, 2), (64, 4, 4), (16, 6, 3)])
+@pytest.mark.parametrize("D,H,KVH", [(32, 8, 2), (64, 4, 4), (16, 6, 3), (8, 4, 2), (24, 8, 1)])
 def test_attention_forward_backward(device, D, H, KVH):
     g = torch.Generator().manual_seed(D + H)
     lengths = [1, 7, 70, 130, 3]
