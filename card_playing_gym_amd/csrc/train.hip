@@ -744,7 +744,9 @@ struct AttnDims {
   static constexpr int LD = DT * 16 + 4;                // LDS row, floats; d in [D, 16 DT) hold 0
   static constexpr int C4 = D / 4;                      // float4 per row
   static constexpr int PER_KV = (2 * KT * C4 + 255) / 256;  // float4 per thread, one K + V tile
-  static constexpr int PER_Q = (2 * 32 * C4 + 255) / 256;   // float4 per thread, one 32-row Q + dO unit
+  static constexpr int QR = D <= 32 ? 64 : 32;             // query tokens per dK / dV unit (VGPRs bound it at 64)
+  static constexpr int QH = QR / 16;                        // its 16-query sub-tiles
+  static constexpr int PER_Q = (2 * QR * C4 + 255) / 256;   // float4 per thread, one Q + dO unit
 };
 
 template <int DC>
@@ -1023,8 +1025,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnTrain a) {
   if (lg == 0) a.dsum[row] = dsum;
 }
 
-// One staged query unit of the dK / dV kernel: QR = 32 tokens of one head (q scaled, dO, lse, D).
-constexpr int QR = 32;
+// One staged query unit of the dK / dV kernel: QR tokens of one head (q scaled, dO, lse, D).
 template <int D>
 struct QueryUnit {
   float4 v[AttnDims<D>::PER_Q];
@@ -1039,9 +1040,9 @@ __device__ __forceinline__ QueryUnit<D> unit_load(const AttnTrain &a, int h, int
   for (int e = 0; e < S::PER_Q; ++e) {
     const int i = threadIdx.x + 256 * e;
     float4 x = {0.f, 0.f, 0.f, 0.f};
-    if (i < 2 * QR * S::C4) {
-      const bool isg = i >= QR * S::C4;
-      const int ii = isg ? i - QR * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
+    if (i < 2 * S::QR * S::C4) {
+      const bool isg = i >= S::QR * S::C4;
+      const int ii = isg ? i - S::QR * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
       const int64_t t = t0 + row;
       if (t < a.n) {
         if (isg) {
@@ -1058,8 +1059,8 @@ __device__ __forceinline__ QueryUnit<D> unit_load(const AttnTrain &a, int h, int
     u.v[e] = x;
   }
   u.s = 0.f;
-  const int64_t t = t0 + (threadIdx.x % QR);
-  if (threadIdx.x < 2 * QR && t < a.n) u.s = threadIdx.x < QR ? a.lse[t * a.H + h] : a.dsum[t * a.H + h];
+  const int64_t t = t0 + (threadIdx.x % S::QR);
+  if (threadIdx.x < 2 * S::QR && t < a.n) u.s = threadIdx.x < S::QR ? a.lse[t * a.H + h] : a.dsum[t * a.H + h];
   return u;
 }
 
@@ -1069,13 +1070,13 @@ __device__ __forceinline__ void unit_store(float *qs, float *gs, float *ls, cons
 #pragma unroll
   for (int e = 0; e < S::PER_Q; ++e) {
     const int i = threadIdx.x + 256 * e;
-    if (i < 2 * QR * S::C4) {
-      const bool isg = i >= QR * S::C4;
-      const int ii = isg ? i - QR * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
+    if (i < 2 * S::QR * S::C4) {
+      const bool isg = i >= S::QR * S::C4;
+      const int ii = isg ? i - S::QR * S::C4 : i, row = ii / S::C4, c = (ii % S::C4) * 4;
       *reinterpret_cast<float4 *>((isg ? gs : qs) + row * S::LD + c) = u.v[e];
     }
   }
-  if (threadIdx.x < 2 * QR) ls[threadIdx.x] = u.s;  // [0, QR) lse, [QR, 2 QR) D
+  if (threadIdx.x < 2 * S::QR) ls[threadIdx.x] = u.s;  // [0, S::QR) lse, [S::QR, 2 S::QR) D
 }
 
 // dK / dV: a block holds 64 keys of KV head blockIdx.y, wave w keys j0 + 16 w + li in
@@ -1085,7 +1086,7 @@ __device__ __forceinline__ void unit_store(float *qs, float *gs, float *ls, cons
 template <int D>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
   using S = AttnDims<D>;
-  __shared__ __align__(16) float qs[2][QR * S::LD], gs[2][QR * S::LD], ls[2][2 * QR];
+  __shared__ __align__(16) float qs[2][S::QR * S::LD], gs[2][S::QR * S::LD], ls[2][2 * S::QR];
   const int G = a.H / a.KVH, hk = blockIdx.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const int64_t j0 = int64_t(blockIdx.x) * 64, jw = j0 + 16 * wave, j = jw + li;
@@ -1093,9 +1094,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
   const int64_t end = live ? a.seq_start[a.seq_of[j] + 1] : 0;
   const int64_t w_hi = wave_live ? a.seq_start[a.seq_of[min<int64_t>(a.n - 1, jw + 15)] + 1] : 0;
   const int64_t q_hi = a.seq_start[a.seq_of[min<int64_t>(a.n - 1, j0 + 63)] + 1];
-  const int units = int((q_hi - j0 + QR - 1) / QR) * G;
-  zero_pad<D>(qs[0], 2 * QR);
-  zero_pad<D>(gs[0], 2 * QR);
+  const int units = int((q_hi - j0 + S::QR - 1) / S::QR) * G;
+  zero_pad<D>(qs[0], 2 * S::QR);
+  zero_pad<D>(gs[0], 2 * S::QR);
   float kf[S::DC], vf[S::DC];
 #pragma unroll
   for (int kk = 0; kk < S::DC; ++kk) {
@@ -1115,17 +1116,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
   for (int u = 0; u < units; ++u) {
     const bool more = u + 1 < units;
     QueryUnit<D> next;
-    if (more) next = unit_load<D>(a, hk * G + (u + 1) % G, j0 + QR * ((u + 1) / G));
-    const int64_t t0 = j0 + QR * (u / G);
-    // The unit's two 16-query halves: independent S / dP chains, then the dV / dK updates.
-    bool act[2];
+    if (more) next = unit_load<D>(a, hk * G + (u + 1) % G, j0 + S::QR * ((u + 1) / G));
+    const int64_t t0 = j0 + S::QR * (u / G);
+    // The unit's 16-query sub-tiles: independent S / dP chains, then the dV / dK updates.
+    bool act[S::QH];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) act[hf] = wave_live && t0 + 16 * hf + 15 >= jw && t0 + 16 * hf < w_hi;
-    if (act[0] || act[1]) {
+    for (int hf = 0; hf < S::QH; ++hf) act[hf] = wave_live && t0 + 16 * hf + 15 >= jw && t0 + 16 * hf < w_hi;
+    bool any = false;
+#pragma unroll
+    for (int hf = 0; hf < S::QH; ++hf) any = any || act[hf];
+    if (any) {
       const float *Q = qs[buf], *GO = gs[buf], *L = ls[buf];
-      f32x4 sc[2], dp[2], p[2], ds[2];
+      f32x4 sc[S::QH], dp[S::QH], p[S::QH], ds[S::QH];
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
+      for (int hf = 0; hf < S::QH; ++hf) {
         sc[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
         dp[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (!act[hf]) continue;
@@ -1139,9 +1143,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
         }
       }
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
+      for (int hf = 0; hf < S::QH; ++hf) {
         const float4 lse4 = *reinterpret_cast<const float4 *>(L + 16 * hf + 4 * lg);
-        const float4 dsum4 = *reinterpret_cast<const float4 *>(L + QR + 16 * hf + 4 * lg);
+        const float4 dsum4 = *reinterpret_cast<const float4 *>(L + S::QR + 16 * hf + 4 * lg);
         const float lse[4] = {lse4.x, lse4.y, lse4.z, lse4.w}, dsm[4] = {dsum4.x, dsum4.y, dsum4.z, dsum4.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -1151,7 +1155,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
         }
       }
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
+      for (int hf = 0; hf < S::QH; ++hf) {
         if (!act[hf]) continue;
 #pragma unroll
         for (int dt = 0; dt < S::DT; ++dt)
