@@ -61,6 +61,11 @@ def parse() -> argparse.Namespace:
         "(for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes), then exit",
     )
     p.add_argument(
+        "--gemm-probe", action="store_true",
+        help="time the training step's fp32 GEMM shapes (ours beside torch.matmul, i.e. hipBLASLt) and exit "
+        "(for rocprofv3 --pmc passes over the GEMM kernels)",
+    )
+    p.add_argument(
         "--train-probe", action="store_true",
         help="run only the fp32 training step (our path, no reference) and print its timings, then exit "
         "(for a rocprofv3 kernel trace of the training kernels)",
@@ -495,6 +500,43 @@ def train_step_time(bench: Bench, with_reference: bool, warmup: int = 3, reps: i
     return out
 
 
+def gemm_probe(device: torch.device, reps: int = 20) -> list:
+    """The fp32 GEMMs of one training layer at 16384 tokens (d 256, d_ff 1024, QKV 384): the
+    token-major products x W^T and the weight gradients dY^T X, ours beside torch.matmul."""
+
+    from card_playing_gym_amd.nn import train as T
+
+    n, out = 16384, []
+
+    def run(fn) -> float:
+        for _ in range(3):
+            fn()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / reps * 1e3
+
+    g = torch.Generator(device=device).manual_seed(3)
+    for m, nn_, k in ((n, 1024, 256), (n, 256, 1024), (n, 256, 256), (n, 384, 256), (n, 256, 384)):
+        x = torch.randn((m, k), generator=g, device=device)
+        w = torch.randn((nn_, k), generator=g, device=device)
+        y = torch.empty((m, nn_), device=device)
+        ours, theirs = run(lambda: T.linear_nt(x, w, y)), run(lambda: torch.matmul(x, w.t(), out=y))
+        out.append({"op": "x W^T", "m": m, "n": nn_, "k": k, "us": round(ours, 1), "torch_us": round(theirs, 1),
+                    "tflops": round(2 * m * nn_ * k / ours / 1e6, 1)})
+    for rows, cols in ((1024, 256), (256, 1024), (256, 256), (384, 256)):
+        dy = torch.randn((n, rows), generator=g, device=device)
+        x = torch.randn((n, cols), generator=g, device=device)
+        y = torch.empty((rows, cols), device=device)
+        ours, theirs = run(lambda: T.matmul_tn(dy, x, y)), run(lambda: torch.matmul(dy.t(), x, out=y))
+        out.append({"op": "dY^T X", "m": rows, "n": cols, "k": n, "us": round(ours, 1), "torch_us": round(theirs, 1),
+                    "tflops": round(2 * rows * cols * n / ours / 1e6, 1)})
+    return out
+
+
 def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) -> dict:
     """The oracle's reference path on the host cores, on `games` of the workload's games, at
     steps first .. first + steps (the middle of the timed range: context lengths there are
@@ -619,6 +661,9 @@ def main() -> int:
         return 2
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f"bench: setting up {args.workload} ({args.warmup} warmup + {args.steps} timed steps)")
+    if args.gemm_probe:  # needs no workload state
+        print(json.dumps({"probe": "gemm", "shapes": gemm_probe(torch.device("cuda", 0))}), flush=True)
+        return 0
     bench = Bench(args.workload, args.steps, args.warmup)
     w = bench.workload
     if args.traffic_probe:

@@ -127,6 +127,11 @@ struct TileRegs {
   float4 v[ROWS / 64];
 };
 
+// Row of float4 slot idx in the k-contiguous layouts (MODE 1 and 0): four 4-k blocks of 16 rows
+// per 64 slots, the four rows of each 16-slot group 4 apart, so that their LDS rows (pitch 20
+// floats) start 0, 16, 32, 48 banks apart and a 16-lane write covers the 64 banks once.
+__device__ __forceinline__ int slot_row(int idx) { return (idx >> 6) * 16 + ((idx >> 2) & 3) * 4 + ((idx >> 4) & 3); }
+
 template <int MODE, int ROWS>
 __device__ __forceinline__ TileRegs<ROWS> load_tile(const float *__restrict__ p, int64_t sr, int64_t sk, int rows_left,
                                                     int k_left, int tid) {
@@ -139,11 +144,11 @@ __device__ __forceinline__ TileRegs<ROWS> load_tile(const float *__restrict__ p,
       const int rc = max(0, min(r, rows_left - 4)), kc = min(k, k_left - 1);
       t.v[e] = *reinterpret_cast<const float4 *>(p + int64_t(kc) * sk + rc);
     } else if constexpr (MODE == 1) {  // 128 rows x 4 groups of 4 k
-      const int r = idx >> 2, k = (idx & 3) * 4;
+      const int r = slot_row(idx), k = (idx & 3) * 4;
       const int rc = min(r, rows_left - 1), kc = max(0, min(k, k_left - 4));
       t.v[e] = *reinterpret_cast<const float4 *>(p + int64_t(rc) * sr + kc);
     } else {  // same slots as MODE 1, element by element
-      const int r = idx >> 2, k = (idx & 3) * 4;
+      const int r = slot_row(idx), k = (idx & 3) * 4;
       const int64_t base = int64_t(min(r, rows_left - 1)) * sr;
       t.v[e] = float4{p[base + int64_t(min(k, k_left - 1)) * sk], p[base + int64_t(min(k + 1, k_left - 1)) * sk],
                       p[base + int64_t(min(k + 2, k_left - 1)) * sk], p[base + int64_t(min(k + 3, k_left - 1)) * sk]};
@@ -166,7 +171,7 @@ __device__ __forceinline__ void store_tile(float *lds, const TileRegs<ROWS> &t, 
       lds[(r + 2) * GT_LDK + k] = ok ? v.z : 0.f;
       lds[(r + 3) * GT_LDK + k] = ok ? v.w : 0.f;
     } else {
-      const int r = idx >> 2, k = (idx & 3) * 4;
+      const int r = slot_row(idx), k = (idx & 3) * 4;
       const bool row = r < rows_left;
       float4 o;
       if constexpr (MODE == 1) {
@@ -201,7 +206,7 @@ __device__ __forceinline__ void store_tile_bf16(unsigned short *lds, const TileR
       lds[(r + 2) * GT_LDKB + k] = static_cast<unsigned short>(hi);
       lds[(r + 3) * GT_LDKB + k] = static_cast<unsigned short>(hi >> 16);
     } else {
-      const int r = idx >> 2, k = (idx & 3) * 4;
+      const int r = slot_row(idx), k = (idx & 3) * 4;
       const bool row = r < rows_left;
       float4 o;
       if constexpr (MODE == 1) {
