@@ -39,6 +39,17 @@ class SequenceModel(nn.Module):
     def device(self) -> torch.device:
         return next(self.parameters()).device
 
+    def packs(self, device: torch.device) -> bool:
+        """Whether this model runs packed rows (cardgym.nn.packing) on ``device`` (model.py:50-58):
+        the trunk's HIP path takes per-row sequence bounds on the GPU, forward and backward, so
+        the trainer's microbatches may be packed there; elsewhere padded batches run as they are."""
+
+        return device.type == "cuda" and torch.version.hip is not None
+
+    def enable_metal_trunk(self, max_length: int | None = None) -> None:
+        """The reference routes MPS bf16 trunks through fused Metal kernels (model.py:108-115);
+        the HIP trunk is always fused, so there is nothing to enable and ``trunk.metal`` stays None."""
+
     def embed(self, tokens: torch.Tensor):
         raise NotImplementedError
 

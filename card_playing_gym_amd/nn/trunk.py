@@ -252,6 +252,15 @@ class Trunk(nn.Module):
         if self.ple_context is not None:
             nn.init.zeros_(self.ple_context.weight)
         self._native_cache: dict[tuple[int, int], _NativeTrunk] = {}
+        # The reference's fused Metal trunk (trunk.py:274, model.py:108-115) exists only on
+        # MPS; callers read `metal` and `uses_metal` to choose that path.  Here the HIP
+        # kernels are the path on every call, so there is never a Metal trunk.
+        self.metal = None
+
+    def uses_metal(self, device: torch.device, length: int) -> bool:
+        """The reference's gate for its MPS-only fused kernels (trunk.py:337-346): never here."""
+
+        return False
 
     # -- native handle ---------------------------------------------------------
 

@@ -202,6 +202,24 @@ def test_kv_cache_host_behaviour():
         KVCache(n_layers=1, kv_heads=1, head_dim=8, capacity=1, max_len=4, device="cpu", dtype=torch.int8)
 
 
+def test_model_exposes_what_the_reference_trainer_reads():
+    """The reference's trainer and setup read model.packs(device) on every microbatch
+    (cardgym/rl/trainer.py:659), trunk.metal / trunk.uses_metal(...) to pick its MPS-only fused
+    trunk (trainer.py:709, setup.py:142) and call model.enable_metal_trunk (setup.py:111): the
+    HIP model answers them without a Metal trunk, and packs rows on the ROCm GPU only."""
+
+    from card_playing_gym_amd.nn import SequenceModel
+
+    model = SequenceModel(TrunkConfig(d_model=64, n_layers=1, n_heads=4, n_kv_heads=2, d_ff=128))
+    assert model.trunk.metal is None
+    assert model.trunk.uses_metal(torch.device("cuda", 0), 128) is False
+    assert model.packs(torch.device("cpu")) is False
+    assert model.packs(torch.device("cuda", 0)) is (torch.version.hip is not None)
+    assert model.enable_metal_trunk(512) is None and model.trunk.metal is None
+    for name in ("forward_ragged", "forward_prefill", "final_norm", "config", "condition"):
+        assert hasattr(model.trunk, name), name
+
+
 def test_no_cpu_fallback_in_the_product_path():
     model = build_model(TrunkConfig(d_model=64, n_layers=1, n_heads=4, n_kv_heads=2, d_ff=128))
     tokens = torch.zeros((2, 1, 1), dtype=torch.int64)
