@@ -494,6 +494,43 @@ def train_step_time(bench: Bench, with_reference: bool, warmup: int = 3, reps: i
                 entry["speedup"] = round(entry["reference_gpu_ms_per_step"] / entry["ms_per_step"], 2)
             result[f"{batch}x{length}"] = entry
             trunk.zero_grad(set_to_none=True)
+        # A ragged microbatch as each trainer runs it (cardgym/rl/trainer.py:652-667): packed rows
+        # here (SequenceModel.packs is True on the ROCm GPU), padded to the longest sequence in
+        # the reference (its packs() is True only with the MPS Metal trunk).
+        lengths = np.random.default_rng(5).integers(32, 257, size=96)
+        starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+        n_real, longest = int(lengths.sum()), int(lengths.max())
+        g = torch.Generator(device=dev).manual_seed(5)
+        xp = torch.randn((n_real, cfg.d_model), generator=g, device=dev).requires_grad_()
+        wp = torch.randn((n_real, cfg.d_model), generator=g, device=dev)
+        bounds = torch.from_numpy(np.concatenate([np.stack([np.full(n, s), np.full(n, s + n)], axis=1)
+                                                  for s, n in zip(starts, lengths)])).to(dev)
+        keep = torch.from_numpy(np.concatenate([np.arange(n) + b * longest for b, n in enumerate(lengths)])).to(dev)
+        xpad = torch.zeros((len(lengths) * longest, cfg.d_model), device=dev)
+        xpad[keep] = xp.detach()
+        xpad = xpad.view(len(lengths), longest, cfg.d_model).requires_grad_()
+        wpad = torch.zeros((len(lengths) * longest, cfg.d_model), device=dev)
+        wpad[keep] = wp
+        wpad = wpad.view(len(lengths), longest, cfg.d_model)
+
+        def ours_packed():
+            with autocast:
+                h = trunk(*trunk.condition(xp, None, None), bounds)
+            (h * wp).sum().backward()
+
+        def theirs_padded():
+            with autocast:
+                h = ref.forward_full(*ref.condition(xpad, None, None))
+            (h * wpad).sum().backward()
+
+        entry = {"sequences": len(lengths), "tokens": n_real, "padded_tokens": len(lengths) * longest,
+                 "ms_per_step": round(wall(ours_packed) * 1e3, 3)}
+        entry["tokens_per_s"] = round(n_real / entry["ms_per_step"] * 1e3, 1)
+        if ref is not None:
+            entry["reference_gpu_ms_per_step"] = round(wall(theirs_padded) * 1e3, 3)
+            entry["speedup"] = round(entry["reference_gpu_ms_per_step"] / entry["ms_per_step"], 2)
+        result["ragged_96_packed_vs_padded"] = entry
+        trunk.zero_grad(set_to_none=True)
         out[precision] = result
     del trunk, ref
     torch.cuda.empty_cache()

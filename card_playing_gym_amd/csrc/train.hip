@@ -405,9 +405,12 @@ GemmPlan gemm_plan(int32_t m, int32_t n, int32_t k, bool generic) {
   int tm = GT_M;
   if (!generic && m > 64 && tiles128 < 512 && !(k >= 1024 && tiles128 < 128)) tm = 64;
   const int64_t tiles = int64_t((m + tm - 1) / tm) * nt;
+  // Split K toward 512 blocks, but never past the 768 the chip holds at once (256 CUs x 3
+  // blocks): 408 tiles split in two would run as a full wave plus a 48-block tail, slower
+  // than the unsplit 408 tiles (13041-token packed batches hit this).
   int slices = 1;
   if (tiles < 512 && k >= 4 * GT_K * 16) {
-    slices = int(std::min<int64_t>((512 + tiles - 1) / tiles, k / (GT_K * 16)));
+    slices = int(std::min<int64_t>({(512 + tiles - 1) / tiles, 768 / tiles, k / (GT_K * 16)}));
     slices = std::max(1, std::min(slices, 64));
   }
   const int kc = ((k + slices - 1) / slices + GT_K - 1) / GT_K * GT_K;
