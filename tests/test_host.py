@@ -315,3 +315,29 @@ def test_ordered_pairs_matches_its_definition():
     assert ordered_pairs(np.array([3, 4, 5, 9]), np.array([0, 1, 2, 3]), 10)
     assert not ordered_pairs(np.array([1, 2]), np.array([2, 1]), 4)
     assert not ordered_pairs(np.array([0, 1, 2]), np.array([1, 2, 3]), 4)
+
+
+def test_packed_bounds_to_sequence_starts():
+    """Packed-row bounds as cardgym.nn.packing.Packing builds them (packing.py:24-40: int32
+    [N, 2], row i -> [start, end) of its sequence) give the sequences' starts and the longest
+    one; bounds that do not tile the rows with whole sequences are refused."""
+
+    lengths = np.array([3, 1, 5, 2])
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    first = np.repeat(starts, lengths)
+    bounds = torch.from_numpy(np.stack([first, first + np.repeat(lengths, lengths)], axis=1).astype(np.int32))
+    seq_start, longest = Trunk._seq_start_of(bounds)
+    assert seq_start.dtype == torch.int64 and seq_start.tolist() == [0, 3, 4, 9, 11] and longest == 5
+    assert Trunk._seq_start_of(torch.tensor([[0, 1]], dtype=torch.int32))[0].tolist() == [0, 1]
+
+    short_end = bounds.clone()
+    short_end[2, 1] -= 1  # the first sequence's last row ends one row early
+    split_seq = bounds.clone()
+    split_seq[5:9, 0] = 5  # the third sequence's rows claim a start inside it
+    for bad in (short_end, split_seq):
+        with pytest.raises(ValueError, match="back to back"):
+            Trunk._seq_start_of(bad)
+    with pytest.raises(ValueError, match=r"\[N, 2\]"):
+        Trunk._seq_start_of(bounds[:, :1])
+    with pytest.raises(ValueError, match="at least one row"):
+        Trunk._seq_start_of(bounds[:0])
