@@ -18,8 +18,11 @@ Each oracle function is checked against something that does not retype its formu
                                              rows, PLE and value embeddings switched on
   conditioning                               zero PLE / VE tables leave the function
                                              unchanged (tests/nn/test_trunk.py:91-104)
-  bf16 rounding policy                       golden vectors written by the reference's own
-                                             trunk (tests/golden/), when present
+  bf16-KV rounding chain (trunk.py:222-255)  golden vectors written by the reference's own
+                                             trunk, bit for bit (tests/test_golden.py)
+  bf16 autocast policy (precision="bf16")    bit-equal to the fp32 oracle under real
+                                             torch.autocast on the GPU
+                                             (tests/test_gpu_golden.py)
 """
 
 from __future__ import annotations
