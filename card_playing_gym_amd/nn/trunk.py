@@ -26,6 +26,7 @@ import torch
 from torch import nn
 
 from .. import _native as nat
+from .derived import DerivedCopies, HandleCache, after_load_hook
 from .kv_cache import KVCache, index_tensor, require_device, stream_handle
 
 ValueEmbeddingMode = Literal["off", "alternating", "all"]
@@ -156,13 +157,12 @@ def compute_dtype_code(device: torch.device) -> int:
     return nat.CG_F32
 
 
-class _NativeTrunk:
+class _NativeTrunk(DerivedCopies):
     """A ``cg_trunk`` handle over the module's parameters for one compute dtype."""
 
-    def __init__(self, trunk: "Trunk", compute: int) -> None:
+    def __init__(self, trunk: "Trunk", compute: int, device: torch.device) -> None:
+        super().__init__(_trunk_tensors(trunk), device)
         self.compute = compute
-        self.params = list(_trunk_tensors(trunk))
-        self.signature = _signature(self.params)
         config = trunk.config
         cfg = nat.TrunkConfig(
             config.d_model, config.n_layers, config.n_heads, config.n_kv_heads, config.d_ff,
@@ -185,20 +185,9 @@ class _NativeTrunk:
             _param(trunk.final_norm.bias).data_ptr(), compute, ctypes.byref(handle),
         )
         self.handle = handle
-        self.versions = _versions(self.params)
 
-    def sync(self, trunk: "Trunk", stream: int) -> bool:
-        """False when the parameters moved (rebuild); re-derives weight copies after edits."""
-
-        if _signature(self.params) != self.signature or len(self.params) != len(list(_trunk_tensors(trunk))):
-            return False
-        if any(a is not b for a, b in zip(self.params, _trunk_tensors(trunk))):
-            return False
-        versions = _versions(self.params)
-        if versions != self.versions:
-            nat.call("cg_trunk_refresh", self.handle, stream)
-            self.versions = versions
-        return True
+    def _refresh(self, stream: int) -> None:
+        nat.call("cg_trunk_refresh", self.handle, stream)
 
     def close(self) -> None:
         if self.handle:
@@ -206,12 +195,6 @@ class _NativeTrunk:
                 nat.lib().cg_trunk_destroy(self.handle)
             finally:
                 self.handle = ctypes.c_void_p()
-
-    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
-        try:
-            self.close()
-        except Exception:
-            pass
 
 
 def _trunk_tensors(trunk: "Trunk"):
@@ -223,14 +206,6 @@ def _trunk_tensors(trunk: "Trunk"):
         )
     yield trunk.final_norm.weight
     yield trunk.final_norm.bias
-
-
-def _signature(params) -> tuple[int, ...]:
-    return tuple(p.data_ptr() for p in params)
-
-
-def _versions(params) -> tuple[int, ...]:
-    return tuple(p._version for p in params)
 
 
 class Trunk(nn.Module):
@@ -252,7 +227,10 @@ class Trunk(nn.Module):
             block.mlp[2].weight.data.mul_(residual_scale)
         if self.ple_context is not None:
             nn.init.zeros_(self.ple_context.weight)
-        self._native_cache: dict[tuple[int, int], _NativeTrunk] = {}
+        # bf16 weight copies per (device, compute dtype), kept current after optimiser steps
+        # and load_state_dict (card_playing_gym_amd/nn/derived.py).
+        self._handles = HandleCache()
+        self.register_load_state_dict_post_hook(after_load_hook)
         # The reference's fused Metal trunk (trunk.py:274, model.py:108-115) exists only on
         # MPS; callers read `metal` and `uses_metal` to choose that path.  Here the HIP
         # kernels are the path on every call, so there is never a Metal trunk.
@@ -268,21 +246,25 @@ class Trunk(nn.Module):
     def native(self, device: torch.device) -> _NativeTrunk:
         compute = compute_dtype_code(device)
         key = (device.index if device.index is not None else torch.cuda.current_device(), compute)
-        entry = self._native_cache.get(key)
-        if entry is not None and entry.sync(self, stream_handle(device)):
-            return entry
-        if entry is not None:
-            entry.close()
-        entry = _NativeTrunk(self, compute)
-        self._native_cache[key] = entry
-        return entry
+        return self._handles.get(
+            key, list(_trunk_tensors(self)), lambda: _NativeTrunk(self, compute, device), stream_handle(device)
+        )
+
+    def refresh_native(self) -> int:
+        """Re-derives the bf16 weight copies now, if the parameters changed in place since
+        (optimiser steps and ``load_state_dict`` do this by themselves).  Returns the number
+        of handles refreshed."""
+
+        return self._handles.refresh()
 
     def _apply(self, fn, *args, **kwargs):
-        # Moving or casting parameters invalidates every handle (they hold raw pointers).
-        for entry in getattr(self, "_native_cache", {}).values():
-            entry.close()
-        self._native_cache = {}
-        return super()._apply(fn, *args, **kwargs)
+        out = super()._apply(fn, *args, **kwargs)
+        # Handles hold raw pointers: those whose parameters moved are retired (kept alive for
+        # graphs captured before the move, no longer used for new calls).
+        handles = self.__dict__.get("_handles")
+        if handles is not None:
+            handles.retire_moved(lambda key: list(_trunk_tensors(self)))
+        return out
 
     # -- conditioning ----------------------------------------------------------
 
@@ -329,6 +311,7 @@ class Trunk(nn.Module):
             return False
         return any(t is not None and t.requires_grad for t in inputs) or any(p.requires_grad for p in self.parameters())
 
+    @torch.compiler.disable
     def _condition_train(self, x, ple_lookup, value_lookup):
         from .train import PleContextFunction, RMSNormFunction, train_precision
 

@@ -22,6 +22,7 @@ import torch
 from torch import nn
 
 from . import _native as nat
+from .nn.derived import DerivedCopies, HandleCache, after_load_hook
 from .nn.kv_cache import require_device, stream_handle
 from .nn.model import SequenceModel, value_mlp
 from .nn.trunk import TrunkConfig, _param, compute_dtype_code, init_weights
@@ -44,6 +45,7 @@ class SyntheticModel(SequenceModel):
         self.policy_head = nn.Linear(d, vocab)
         init_weights(self.policy_head)
         self.value_head = value_mlp(d, seats)
+        self.register_load_state_dict_post_hook(after_load_hook)
 
     def embed(self, tokens: torch.Tensor):
         return self.embedding(tokens[..., 0]), None, None
@@ -52,7 +54,8 @@ class SyntheticModel(SequenceModel):
         """Embedding lookup fused with the trunk's input RMSNorm (one kernel)."""
 
         trunk = self.trunk
-        if trunk.input_norm is None:
+        if trunk.input_norm is None or trunk._recording(self.embedding.weight):
+            # Under autograd: the embedding lookup, then the trunk's differentiable input norm.
             return super().prepare(tokens)
         require_device(tokens)
         ids = tokens[..., 0].reshape(-1).to(torch.int64).contiguous()
@@ -72,6 +75,8 @@ class SyntheticModel(SequenceModel):
         rounding; otherwise three fp32 ``cg_linear`` products."""
 
         require_device(hidden)
+        if torch.is_grad_enabled() and (hidden.requires_grad or any(p.requires_grad for p in self._head_tensors())):
+            raise RuntimeError("the fused heads are inference-only: call them under torch.no_grad()")
         device = hidden.device
         compute = compute_dtype_code(device)
         stream = stream_handle(device)
@@ -106,47 +111,39 @@ class SyntheticModel(SequenceModel):
 
     def _native_heads(self, device: torch.device) -> "_NativeHeads":
         key = device.index if device.index is not None else torch.cuda.current_device()
-        cache = self.__dict__.setdefault("_heads_cache", {})
-        entry = cache.get(key)
-        if entry is not None and entry.sync(self._head_tensors(), stream_handle(device)):
-            return entry
-        if entry is not None:
-            entry.close()
-        entry = _NativeHeads(self)
-        cache[key] = entry
-        return entry
+        handles = self.__dict__.get("_heads_handles")
+        if handles is None:
+            handles = self.__dict__["_heads_handles"] = HandleCache()
+        return handles.get(key, self._head_tensors(), lambda: _NativeHeads(self, device), stream_handle(device))
+
+    def refresh_native(self) -> int:
+        """Re-derives every bf16 weight copy (trunk and heads) whose parameters changed in
+        place; optimiser steps and ``load_state_dict`` do this by themselves."""
+
+        handles = self.__dict__.get("_heads_handles")
+        return self.trunk.refresh_native() + (handles.refresh() if handles is not None else 0)
 
     def _apply(self, fn, *args, **kwargs):
-        # Moving or casting parameters invalidates the heads handles (they hold raw pointers).
-        for entry in self.__dict__.get("_heads_cache", {}).values():
-            entry.close()
-        self.__dict__["_heads_cache"] = {}
-        return super()._apply(fn, *args, **kwargs)
+        out = super()._apply(fn, *args, **kwargs)
+        handles = self.__dict__.get("_heads_handles")
+        if handles is not None:
+            handles.retire_moved(lambda key: self._head_tensors())
+        return out
 
 
-class _NativeHeads:
+class _NativeHeads(DerivedCopies):
     """A ``cg_heads`` handle over the model's head parameters (bf16 fragment copies)."""
 
-    def __init__(self, model: SyntheticModel) -> None:
-        self.params = [_param(t) for t in model._head_tensors()]
-        self.signature = tuple(t.data_ptr() for t in self.params)
-        self.versions = tuple(t._version for t in self.params)
+    def __init__(self, model: SyntheticModel, device: torch.device) -> None:
+        super().__init__([_param(t) for t in model._head_tensors()], device)
         first, last = model.value_head[0], model.value_head[2]
         cfg = nat.HeadsConfig(model.trunk_config.d_model, model.vocab, first.out_features, last.out_features)
         handle = ctypes.c_void_p()
         nat.call("cg_heads_create", ctypes.byref(cfg), *(t.data_ptr() for t in self.params), ctypes.byref(handle))
         self.handle = handle
 
-    def sync(self, tensors: list[torch.Tensor], stream: int) -> bool:
-        """False when the parameters moved (rebuild); re-derives the copies after edits."""
-
-        if tuple(t.data_ptr() for t in tensors) != self.signature or any(a is not b for a, b in zip(tensors, self.params)):
-            return False
-        versions = tuple(t._version for t in self.params)
-        if versions != self.versions:
-            nat.call("cg_heads_refresh", self.handle, stream)
-            self.versions = versions
-        return True
+    def _refresh(self, stream: int) -> None:
+        nat.call("cg_heads_refresh", self.handle, stream)
 
     def close(self) -> None:
         if self.handle:
@@ -154,12 +151,6 @@ class _NativeHeads:
                 nat.lib().cg_heads_destroy(self.handle)
             finally:
                 self.handle = ctypes.c_void_p()
-
-    def __del__(self) -> None:  # pragma: no cover - interpreter shutdown order
-        try:
-            self.close()
-        except Exception:
-            pass
 
 
 def build_model(config: TrunkConfig, seed: int = 0, device: str | torch.device = "cpu") -> SyntheticModel:

@@ -100,7 +100,7 @@ def test_bad_ids_and_codes_are_flagged(device):
     x = torch.empty((20, config.d_model), dtype=torch.bfloat16, device=device)
     cards = torch.empty((20, NUM_CARDS, 32), device=device)
     stream = torch.cuda.current_stream().cuda_stream
-    handle = module.native(stream)
+    handle = module.native(device)
     nat.call("cg_piquet_embed", handle.handle, flat.data_ptr(), 64, 20, x.data_ptr(), None, None, cards.data_ptr(),
              flag.data_ptr(), stream)
     torch.cuda.synchronize()
@@ -169,3 +169,18 @@ def test_piquet_trunk_step(device):
             got = trunk.forward_ragged(*trunk.condition(x, ple, values), cache, lengths.to(device), readout.to(device))
     err = (got.float().cpu() - want.float()).abs().max().item()
     assert err <= TOL, err
+
+
+def test_embedder_refuses_autograd(device):
+    """The kernels have no backward: under autograd with trainable parameters the call
+    raises instead of returning values whose tables and grid would get no gradient."""
+
+    config = PiquetModelConfig(card_layers=1)
+    module, _ = twins(config, 0, 0, device, seed=3)
+    tokens = random_tokens(4, seed=4).to(device)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        with pytest.raises(RuntimeError, match="inference-only"):
+            module(tokens)
+        module.requires_grad_(False)
+        x, _, _ = module(tokens)  # frozen parameters: nothing to differentiate
+    assert not x.requires_grad

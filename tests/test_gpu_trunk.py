@@ -178,6 +178,74 @@ def test_graph_replay_matches_eager(device):
             assert torch.equal(got[0], eager[0]) and torch.equal(got[1], eager[1]), f"replay {replay}"
 
 
+@pytest.mark.parametrize("update", ["load_state_dict", "sgd_step", "fused_adam_step"])
+def test_graph_replay_follows_weight_updates(device, update):
+    """A step captured once keeps replaying with the current weights after they change in
+    place, as the reference's decode graphs do across trainer updates
+    (cardgym/rl/graphs.py:17-22): replay == eager == oracle on the new weights."""
+
+    config = trunk_config(4)
+    model, _ = twins(config, "bf16", device)
+    games, max_len = 128, 96
+    cache = model.new_cache(games, max_len, torch.bfloat16)
+    gen = torch.Generator(device=device).manual_seed(5)
+    for layer in range(config.n_layers):
+        cache.k[layer].normal_(generator=gen)
+        cache.v[layer].normal_(generator=gen)
+    lengths = torch.randint(1, 80, (games,), device=device, generator=gen)
+    tokens = torch.randint(0, 512, (games, 1, 1), device=device, generator=gen)
+    readout = torch.zeros(games, dtype=torch.int64, device=device)
+
+    def body():
+        with autocast(device, "bf16"):
+            hidden = model.forward_ragged(tokens, lengths, cache, readout)
+            return model.heads(hidden)
+
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            body()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            g_logits, g_values = body()
+        graph.replay()
+        before = g_logits.clone()
+    # Change every weight in place, the way the named update does.
+    if update == "load_state_dict":
+        fresh = {k: v.detach().clone() for k, v in twins(config, "bf16", device, seed=9)[0].state_dict().items()}
+        model.load_state_dict(fresh)
+    else:
+        params = [p for p in model.parameters()]
+        optimizer = (torch.optim.SGD(params, lr=0.05) if update == "sgd_step"
+                     else torch.optim.Adam(params, lr=0.01, fused=True))
+        g = torch.Generator(device=device).manual_seed(6)
+        for p in params:
+            p.grad = torch.randn(p.shape, device=device, generator=g) * 0.1
+        optimizer.step()
+        optimizer.zero_grad(set_to_none=True)
+    with torch.no_grad():
+        graph.replay()
+        got = (g_logits.clone(), g_values.clone())
+        eager = body()
+    torch.cuda.synchronize()
+    assert not torch.equal(got[0], before), "the replay did not see the new weights"
+    assert torch.equal(got[0], eager[0]) and torch.equal(got[1], eager[1])
+    # And the new weights are the oracle's: the same step on a CPU copy.
+    from oracle.reference_path import RefSynthetic
+
+    state = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    ref = RefSynthetic(state, ref_config_of(config), "bf16")
+    ref_cache = RefCache(config.n_layers, config.n_kv_heads, config.head_dim, games, max_len, torch.bfloat16)
+    for layer in range(config.n_layers):
+        ref_cache.k[layer].copy_(cache.k[layer].cpu())
+        ref_cache.v[layer].copy_(cache.v[layer].cpu())
+    with torch.no_grad():
+        want = ref.heads(ref.forward_ragged(tokens.cpu(), lengths.cpu(), ref_cache, readout.cpu()))
+    assert max_err(got[0], want[0]) <= BF16_TOL and max_err(got[1], want[1]) <= BF16_TOL
+
+
 @pytest.mark.parametrize("name", ["cfg3", "cfg4", "cfg5"])
 def test_full_size_sampled_games_match_oracle(device, name):
     """Configs 3-5 at full size (4096 games, 8192 permuted slots, ~35k packed chunk tokens):
