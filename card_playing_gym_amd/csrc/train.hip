@@ -1192,6 +1192,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const AttnTrain a) {
     }
 }
 
+// dst[i] = 0: clears the accumulated gradients (a kernel rather than a memset node, so a
+// captured backward replays it like any other launch).
+__global__ void zero_fill_kernel(float *__restrict__ dst, int64_t n) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+    dst[i] = 0.0f;
+}
+
 // dst[r, c] += alpha * src[r * ld_src + c] (ld_src 0 broadcasts one row: bias adds).
 __global__ void add_strided_kernel(int32_t rows, int32_t cols, float alpha, const float *__restrict__ src,
                                    int64_t ld_src, float *__restrict__ dst, int64_t ld_dst) {
@@ -1850,8 +1857,14 @@ int cg_trunk_train_backward(const cg_train_config *c, const cg_train_block *bloc
     const int32_t N = int32_t(t.n);
     ok(cg_norm_bwd(tail.x_last, dhidden, final_w, tail.mf, tail.rf, s.dx, nullptr, grads->final_dw,
                    grads->final_db, N, int32_t(t.d), s.red, s.red_bytes, 0, st));
-    if (dple) CG_HIP(hipMemsetAsync(dple, 0, size_t(t.n * t.P) * 4, st));
-    if (dvalues) CG_HIP(hipMemsetAsync(dvalues, 0, size_t(t.n * t.V) * 4, st));
+    if (dple) {
+      zero_fill_kernel<<<grid_1d(t.n * t.P), 256, 0, st>>>(dple, t.n * t.P);
+      CG_LAUNCHED();
+    }
+    if (dvalues) {
+      zero_fill_kernel<<<grid_1d(t.n * t.V), 256, 0, st>>>(dvalues, t.n * t.V);
+      CG_LAUNCHED();
+    }
     for (int64_t l = t.L - 1; l >= 0; --l) {
       const cg_train_block &w = blocks[l];
       const cg_train_block_grads &gw = grads->blocks[l];

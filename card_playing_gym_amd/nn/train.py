@@ -294,9 +294,14 @@ class TrunkFunction(torch.autograd.Function):
         return (None, None, None, dx, dple, dvalues, *grads)
 
 
+@torch.compiler.disable
 def trunk_train_forward(trunk, x, ple, values, bounds=None):
     """Trunk.forward under autograd: [B, T, d] (or packed rows [N, d] with ``bounds``) ->
-    final-norm hidden states of the same leading shape, differentiable."""
+    final-norm hidden states of the same leading shape, differentiable.
+
+    Opaque to torch.compile: the reference trainer compiles ``forward_hidden``
+    (cardgym/rl/trainer.py:386, cardgym/nn/compile.py:26-44); dynamo runs this call eagerly
+    (its host-side bounds check and the C-ABI calls) and compiles around it."""
 
     bf16 = train_precision(x.device)
     c = trunk.config
