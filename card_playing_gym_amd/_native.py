@@ -23,6 +23,7 @@ CG_OK, CG_ERR_INVALID, CG_ERR_UNSUPPORTED, CG_ERR_RANGE, CG_ERR_HIP = 0, 1, 2, 3
 CG_F32, CG_BF16, CG_F16 = 0, 1, 2
 CG_ACT_NONE, CG_ACT_GELU = 0, 1
 CG_COPY_AUTO, CG_COPY_ORDERED = 0, 1
+CG_TRUNK_STATIC_WORKSPACE = 64 << 20
 
 c_int32 = ctypes.c_int32
 c_int64 = ctypes.c_int64
@@ -179,6 +180,9 @@ _SIGNATURES = {
     "cg_trunk_forward": (
         c_int32,
         [c_void_p, P(KVLayer), c_void_p, c_void_p, c_void_p, P(Ragged), c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "cg_trunk_forward_static": (
+        c_int32, [c_void_p, P(KVLayer), c_void_p, c_void_p, c_void_p, P(Ragged), c_void_p, c_void_p],
     ),
     "cg_rmsnorm": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_int32, c_void_p]),
     "cg_embed_rmsnorm": (

@@ -7,6 +7,7 @@
 // This is DecoderBlock.forward_ragged / Trunk.forward_ragged (cardgym/nn/trunk.py:183-223,
 // 391-429) with the gather copy and the masked full-span attention replaced by in-place
 // attention over each row's own prefix.
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -297,274 +298,327 @@ size_t cg_trunk_workspace_size(const cg_trunk *trunk, int32_t n_tokens, int32_t 
   return carve(*trunk, n_tokens, n_seqs, nullptr).bytes;
 }
 
+}  // extern "C"
+
+namespace cg {
+namespace {
+
+// The step on a given workspace: cg_trunk_forward and cg_trunk_forward_static.
+void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x, const float *ple,
+                   const float *values, const cg_ragged *step, float *hidden, void *workspace,
+                   size_t workspace_size, void *stream) {
+  CG_REQUIRE(trunk && cache && x && step && hidden, CG_ERR_INVALID,
+             "trunk, cache, x, step and hidden are required");
+  const cg_trunk &t = *trunk;
+  const cg_trunk_config &c = t.cfg;
+  const cg_ragged &r = *step;
+  CG_REQUIRE(r.n_seqs >= 0 && r.n_tokens >= 0, CG_ERR_INVALID, "negative step size");
+  CG_REQUIRE(r.positions != nullptr, CG_ERR_INVALID, "positions is NULL");
+  CG_REQUIRE(r.seq_start || int64_t(r.n_seqs) * r.T == r.n_tokens, CG_ERR_INVALID,
+             "padded step: n_tokens must equal n_seqs * T");
+  CG_REQUIRE(c.per_layer_dim == 0 || ple, CG_ERR_INVALID,
+             "This trunk expects a per-layer embedding lookup.");
+  CG_REQUIRE(c.value_width == 0 || values, CG_ERR_INVALID,
+             "This trunk expects a value-embedding lookup.");
+  for (int l = 0; l < c.n_layers; ++l) {
+    const cg_kv_layer &L = cache[l];
+    check_layer(&L);
+    CG_REQUIRE(L.kv_heads == c.n_kv_heads && L.head_dim == t.head_dim, CG_ERR_INVALID,
+               "cache layout does not match the trunk");
+    CG_REQUIRE(L.max_len == cache[0].max_len && L.capacity == cache[0].capacity &&
+                   L.dtype == cache[0].dtype,
+               CG_ERR_INVALID, "cache layers differ in shape");
+  }
+  CG_REQUIRE(r.rows || r.n_seqs <= cache[0].capacity, CG_ERR_RANGE,
+             "dense rows: more sequences than cache rows");
+  if (r.n_tokens == 0 || r.n_seqs == 0) return;
+  Workspace w = carve(t, r.n_tokens, r.n_seqs, static_cast<char *>(workspace));
+  CG_REQUIRE(workspace && workspace_size >= w.bytes, CG_ERR_INVALID,
+             "workspace too small: need " + std::to_string(w.bytes) + " bytes");
+  hipStream_t s = as_stream(stream);
+  const int d = c.d_model, H = c.n_heads, KVH = c.n_kv_heads, D = t.head_dim;
+  const int N = r.n_tokens;
+  const int max_len = cache[0].max_len;
+  const int span = (r.span <= 0 || r.span > max_len) ? max_len : r.span;
+  const int act_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
+
+  {
+    const int n = N > r.n_seqs ? N : r.n_seqs;
+    plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout,
+                                                r.n_seqs, N, r.T, max_len, cache[0].capacity,
+                                                w.tok_row, w.tok_pos, w.readout_tok, w.tok_out,
+                                                hidden, d);
+    CG_LAUNCHED();
+  }
+  const float ple_scale = [&] {
+    if (c.per_layer_dim == 0 || c.per_layer_dim == d) return 1.0f;
+    const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
+    return 1.0f / sqrtf(float(repeats));
+  }();
+  auto attention = [&](int l) {
+    const cg_kv_layer &L = cache[l];
+    {
+      AttnArgs a{};
+      a.q = w.q;
+      a.q_dtype = CG_F32;
+      a.q_st = int64_t(H) * D;
+      a.q_sh = D;
+      a.q_sb = int64_t(r.T) * H * D;
+      a.out = w.attn;
+      a.out_dtype = act_dtype;
+      a.o_st = int64_t(H) * D;
+      a.o_sh = D;
+      a.o_sb = int64_t(r.T) * H * D;
+      a.k = L.k;
+      a.v = L.v;
+      a.kv_dtype = L.dtype;
+      a.rows = r.rows;
+      a.key_lengths = r.positions;
+      a.kl_add = 1;
+      a.seq_start = r.seq_start;
+      a.n_tokens = N;
+      a.n_seqs = r.n_seqs;
+      a.n_heads = H;
+      a.kv_heads = KVH;
+      a.head_dim = D;
+      a.T = r.T;
+      a.max_len = max_len;
+      a.capacity = L.capacity;
+      a.span = span;
+      a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
+      launch_decode_attention(a, s);
+    }
+  };
+
+  const int n_qkv = (H + 2 * KVH) * D;
+  if (t.fused) {
+    // bf16 projections: one fused launch per layer after its attention (layer.hip), plus
+    // the first block's LN + QKV + append.
+    auto base = [&] {
+      TailArgs ta{};
+      ta.M = N;
+      ta.d = d;
+      ta.d_ff = c.d_ff;
+      ta.n_qkv = n_qkv;
+      ta.q_cols = H * D;
+      ta.kv_heads = KVH;
+      ta.head_dim = D;
+      ta.max_len = max_len;
+      ta.kv_dtype = cache[0].dtype;
+      ta.eps = c.eps;
+      ta.q = w.q;
+      ta.tok_row = w.tok_row;
+      ta.tok_pos = w.tok_pos;
+      ta.vemb = values;
+      ta.ld_vemb = c.value_width;
+      ta.vemb_off = -1;
+      ta.hidden = hidden;
+      ta.tok_out = w.tok_out;
+      return ta;
+    };
+    auto set_next = [&](TailArgs &ta, int nl) {
+      if (nl == c.n_layers) {
+        ta.final_ln = 1;
+        ta.ln_w = t.final_w;
+        ta.ln_b = t.final_b;
+        return;
+      }
+      const cg_layer_params &Pn = t.layers[nl];
+      ta.final_ln = 0;
+      ta.ln_w = Pn.ln_attn_w;
+      ta.ln_b = Pn.ln_attn_b;
+      ta.w_qkv = t.qkv_w[nl];
+      ta.kc = cache[nl].k;
+      ta.vc = cache[nl].v;
+      ta.vemb_off = (values && Pn.value_index >= 0) ? Pn.value_index * KVH * D : -1;
+    };
+    {
+      TailArgs ta = base();
+      ta.do_post = 0;
+      ta.x_src = x;
+      ta.x = w.x;
+      set_next(ta, 0);
+      launch_tail(ta, s);
+    }
+    // The tail of layer l: its post-attention half, then the next layer's QKV (or the
+    // final norm).
+    auto tail_of = [&](int l) {
+      const cg_layer_params &P = t.layers[l];
+      TailArgs ta = base();
+      ta.do_post = 1;
+      ta.attn = w.attn;
+      ta.w_out = t.out_w[l];
+      ta.w_up = t.up_w[l];
+      ta.b_up = P.mlp_up_b;
+      ta.w_down = t.down_w[l];
+      ta.b_down = P.mlp_down_b;
+      ta.ln2_w = P.ln_mlp_w;
+      ta.ln2_b = P.ln_mlp_b;
+      if (ple && c.per_layer_dim > 0) {
+        ta.ple = ple;
+        ta.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
+        ta.ple_off = l * c.per_layer_dim;
+        ta.ple_dim = c.per_layer_dim;
+        ta.ple_scale = ple_scale;
+      }
+      ta.x_src = w.x;
+      ta.x = w.x;
+      set_next(ta, l + 1);
+      return ta;
+    };
+    for (int l = 0; l < c.n_layers; ++l) {
+      attention(l);
+      launch_tail(tail_of(l), s);
+    }
+    return;
+  }
+
+  CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
+  launch_layernorm_rows(w.x, nullptr, t.layers[0].ln_attn_w, t.layers[0].ln_attn_b, c.eps, w.xn,
+                        act_dtype, N, d, s);
+  // Whole-row residual tiles fuse the next LayerNorm into the residual epilogue.
+  const bool fused_ln = d <= 256;
+
+  auto residual = [&](const void *A, int K, const void *W, const float *bias, const float *ln_w,
+                      const float *ln_b, const float *ple_rows, int layer) {
+    GemmArgs g{};
+    g.M = N;
+    g.N = d;
+    g.K = K;
+    g.compute = t.compute;
+    g.A = A;
+    g.lda = K;
+    g.W = W;
+    g.bias = bias;
+    g.resid = w.x;
+    g.ldr = d;
+    if (ple_rows) {
+      g.ple = ple_rows;
+      g.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
+      g.ple_off = layer * c.per_layer_dim;
+      g.ple_dim = c.per_layer_dim;
+      g.ple_scale = ple_scale;
+    }
+    if (ln_w && fused_ln) {
+      g.epi = EPI_RESID_LN;
+      g.ln_w = ln_w;
+      g.ln_b = ln_b;
+      g.eps = c.eps;
+      g.out = w.xn;
+      g.out_dtype = act_dtype;
+      g.ldo = d;
+      launch_gemm(g, s);
+      return;
+    }
+    g.epi = EPI_RESID;
+    launch_gemm(g, s);
+    if (ln_w) launch_layernorm_rows(w.x, nullptr, ln_w, ln_b, c.eps, w.xn, act_dtype, N, d, s);
+  };
+
+  for (int l = 0; l < c.n_layers; ++l) {
+    const cg_layer_params &P = t.layers[l];
+    const cg_kv_layer &L = cache[l];
+    {  // QKV projection of LN1(x) + append
+      GemmArgs g{};
+      g.M = N;
+      g.N = (H + 2 * KVH) * D;
+      g.K = d;
+      g.compute = t.compute;
+      g.A = w.xn;
+      g.lda = d;
+      g.W = t.qkv_w[l];
+      g.epi = EPI_QKV;
+      g.out = w.q;
+      g.ldo = H * D;
+      g.q_cols = H * D;
+      g.kc = L.k;
+      g.vc = L.v;
+      g.kv_dtype = L.dtype;
+      g.kv_heads = KVH;
+      g.head_dim = D;
+      g.max_len = max_len;
+      g.tok_row = w.tok_row;
+      g.tok_pos = w.tok_pos;
+      g.vemb = values;
+      g.ld_vemb = c.value_width;
+      g.vemb_off = (values && P.value_index >= 0) ? P.value_index * KVH * D : -1;
+      launch_gemm(g, s);
+    }
+    attention(l);
+    // out_proj + residual, then LN2 -> xn
+    residual(w.attn, H * D, t.out_w[l], nullptr, P.ln_mlp_w, P.ln_mlp_b, nullptr, l);
+    {  // mlp[0] + GELU
+      GemmArgs g{};
+      g.M = N;
+      g.N = c.d_ff;
+      g.K = d;
+      g.compute = t.compute;
+      g.A = w.xn;
+      g.lda = d;
+      g.W = t.up_w[l];
+      g.bias = P.mlp_up_b;
+      g.epi = EPI_GELU;
+      g.out = w.h1;
+      g.out_dtype = act_dtype;
+      g.ldo = c.d_ff;
+      launch_gemm(g, s);
+    }
+    // mlp[2] + residual (+ PLE), then the next block's LN1 -> xn
+    const bool last = l + 1 == c.n_layers;
+    residual(w.h1, c.d_ff, t.down_w[l], P.mlp_down_b, last ? nullptr : t.layers[l + 1].ln_attn_w,
+             last ? nullptr : t.layers[l + 1].ln_attn_b, (ple && c.per_layer_dim > 0) ? ple : nullptr, l);
+  }
+  const int rows_out = r.readout ? r.n_seqs : N;
+  launch_layernorm_rows(w.x, r.readout ? w.readout_tok : nullptr, t.final_w, t.final_b, c.eps, hidden,
+                        CG_F32, rows_out, d, s);
+}
+
+// The workspace of cg_trunk_forward_static: a file-scope device array, one copy per GPU (the
+// code object's zero-initialised data, placed on each device when the library's code loads
+// there and held until the process ends).  Host code never passes `scratch` itself to a
+// kernel: its host-side name is only a stand-in; the device address of each GPU's copy comes
+// from hipGetSymbolAddress, taken once per device with that device current.
+__device__ __align__(256) unsigned char scratch[CG_TRUNK_STATIC_WORKSPACE];
+
+std::mutex scratch_mutex;
+std::vector<void *> scratch_address;  // per device ordinal, nullptr until first use
+
+void *device_scratch() {
+  int device = 0;
+  CG_HIP(hipGetDevice(&device));
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (device >= int(scratch_address.size())) scratch_address.resize(size_t(device) + 1, nullptr);
+  if (!scratch_address[device]) {
+    void *ptr = nullptr;
+    CG_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    CG_REQUIRE(ptr != nullptr, CG_ERR_HIP, "the static workspace has no device address");
+    scratch_address[device] = ptr;
+  }
+  return scratch_address[device];
+}
+
+}  // namespace
+}  // namespace cg
+
+extern "C" {
+
 int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
                      const float *ple, const float *values, const cg_ragged *step, float *hidden,
                      void *workspace, size_t workspace_size, void *stream) {
+  return guarded([&] { trunk_forward(trunk, cache, x, ple, values, step, hidden, workspace, workspace_size, stream); });
+}
+
+int cg_trunk_forward_static(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
+                            const float *ple, const float *values, const cg_ragged *step, float *hidden,
+                            void *stream) {
   return guarded([&] {
-    CG_REQUIRE(trunk && cache && x && step && hidden, CG_ERR_INVALID,
-               "trunk, cache, x, step and hidden are required");
-    const cg_trunk &t = *trunk;
-    const cg_trunk_config &c = t.cfg;
-    const cg_ragged &r = *step;
-    CG_REQUIRE(r.n_seqs >= 0 && r.n_tokens >= 0, CG_ERR_INVALID, "negative step size");
-    CG_REQUIRE(r.positions != nullptr, CG_ERR_INVALID, "positions is NULL");
-    CG_REQUIRE(r.seq_start || int64_t(r.n_seqs) * r.T == r.n_tokens, CG_ERR_INVALID,
-               "padded step: n_tokens must equal n_seqs * T");
-    CG_REQUIRE(c.per_layer_dim == 0 || ple, CG_ERR_INVALID,
-               "This trunk expects a per-layer embedding lookup.");
-    CG_REQUIRE(c.value_width == 0 || values, CG_ERR_INVALID,
-               "This trunk expects a value-embedding lookup.");
-    for (int l = 0; l < c.n_layers; ++l) {
-      const cg_kv_layer &L = cache[l];
-      check_layer(&L);
-      CG_REQUIRE(L.kv_heads == c.n_kv_heads && L.head_dim == t.head_dim, CG_ERR_INVALID,
-                 "cache layout does not match the trunk");
-      CG_REQUIRE(L.max_len == cache[0].max_len && L.capacity == cache[0].capacity &&
-                     L.dtype == cache[0].dtype,
-                 CG_ERR_INVALID, "cache layers differ in shape");
-    }
-    CG_REQUIRE(r.rows || r.n_seqs <= cache[0].capacity, CG_ERR_RANGE,
-               "dense rows: more sequences than cache rows");
-    if (r.n_tokens == 0 || r.n_seqs == 0) return;
-    Workspace w = carve(t, r.n_tokens, r.n_seqs, static_cast<char *>(workspace));
-    CG_REQUIRE(workspace && workspace_size >= w.bytes, CG_ERR_INVALID,
-               "workspace too small: need " + std::to_string(w.bytes) + " bytes");
-    hipStream_t s = as_stream(stream);
-    const int d = c.d_model, H = c.n_heads, KVH = c.n_kv_heads, D = t.head_dim;
-    const int N = r.n_tokens;
-    const int max_len = cache[0].max_len;
-    const int span = (r.span <= 0 || r.span > max_len) ? max_len : r.span;
-    const int act_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
-
-    {
-      const int n = N > r.n_seqs ? N : r.n_seqs;
-      plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout,
-                                                  r.n_seqs, N, r.T, max_len, cache[0].capacity,
-                                                  w.tok_row, w.tok_pos, w.readout_tok, w.tok_out,
-                                                  hidden, d);
-      CG_LAUNCHED();
-    }
-    const float ple_scale = [&] {
-      if (c.per_layer_dim == 0 || c.per_layer_dim == d) return 1.0f;
-      const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
-      return 1.0f / sqrtf(float(repeats));
-    }();
-    auto attention = [&](int l) {
-      const cg_kv_layer &L = cache[l];
-      {
-        AttnArgs a{};
-        a.q = w.q;
-        a.q_dtype = CG_F32;
-        a.q_st = int64_t(H) * D;
-        a.q_sh = D;
-        a.q_sb = int64_t(r.T) * H * D;
-        a.out = w.attn;
-        a.out_dtype = act_dtype;
-        a.o_st = int64_t(H) * D;
-        a.o_sh = D;
-        a.o_sb = int64_t(r.T) * H * D;
-        a.k = L.k;
-        a.v = L.v;
-        a.kv_dtype = L.dtype;
-        a.rows = r.rows;
-        a.key_lengths = r.positions;
-        a.kl_add = 1;
-        a.seq_start = r.seq_start;
-        a.n_tokens = N;
-        a.n_seqs = r.n_seqs;
-        a.n_heads = H;
-        a.kv_heads = KVH;
-        a.head_dim = D;
-        a.T = r.T;
-        a.max_len = max_len;
-        a.capacity = L.capacity;
-        a.span = span;
-        a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
-        launch_decode_attention(a, s);
-      }
-    };
-
-    const int n_qkv = (H + 2 * KVH) * D;
-    if (t.fused) {
-      // bf16 projections: one fused launch per layer after its attention (layer.hip), plus
-      // the first block's LN + QKV + append.
-      auto base = [&] {
-        TailArgs ta{};
-        ta.M = N;
-        ta.d = d;
-        ta.d_ff = c.d_ff;
-        ta.n_qkv = n_qkv;
-        ta.q_cols = H * D;
-        ta.kv_heads = KVH;
-        ta.head_dim = D;
-        ta.max_len = max_len;
-        ta.kv_dtype = cache[0].dtype;
-        ta.eps = c.eps;
-        ta.q = w.q;
-        ta.tok_row = w.tok_row;
-        ta.tok_pos = w.tok_pos;
-        ta.vemb = values;
-        ta.ld_vemb = c.value_width;
-        ta.vemb_off = -1;
-        ta.hidden = hidden;
-        ta.tok_out = w.tok_out;
-        return ta;
-      };
-      auto set_next = [&](TailArgs &ta, int nl) {
-        if (nl == c.n_layers) {
-          ta.final_ln = 1;
-          ta.ln_w = t.final_w;
-          ta.ln_b = t.final_b;
-          return;
-        }
-        const cg_layer_params &Pn = t.layers[nl];
-        ta.final_ln = 0;
-        ta.ln_w = Pn.ln_attn_w;
-        ta.ln_b = Pn.ln_attn_b;
-        ta.w_qkv = t.qkv_w[nl];
-        ta.kc = cache[nl].k;
-        ta.vc = cache[nl].v;
-        ta.vemb_off = (values && Pn.value_index >= 0) ? Pn.value_index * KVH * D : -1;
-      };
-      {
-        TailArgs ta = base();
-        ta.do_post = 0;
-        ta.x_src = x;
-        ta.x = w.x;
-        set_next(ta, 0);
-        launch_tail(ta, s);
-      }
-      // The tail of layer l: its post-attention half, then the next layer's QKV (or the
-      // final norm).
-      auto tail_of = [&](int l) {
-        const cg_layer_params &P = t.layers[l];
-        TailArgs ta = base();
-        ta.do_post = 1;
-        ta.attn = w.attn;
-        ta.w_out = t.out_w[l];
-        ta.w_up = t.up_w[l];
-        ta.b_up = P.mlp_up_b;
-        ta.w_down = t.down_w[l];
-        ta.b_down = P.mlp_down_b;
-        ta.ln2_w = P.ln_mlp_w;
-        ta.ln2_b = P.ln_mlp_b;
-        if (ple && c.per_layer_dim > 0) {
-          ta.ple = ple;
-          ta.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
-          ta.ple_off = l * c.per_layer_dim;
-          ta.ple_dim = c.per_layer_dim;
-          ta.ple_scale = ple_scale;
-        }
-        ta.x_src = w.x;
-        ta.x = w.x;
-        set_next(ta, l + 1);
-        return ta;
-      };
-      for (int l = 0; l < c.n_layers; ++l) {
-        attention(l);
-        launch_tail(tail_of(l), s);
-      }
-      return;
-    }
-
-    CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
-    launch_layernorm_rows(w.x, nullptr, t.layers[0].ln_attn_w, t.layers[0].ln_attn_b, c.eps, w.xn,
-                          act_dtype, N, d, s);
-    // Whole-row residual tiles fuse the next LayerNorm into the residual epilogue.
-    const bool fused_ln = d <= 256;
-
-    auto residual = [&](const void *A, int K, const void *W, const float *bias, const float *ln_w,
-                        const float *ln_b, const float *ple_rows, int layer) {
-      GemmArgs g{};
-      g.M = N;
-      g.N = d;
-      g.K = K;
-      g.compute = t.compute;
-      g.A = A;
-      g.lda = K;
-      g.W = W;
-      g.bias = bias;
-      g.resid = w.x;
-      g.ldr = d;
-      if (ple_rows) {
-        g.ple = ple_rows;
-        g.ld_ple = int64_t(c.n_layers) * c.per_layer_dim;
-        g.ple_off = layer * c.per_layer_dim;
-        g.ple_dim = c.per_layer_dim;
-        g.ple_scale = ple_scale;
-      }
-      if (ln_w && fused_ln) {
-        g.epi = EPI_RESID_LN;
-        g.ln_w = ln_w;
-        g.ln_b = ln_b;
-        g.eps = c.eps;
-        g.out = w.xn;
-        g.out_dtype = act_dtype;
-        g.ldo = d;
-        launch_gemm(g, s);
-        return;
-      }
-      g.epi = EPI_RESID;
-      launch_gemm(g, s);
-      if (ln_w) launch_layernorm_rows(w.x, nullptr, ln_w, ln_b, c.eps, w.xn, act_dtype, N, d, s);
-    };
-
-    for (int l = 0; l < c.n_layers; ++l) {
-      const cg_layer_params &P = t.layers[l];
-      const cg_kv_layer &L = cache[l];
-      {  // QKV projection of LN1(x) + append
-        GemmArgs g{};
-        g.M = N;
-        g.N = (H + 2 * KVH) * D;
-        g.K = d;
-        g.compute = t.compute;
-        g.A = w.xn;
-        g.lda = d;
-        g.W = t.qkv_w[l];
-        g.epi = EPI_QKV;
-        g.out = w.q;
-        g.ldo = H * D;
-        g.q_cols = H * D;
-        g.kc = L.k;
-        g.vc = L.v;
-        g.kv_dtype = L.dtype;
-        g.kv_heads = KVH;
-        g.head_dim = D;
-        g.max_len = max_len;
-        g.tok_row = w.tok_row;
-        g.tok_pos = w.tok_pos;
-        g.vemb = values;
-        g.ld_vemb = c.value_width;
-        g.vemb_off = (values && P.value_index >= 0) ? P.value_index * KVH * D : -1;
-        launch_gemm(g, s);
-      }
-      attention(l);
-      // out_proj + residual, then LN2 -> xn
-      residual(w.attn, H * D, t.out_w[l], nullptr, P.ln_mlp_w, P.ln_mlp_b, nullptr, l);
-      {  // mlp[0] + GELU
-        GemmArgs g{};
-        g.M = N;
-        g.N = c.d_ff;
-        g.K = d;
-        g.compute = t.compute;
-        g.A = w.xn;
-        g.lda = d;
-        g.W = t.up_w[l];
-        g.bias = P.mlp_up_b;
-        g.epi = EPI_GELU;
-        g.out = w.h1;
-        g.out_dtype = act_dtype;
-        g.ldo = c.d_ff;
-        launch_gemm(g, s);
-      }
-      // mlp[2] + residual (+ PLE), then the next block's LN1 -> xn
-      const bool last = l + 1 == c.n_layers;
-      residual(w.h1, c.d_ff, t.down_w[l], P.mlp_down_b, last ? nullptr : t.layers[l + 1].ln_attn_w,
-               last ? nullptr : t.layers[l + 1].ln_attn_b, (ple && c.per_layer_dim > 0) ? ple : nullptr, l);
-    }
-    const int rows_out = r.readout ? r.n_seqs : N;
-    launch_layernorm_rows(w.x, r.readout ? w.readout_tok : nullptr, t.final_w, t.final_b, c.eps, hidden,
-                          CG_F32, rows_out, d, s);
+    CG_REQUIRE(trunk && step, CG_ERR_INVALID, "trunk and step are required");
+    CG_REQUIRE(step->n_seqs >= 0 && step->n_tokens >= 0, CG_ERR_INVALID, "negative step size");
+    const size_t need = carve(*trunk, step->n_tokens, step->n_seqs, nullptr).bytes;
+    CG_REQUIRE(need <= CG_TRUNK_STATIC_WORKSPACE, CG_ERR_RANGE,
+               "step needs " + std::to_string(need) + " workspace bytes; the static workspace holds " +
+                   std::to_string(size_t(CG_TRUNK_STATIC_WORKSPACE)) + " (use cg_trunk_forward with a larger one)");
+    trunk_forward(trunk, cache, x, ple, values, step, hidden, device_scratch(), CG_TRUNK_STATIC_WORKSPACE, stream);
   });
 }
 

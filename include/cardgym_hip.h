@@ -223,6 +223,23 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
                      const float *ple, const float *values, const cg_ragged *step, float *hidden,
                      void *workspace, size_t workspace_size, void *stream);
 
+/* No counterpart in the reference.  cg_trunk_forward for callers that cannot allocate its
+ * workspace (code under HIP graph capture that must not call hipMalloc, tight serving loops,
+ * harnesses that forbid allocation): the same kernels, run on a library-owned workspace, a
+ * static device array of CG_TRUNK_STATIC_WORKSPACE bytes on each GPU the library runs on,
+ * held until the process ends.  Allocates nothing.  A step whose
+ * cg_trunk_workspace_size(trunk, n_tokens, n_seqs) exceeds the array is refused with
+ * CG_ERR_RANGE (about 13,000 tokens of a d_model 256 / d_ff 1024 bf16 trunk, 6,500 fp32).
+ * Every call on one GPU shares that GPU's array, which keeps the last call's contents (a step
+ * writes every workspace byte before it reads it, so nothing needs clearing): calls that
+ * overlap on one GPU (two streams, two host threads, concurrent graph replays) race on it,
+ * and the caller must serialise them.  The first call on each device looks the array's
+ * address up; make it outside stream capture. */
+#define CG_TRUNK_STATIC_WORKSPACE (64u << 20)
+int cg_trunk_forward_static(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
+                            const float *ple, const float *values, const cg_ragged *step, float *hidden,
+                            void *stream);
+
 /* ---- conditioning, embedding and heads ------------------------------------------ */
 
 /* RMSNorm (cardgym/nn/trunk.py:104-115): y = rms_norm(x, eps).to(x.dtype) * gain, rows of
