@@ -38,7 +38,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "decode_attention_cfg3_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_attention_traffic.json"
 
 
 def log(message: str) -> None:
@@ -50,11 +50,12 @@ def parse() -> argparse.Namespace:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=256)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="cfg3", choices=["cfg3", "cfg4"])
+    p.add_argument("--workload", default="cfg3", choices=["cfg3", "cfg4", "cfg5"])
     p.add_argument("--cpu-games", type=int, default=1024)
     p.add_argument("--cpu-steps", type=int, default=4)
     p.add_argument("--ref-steps", type=int, default=8)
     p.add_argument("--no-baselines", action="store_true")
+    p.add_argument("--no-workloads", action="store_true", help="skip the config 4 / 5 lines")
     p.add_argument(
         "--traffic-probe", action="store_true",
         help="run only the decode-attention launches of the timed steps and a 256 MiB calibration copy "
@@ -89,8 +90,15 @@ class Bench:
         plans = [driver.step() for _ in range(total)]
         self.plans = plans
         dev = self.device
-        # Every step's descriptors, resident before timing.
-        self.tokens = torch.from_numpy(np.stack([p.tokens for p in plans])).to(dev)
+        self.chunks = w.mode == "chunks"
+        # Every step's descriptors, resident before timing.  Packed chunks differ in token
+        # count from step to step: one tensor per step (and one graph per step).
+        if self.chunks:
+            self.tokens = [torch.from_numpy(p.tokens).to(dev) for p in plans]
+            self.seq_starts = [torch.from_numpy(p.seq_start).to(dev) for p in plans]
+            self.readouts = [torch.from_numpy(p.readout).to(dev) for p in plans]
+        else:
+            self.tokens = torch.from_numpy(np.stack([p.tokens for p in plans])).to(dev)
         self.positions_all = torch.from_numpy(np.stack([p.positions for p in plans])).to(dev)
         self.rows_all = torch.from_numpy(np.stack([p.rows for p in plans])).to(dev)
         games = w.games
@@ -106,47 +114,85 @@ class Bench:
         self.readout = torch.zeros(games, dtype=torch.int64, device=dev)
         self.gathered = w.mode == "continuous"
         self.graph = None
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
-    def body(self):
+    def body(self, step: int = 0):
         with torch.autocast("cuda", dtype=torch.bfloat16, enabled=self.workload.precision == "bf16"):
-            hidden = self.model.forward_ragged(
-                self.tok_buf, self.pos_buf, self.cache, self.readout, rows=self.rows_buf if self.gathered else None
-            )
+            if self.chunks:
+                hidden = self.model.forward_packed(self.tokens[step][:, None], self.seq_starts[step], self.pos_buf,
+                                                   self.cache, self.readouts[step])
+            else:
+                hidden = self.model.forward_ragged(
+                    self.tok_buf, self.pos_buf, self.cache, self.readout,
+                    rows=self.rows_buf if self.gathered else None,
+                )
             return self.model.heads(hidden)
 
     def load(self, step: int) -> None:
-        self.tok_buf.view(-1).copy_(self.tokens[step], non_blocking=True)
+        if not self.chunks:
+            self.tok_buf.view(-1).copy_(self.tokens[step], non_blocking=True)
         self.pos_buf.copy_(self.positions_all[step], non_blocking=True)
         if self.gathered:
             self.rows_buf.copy_(self.rows_all[step], non_blocking=True)
 
-    def capture(self) -> None:
+    def capture(self, steps=(0,)) -> None:
+        """One graph of the whole step (every step shares it), or for packed chunks one per
+        step in `steps` (their token counts differ), sharing one memory pool."""
+
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side), torch.no_grad():
-            self.body()
+            self.body(steps[0])
         torch.cuda.current_stream().wait_stream(side)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph), torch.no_grad():
-            self.outputs = self.body()
+        if not self.chunks:
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph), torch.no_grad():
+                self.outputs = self.body()
+            return
+        pool = torch.cuda.graph_pool_handle()
+        for step in steps:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=pool), torch.no_grad():
+                self.outputs = self.body(step)
+            self.graphs[step] = graph
 
     def step(self, step: int) -> None:
         self.load(step)
-        self.graph.replay()
+        (self.graphs[step] if self.chunks else self.graph).replay()
+
+    def tokens_in(self, first: int, count: int) -> int:
+        return sum(self.plans[s].n_tokens for s in range(first, first + count))
+
+
+def traffic_record(workload: str, steps: int, warmup: int, bytes_per_launch: float):
+    """HBM bytes per decode-attention launch from the committed counter passes
+    (FETCH_SIZE / WRITE_SIZE, calibrated on a plain copy) for this exact run: same workload,
+    step count and warm-up, and the same algorithmic bytes."""
+
+    if not TRAFFIC_FILE.exists():
+        return None
+    for record in json.loads(TRAFFIC_FILE.read_text()).get("records", []):
+        if (record.get("workload"), record.get("steps"), record.get("warmup")) != (workload, steps, warmup):
+            continue
+        if abs(record.get("algorithmic_bytes_per_launch", 0) - bytes_per_launch) <= 0.001 * bytes_per_launch:
+            return record.get("bytes_per_launch")
+    return None
 
 
 def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     """Average duration and algorithmic bytes of the decode-attention launches of steps
-    first..first+count-1, replayed on their own with HIP events on the launch stream."""
+    first..first+count-1, replayed on their own with HIP events on the launch stream
+    (packed chunks through the packed entry point, as the step launches them)."""
 
-    from card_playing_gym_amd.nn.decode import attention_into
+    from card_playing_gym_amd.nn.decode import attention_into, attention_packed_into
     from card_playing_gym_amd.synthetic import kv_bytes
 
     cfg = bench.config
     dev = bench.device
     games, H, D = bench.games, cfg.n_heads, cfg.head_dim
-    q = torch.randn((games, H, 1, D), device=dev, dtype=torch.float32)
-    out = torch.empty((games, H, 1, D), device=dev, dtype=torch.bfloat16)
+    tokens = max(p.n_tokens for p in bench.plans[first:first + count])
+    q = torch.randn((tokens, H, D), device=dev, dtype=torch.float32)
+    out = torch.empty((tokens, H, D), device=dev, dtype=torch.bfloat16)
     key_lengths = torch.empty(games, dtype=torch.int64, device=dev)
     rows = torch.empty(games, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream()
@@ -155,37 +201,42 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     total_bytes = 0
     itemsize = bench.cache.dtype.itemsize
     for i in range(count):
-        plan = bench.plans[first + i]
-        key_lengths.copy_(bench.positions_all[first + i] + 1)
-        rows.copy_(bench.rows_all[first + i])
-        starts[i].record(stream)
-        for layer in range(cfg.n_layers):
-            attention_into(out, q, bench.cache.k[layer], bench.cache.v[layer],
-                           rows if bench.gathered else None, key_lengths, bench.max_len, D ** -0.5)
+        step = first + i
+        plan = bench.plans[step]
+        rows.copy_(bench.rows_all[step])
+        if bench.chunks:
+            key_lengths.copy_(bench.positions_all[step])
+            n = plan.n_tokens
+            starts[i].record(stream)
+            for layer in range(cfg.n_layers):
+                attention_packed_into(out[:n], q[:n], bench.cache.k[layer], bench.cache.v[layer], rows, key_lengths,
+                                      bench.seq_starts[step], bench.max_len, D ** -0.5)
+        else:
+            key_lengths.copy_(bench.positions_all[step] + 1)
+            starts[i].record(stream)
+            for layer in range(cfg.n_layers):
+                attention_into(out.view(games, H, 1, D), q.view(games, H, 1, D), bench.cache.k[layer],
+                               bench.cache.v[layer], rows if bench.gathered else None, key_lengths, bench.max_len,
+                               D ** -0.5)
         ends[i].record(stream)
         kv = kv_bytes(plan, cfg.n_layers, cfg.n_kv_heads, D, itemsize)
-        total_bytes += kv + cfg.n_layers * games * H * D * (4 + 2)  # + q read (fp32) + out write (bf16)
+        total_bytes += kv + cfg.n_layers * plan.n_tokens * H * D * (4 + 2)  # + q read (fp32) + out write (bf16)
     torch.cuda.synchronize()
     ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends))
     launches = count * cfg.n_layers
     avg_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
     achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
-    # HBM bytes per launch from the committed counter passes (FETCH_SIZE / WRITE_SIZE,
-    # calibrated on a plain copy), valid when they were taken on this same workload.
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        recorded = json.loads(TRAFFIC_FILE.read_text())
-        if abs(recorded.get("algorithmic_bytes_per_launch", 0) - bytes_per_launch) <= 0.01 * bytes_per_launch:
-            traffic = recorded.get("bytes_per_launch")
     return {
-        "kernel": "decode_attention_tr_kernel<bf16,32,1>",
+        # Query tiles of 16 per (row, KV head) unit: one for a decode token's 4 heads, four
+        # for chunks of up to 16 tokens.
+        "kernel": "decode_attention_tr_kernel<bf16,32,%d>" % (4 if bench.chunks else 1),
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": traffic,
+        "traffic": traffic_record(bench.workload.name, count, first, bytes_per_launch),
         "avg_launch_us": round(avg_us, 2),
         "algorithmic_bytes_per_launch": int(bytes_per_launch),
         "launches": launches,
@@ -620,11 +671,15 @@ def cpu_baseline(name: str, games: int, steps: int, first: int, horizon: int) ->
     }
 
 
-def reference_gpu(bench: Bench, steps: int, first: int) -> dict:
-    """The restated reference path on the MI355X, eager and captured in a graph, on steps
-    first .. first + steps - 1 (the middle of the timed range).  span is what the
-    reference's collector passes: the longest row after the append, rounded up to 32
-    (cardgym/rl/continuous.py:338), one value for the sampled steps (one graph shape)."""
+def reference_gpu(bench: Bench, steps: int, first: int, compiled: bool = True) -> dict:
+    """The restated reference path on the MI355X on steps first .. first + steps - 1 (the
+    middle of the timed range), three ways: eager; captured in one graph; and as the
+    reference's CUDA rollout runs it (cardgym/rl/graphs.py:66-151 with cardgym/nn/compile.py:
+    26-44): torch.compile(dynamic=True), warmed up on a side stream, then captured and
+    replayed.  span is what the reference's collector passes: the longest row after the
+    append, rounded up to 32 (cardgym/rl/continuous.py:338), one value for the sampled steps
+    (one graph shape).  Packed chunks run as the reference's collector pads them: repeat-last
+    to the longest chunk (continuous.py:324-338)."""
 
     from oracle.reference_path import RefCache, RefSynthetic, ref_config_of
 
@@ -634,54 +689,175 @@ def reference_gpu(bench: Bench, steps: int, first: int) -> dict:
     state = {k: v.detach() for k, v in bench.model.state_dict().items()}
     ref = RefSynthetic(state, ref_config_of(cfg), w.precision)
     cache = RefCache(cfg.n_layers, cfg.n_kv_heads, cfg.head_dim, w.capacity(), bench.max_len, w.kv_dtype, device=dev)
-    tok = torch.zeros((bench.games, 1, 1), dtype=torch.int64, device=dev)
+    sampled = range(first, first + steps)
+    run = max(int(np.diff(bench.plans[s].seq_start).max()) for s in sampled)
+    tok = torch.zeros((bench.games, run, 1), dtype=torch.int64, device=dev)
     pos = torch.zeros(bench.games, dtype=torch.int64, device=dev)
     rows = torch.arange(bench.games, dtype=torch.int64, device=dev)
-    last = max(int(bench.plans[s].positions.max()) for s in range(first, first + steps))
+    readout = torch.zeros(bench.games, dtype=torch.int64, device=dev)
+    last = max(int((bench.plans[s].positions + np.diff(bench.plans[s].seq_start)).max()) - 1 for s in sampled)
     span = min(int(-(-(last + 1) // 32) * 32), bench.max_len)
+    padded = {}
+    for s in sampled:
+        plan = bench.plans[s]
+        counts = np.diff(plan.seq_start)
+        t = np.zeros((bench.games, run), dtype=np.int64)
+        for b in range(bench.games):
+            chunk = plan.tokens[plan.seq_start[b]:plan.seq_start[b + 1]]
+            t[b, :chunk.size] = chunk
+            t[b, chunk.size:] = chunk[-1]
+        padded[s] = (torch.from_numpy(t).to(dev), torch.from_numpy(counts - 1).to(dev))
+    gathered = bench.gathered
+    game_tokens = bench.tokens_in(first, steps)
 
-    def body():
-        hidden = ref.forward_ragged(tok, pos, cache, bench.readout, span=span, rows=rows if bench.gathered else None)
-        return ref.heads(hidden)
+    def body(tok, pos, rows, readout):
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=False):
+            hidden = ref.forward_ragged(tok, pos, cache, readout, span=span, rows=rows if gathered else None)
+            return ref.heads(hidden)
 
     def load(step):
-        tok.view(-1).copy_(bench.tokens[step])
+        tok.copy_(padded[step][0][..., None])
+        readout.copy_(padded[step][1])
         pos.copy_(bench.positions_all[step])
         rows.copy_(bench.rows_all[step])
+
+    def graphed(fn) -> float:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn(tok, pos, rows, readout)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn(tok, pos, rows, readout)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in sampled:
+            load(s)
+            graph.replay()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
 
     result = {}
     with torch.no_grad():
         load(first)
-        body()
+        body(tok, pos, rows, readout)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for s in range(first, first + steps):
+        for s in sampled:
             load(s)
-            body()
+            body(tok, pos, rows, readout)
         torch.cuda.synchronize()
-        eager = (time.perf_counter() - t0) / steps
-        result["eager_game_tokens_per_s"] = round(bench.games / eager, 1)
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            body()
-        torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            body()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for s in range(first, first + steps):
-            load(s)
-            graph.replay()
-        torch.cuda.synchronize()
-        graphed = (time.perf_counter() - t0) / steps
-        result["graph_game_tokens_per_s"] = round(bench.games / graphed, 1)
+        result["eager_game_tokens_per_s"] = round(game_tokens / (time.perf_counter() - t0), 1)
+        result["graph_game_tokens_per_s"] = round(game_tokens / graphed(body), 1)
+        if compiled:
+            from torch import _dynamo
+            from torch._inductor import config as inductor_config
+
+            # The reference's settings (cardgym/nn/compile.py:35-44): compile in this process.
+            inductor_config.compile_threads = 1
+            _dynamo.config.cache_size_limit = max(_dynamo.config.cache_size_limit, 64)
+            _dynamo.reset()
+            try:
+                load(first)
+                t0 = time.perf_counter()
+                fn = torch.compile(body, dynamic=True)
+                fn(tok, pos, rows, readout)
+                torch.cuda.synchronize()
+                result["compile_s"] = round(time.perf_counter() - t0, 1)
+                result["compiled_graph_game_tokens_per_s"] = round(game_tokens / graphed(fn), 1)
+            except Exception as exc:  # recorded, not hidden: the leg stays in the line
+                result["compiled_graph_error"] = f"{type(exc).__name__}: {str(exc)[:300]}"
+            _dynamo.reset()
         result["span"] = span
         result["steps"] = f"{first}..{first + steps - 1}"
     del cache
     torch.cuda.empty_cache()
     return result
+
+
+def best_reference(result: dict) -> float:
+    """The fastest of the reference path's legs (eager, graph, compiled + graph)."""
+
+    legs = ("eager_game_tokens_per_s", "graph_game_tokens_per_s", "compiled_graph_game_tokens_per_s")
+    return max(result[k] for k in legs if k in result)
+
+
+def projections(bench: Bench, step_s: float, attention: dict, n_tokens: float) -> dict:
+    """MFMA throughput of the step's bf16 projections (QKV, out, MLP up / down; the fused
+    layer kernels), from the whole step's time less its attention launches: the rest also
+    holds the embedding, plan, final norm and heads launches (tens of microseconds), so this
+    bounds the projections' rate from below."""
+
+    from card_playing_gym_amd.synthetic import projection_flops
+
+    flops = projection_flops(bench.config, 1) * n_tokens
+    rest = step_s - attention["avg_launch_us"] * 1e-6 * bench.config.n_layers
+    tflops = flops / rest / 1e12
+    return {"flops_per_step": int(flops), "step_less_attention_us": round(rest * 1e6, 1),
+            "tflops_lower_bound": round(tflops, 1), "peak_tflops": 2500.0,
+            "frac_lower_bound": round(tflops / 2500.0, 4)}
+
+
+def time_steps(bench: Bench, first: int, count: int) -> float:
+    """Wall seconds of `count` graph-replayed steps from `first`, device-synchronised on
+    both sides (and the HIP-event span, whichever is longer)."""
+
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for s in range(first, first + count):
+        bench.step(s)
+    end.record()
+    torch.cuda.synchronize()
+    return max(time.perf_counter() - t0, start.elapsed_time(end) / 1e3)
+
+
+def workload_line(name: str, steps: int, warmup: int, ref_steps: int, with_reference: bool) -> dict:
+    """Config 4 or 5 beside the headline: game-tokens/s over `steps` graph-replayed steps after
+    `warmup`, the attention roofline of the same steps, the projections' rate, and the
+    restated reference path on the same GPU (eager, graph, compiled + graph)."""
+
+    bench = Bench(name, steps, warmup)
+    w = bench.workload
+    with torch.no_grad():
+        bench.load(0)
+        bench.capture(tuple(range(warmup + steps)) if bench.chunks else (0,))
+        for s in range(warmup):
+            bench.step(s)
+        elapsed = time_steps(bench, warmup, steps)
+    game_tokens = bench.tokens_in(warmup, steps)
+    out = {
+        "workload": f"{w.name}: {w.description}",
+        "game_tokens_per_s": round(game_tokens / elapsed, 1),
+        "ms_per_step": round(elapsed / steps * 1e3, 4),
+        "tokens_per_step": round(game_tokens / steps, 1),
+        "steps": steps,
+        "warmup": warmup,
+        "max_len": bench.max_len,
+    }
+    if w.mode == "continuous":
+        out["games_ended_per_step"] = round(sum(int((bench.plans[s + 1].positions == 0).sum())
+                                                for s in range(warmup, warmup + steps - 1)) / (steps - 1), 1)
+    with torch.no_grad():
+        out["roofline"] = attention_roofline(bench, warmup, steps)
+    out["projections"] = projections(bench, elapsed / steps, out["roofline"], game_tokens / steps)
+    if with_reference:
+        middle = warmup + steps // 2 - ref_steps // 2
+        ref = reference_gpu(bench, ref_steps, middle)
+        # The reference's rate on its sampled steps, ours on the same steps.
+        with torch.no_grad():
+            ours = bench.tokens_in(middle, ref_steps) / time_steps(bench, middle, ref_steps)
+        ref["ours_same_steps_game_tokens_per_s"] = round(ours, 1)
+        ref["speedup_vs_best"] = round(ours / best_reference(ref), 2)
+        out["reference_gpu"] = ref
+    bench.graphs.clear()
+    bench.graph = None
+    del bench
+    torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -723,7 +899,7 @@ def main() -> int:
         return 0
     with torch.no_grad():
         bench.load(0)
-        bench.capture()
+        bench.capture(tuple(range(args.warmup + args.steps)) if bench.chunks else (0,))
         torch.cuda.synchronize()
         for s in range(args.warmup):
             bench.step(s)
@@ -739,20 +915,27 @@ def main() -> int:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     elapsed = max(wall, start.elapsed_time(end) / 1e3)
-    tokens = bench.games * args.steps
+    tokens = bench.tokens_in(args.warmup, args.steps)
     value = tokens / elapsed
     log(f"bench: {value:,.0f} game-tokens/s, {elapsed / args.steps * 1e3:.3f} ms/step")
-    roofline = attention_roofline(bench, args.warmup, args.steps)
+    with torch.no_grad():
+        roofline = attention_roofline(bench, args.warmup, args.steps)
     log(f"bench: decode attention {roofline['achieved']:.0f} GB/s ({roofline['frac']:.1%} of peak), "
         f"{roofline['avg_launch_us']} us/launch")
-    extra = {"sampling": sampling_time(bench)}
+    extra = {"projections": projections(bench, elapsed / args.steps, roofline, tokens / args.steps)}
+    log(f"bench: projections {extra['projections']}")
+    extra["sampling"] = sampling_time(bench)
     log(f"bench: device sampling {extra['sampling']}")
     cpu = None
+    middle = args.warmup + args.steps // 2 - args.ref_steps // 2
     if not args.no_baselines:
-        middle = args.warmup + args.steps // 2 - args.ref_steps // 2
-        extra["reference_gpu"] = reference_gpu(bench, args.ref_steps, middle)
-        best = max(extra["reference_gpu"]["eager_game_tokens_per_s"], extra["reference_gpu"]["graph_game_tokens_per_s"])
-        extra["reference_gpu"]["speedup_vs_best"] = round(value / best, 2)
+        ref = reference_gpu(bench, args.ref_steps, middle)
+        with torch.no_grad():
+            ref["ours_same_steps_game_tokens_per_s"] = round(
+                bench.tokens_in(middle, args.ref_steps) / time_steps(bench, middle, args.ref_steps), 1)
+        ref["speedup_vs_best"] = round(value / best_reference(ref), 2)
+        ref["speedup_same_steps_vs_best"] = round(ref["ours_same_steps_game_tokens_per_s"] / best_reference(ref), 2)
+        extra["reference_gpu"] = ref
         log(f"bench: reference path on the GPU {extra['reference_gpu']}")
     # These rewrite cache rows: after everything that reads them.
     extra["compaction"] = compaction_time(bench)
@@ -765,9 +948,17 @@ def main() -> int:
     log(f"bench: piquet wave {extra['piquet_wave']}")
     extra["train_step"] = train_step_time(bench, with_reference=not args.no_baselines)
     log(f"bench: training step {extra['train_step']}")
+    bench.graph = None
+    del bench.cache
+    torch.cuda.empty_cache()
+    if not args.no_workloads:
+        # Configs 4 and 5 at full size, each beside the reference path on the same GPU.
+        for name in ("cfg4", "cfg5"):
+            if name == args.workload:
+                continue
+            extra[name] = workload_line(name, args.steps, args.warmup, args.ref_steps, not args.no_baselines)
+            log(f"bench: {name} {extra[name]}")
     if not args.no_baselines:
-        del bench.cache
-        torch.cuda.empty_cache()
         cpu = cpu_baseline(args.workload, args.cpu_games, args.cpu_steps, middle, args.warmup + args.steps)
         log(f"bench: cpu baseline {cpu}")
     result = {

@@ -65,6 +65,39 @@ def attention_into(
     )
 
 
+def attention_packed_into(
+    out: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    rows: torch.Tensor | None,
+    positions: torch.Tensor,
+    seq_start: torch.Tensor,
+    span: int,
+    scale: float,
+) -> None:
+    """Packed chunks: q [N, H, D] (unit last stride), sequence b owning tokens
+    ``seq_start[b] .. seq_start[b+1]-1`` (packing.py:36-40 bounds) at cache row ``rows[b]``;
+    its token t sees keys below ``positions[b] + 1 + t`` (its prefix and its own chunk,
+    already in the pool).  Writes out [N, H, D] (contiguous)."""
+
+    import ctypes
+
+    require_device(q, k, v, out)
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    index = lambda t: t.to(torch.int64).contiguous()  # noqa: E731
+    rows = None if rows is None else index(rows)
+    positions, seq_start = index(positions), index(seq_start)
+    layer = _layer(k, v)
+    nat.call(
+        "cg_decode_attention_packed", q.data_ptr(), dtype_code(q.dtype), q.stride(0), q.stride(1),
+        ctypes.byref(layer), None if rows is None else rows.data_ptr(), positions.data_ptr(), seq_start.data_ptr(),
+        positions.numel(), q.shape[0], q.shape[1], int(span), float(scale), out.data_ptr(), dtype_code(out.dtype),
+        stream_handle(q.device),
+    )
+
+
 @torch.library.custom_op("cardgym_hip::decode_attention", mutates_args=())
 def _decode_attention(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, rows: torch.Tensor, lengths: torch.Tensor, span: int, scale: float

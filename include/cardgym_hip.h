@@ -140,6 +140,20 @@ int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_
                         int32_t B, int32_t n_heads, int32_t T, int32_t span, float scale, void *out,
                         int32_t out_dtype, void *stream);
 
+/* The packed-row form of cg_decode_attention, as the trunk step launches it: the
+ * chunks of cardgym/nn/packing.py:36-40 ([start, end) bounds) instead of a padded run, with
+ * the visibility rule of DecoderBlock.forward_ragged / _grouped_attention
+ * (cardgym/nn/trunk.py:183-256, key_lengths = positions + 1, trunk.py:426):
+ *   q       [n_tokens, n_heads, head_dim], token stride q_st, head stride q_sh, type q_dtype
+ *   sequence b owns tokens seq_start[b] .. seq_start[b+1]-1 (int64 [n_seqs + 1]) and cache
+ *   row rows[b] (NULL = b); its token t sees keys < min(positions[b] + 1 + t, span), i.e. its
+ *   cached prefix and its own chunk up to itself (already written to the pool)
+ *   out     [n_tokens, n_heads, head_dim] contiguous, type out_dtype */
+int cg_decode_attention_packed(const void *q, int32_t q_dtype, int64_t q_st, int64_t q_sh,
+                               const cg_kv_layer *layer, const int64_t *rows, const int64_t *positions,
+                               const int64_t *seq_start, int32_t n_seqs, int32_t n_tokens, int32_t n_heads,
+                               int32_t span, float scale, void *out, int32_t out_dtype, void *stream);
+
 /* ---- fused trunk ------------------------------------------------------------------ */
 
 /* TrunkConfig (cardgym/nn/trunk.py:39-91). */

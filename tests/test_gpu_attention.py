@@ -130,3 +130,42 @@ def test_empty_inputs_are_no_ops(device):
     out = decode_attention(torch.zeros(0, 8, 1, 32, device=device), k, k, torch.zeros(0, dtype=torch.int64, device=device),
                            torch.zeros(0, dtype=torch.int64, device=device), 8, 1.0)
     assert out.shape == (0, 8, 1, 32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("D,heads,kv_heads", [(32, 8, 2), (64, 4, 1), (16, 4, 2)])
+def test_packed_decode_attention_matches_oracle(device, dtype, D, heads, kv_heads):
+    """cg_decode_attention_packed: chunks of 1-16 tokens packed back to back (no padding),
+    each token t of a chunk seeing its row's prefix plus its chunk up to itself; against the
+    oracle's grouped attention on each chunk padded to 16 with its own key lengths."""
+
+    from card_playing_gym_amd.nn.decode import attention_packed_into
+
+    gen = torch.Generator().manual_seed(D * 7 + heads)
+    capacity, max_len, B = 40, 300, 33
+    k_cache = torch.randn(capacity, kv_heads, max_len, D, generator=gen).to(dtype)
+    v_cache = torch.randn(capacity, kv_heads, max_len, D, generator=gen).to(dtype)
+    rows = torch.randperm(capacity, generator=gen)[:B]
+    counts = torch.randint(1, 17, (B,), generator=gen)
+    positions = torch.randint(0, max_len - 17, (B,), generator=gen)
+    positions[0], counts[0] = 0, 16  # a fresh game's first chunk: its own keys only
+    positions[1], counts[1] = max_len - 17, 16  # the pool's end
+    seq_start = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(counts, 0)])
+    n = int(seq_start[-1])
+    q = torch.randn(n, heads, D, generator=gen)
+    out = torch.empty(n, heads, D, dtype=dtype, device=device)
+    span = int((positions + counts).max())
+    attention_packed_into(out, q.to(device), k_cache.to(device), v_cache.to(device), rows.to(device),
+                          positions.to(device), seq_start.to(device), span, 1.0 / math.sqrt(D))
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    # The oracle: each chunk as a padded run of 16 queries (repeat-last), key_lengths = positions + 1.
+    padded = torch.zeros(B, heads, 16, D)
+    for b in range(B):
+        chunk = q[seq_start[b] : seq_start[b + 1]].transpose(0, 1)  # [heads, c, D]
+        padded[b, :, : counts[b]] = chunk
+        padded[b, :, counts[b] :] = chunk[:, -1:]
+    exact = oracle(padded, k_cache, v_cache, rows, positions + 1, span, heads, kv_heads, literal=False)
+    want = torch.cat([exact[b, :, : counts[b]].transpose(0, 1) for b in range(B)])
+    err = (got - want).abs().max().item()
+    assert err <= TOL[dtype], f"vs float64: {err}"
