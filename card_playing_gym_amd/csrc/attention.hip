@@ -556,10 +556,13 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
 #ifndef TR_WAVES_PER_EU
 #define TR_WAVES_PER_EU 4
 #endif
-template <typename TKV, int D, int NQT, int SPLIT, int KT, int DEPTH>
+// QRAW: the queries are stored in the cache type (16-byte aligned rows); they load as they
+// are and the softmax scale multiplies the fp32 scores.  Otherwise any query type is read,
+// scaled and rounded to the cache type.
+template <typename TKV, int D, int NQT, int SPLIT, int KT, int DEPTH, bool QRAW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NQT == 1 && D == 32 ? TR_WAVES_PER_EU : 1)))
 void decode_attention_tr_kernel(AttnArgs a) {
-  static_assert(SPLIT == 1 || SPLIT == 4, "a block holds 4 / SPLIT whole units");
+  static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "a block holds 4 / SPLIT whole units");
   static_assert(KT % 32 == 0, "key tiles are whole 32-key MFMA steps");
   constexpr int NJ = KT / 16;     // 16-key score tiles per key tile
   constexpr int DK = D / 32;      // 32-dim slices of a key (S^T k-steps)
@@ -575,9 +578,14 @@ void decode_attention_tr_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int unit = blockIdx.x * (4 / SPLIT) + wave / SPLIT;
   const int part = wave % SPLIT;
-  // A unit's waves all leave together (same unit), so block barriers below stay matched.
-  if (unit >= a.n_seqs * a.kv_heads) return;
-  const int b = unit / a.kv_heads, h = unit % a.kv_heads;
+  // Block barriers below must be reached by every wave of the block the same number of
+  // times.  SPLIT 4: the block is one unit, whose waves all leave together.  SPLIT 1: no
+  // barriers.  SPLIT 2 (launched for padded runs only, where every unit has the same query
+  // count and so the same loop trips): a unit past the end stays and runs the loops with
+  // no visible key and no store.
+  const bool unit_ok = unit < a.n_seqs * a.kv_heads;
+  if (!unit_ok && SPLIT != 2) return;
+  const int b = unit_ok ? unit / a.kv_heads : 0, h = unit_ok ? unit % a.kv_heads : 0;
   const int li = lane & 15, lg = lane >> 4;
   const int G = a.n_heads / a.kv_heads;
   unsigned char *vt = vtile[wave];
@@ -594,7 +602,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
   const int64_t q_base = a.seq_start ? tok0 * a.q_st : int64_t(b) * a.q_sb;
   const int64_t o_base = a.seq_start ? tok0 * a.o_st : int64_t(b) * a.o_sb;
   const int64_t kl = a.key_lengths[b] + a.kl_add;
-  const bool row_ok = row >= 0 && row < a.capacity;
+  const bool row_ok = unit_ok && row >= 0 && row < a.capacity;
   // This (row, head) segment: max_len keys of D elements.
   const int64_t seg = row_ok ? (row * a.kv_heads + h) * int64_t(a.max_len) * D : 0;
   const uint32_t seg_bytes = uint32_t(a.max_len) * D * 2;
@@ -644,14 +652,33 @@ void decode_attention_tr_kernel(AttnArgs a) {
       for (int st = 0; st < DEPTH; ++st) fetch(st, part * KT + st * SPLIT * KT);
     }
 
-    // ---- queries (scaled by softmax scale * log2 e); fp32 rows at 16-byte alignment load as
-    //      two float4 per 8 dims -------------------------------------------------------------
-    const bool q4 = a.q_dtype == CG_F32 &&
+    // ---- queries.  QRAW: already rounded to the cache type unscaled, as the reference rounds
+    //      q (q.to(cache.dtype), trunk.py:222), loaded 16 bytes per 8 dims; the scale (times
+    //      log2 e) then multiplies the fp32 scores.  Otherwise scaled by the softmax scale *
+    //      log2 e and rounded to the cache type; fp32 rows at 16-byte alignment load as two
+    //      float4 per 8 dims. ----------------------------------------------------------------
+    const bool q4 = !QRAW && a.q_dtype == CG_F32 &&
                     ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 3) | (a.q_sh & 3) | (a.q_st & 3) | (q_base & 3)) == 0;
     typename Mfma16<TKV>::vec qv[NQT][DK];
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
       const int m = qg + 16 * qt + li;
+      if constexpr (QRAW) {
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          if (m < nq) {
+            const int64_t qo = q_base + int64_t(h * G + m % G) * a.q_sh + int64_t(m / G) * a.q_st;
+            qv[qt][dk] = *reinterpret_cast<const typename Mfma16<TKV>::vec *>(static_cast<const TKV *>(a.q) + qo +
+                                                                               32 * dk + 8 * lg);
+          } else {
+            f32x8 z;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) z[e] = 0.f;
+            qv[qt][dk] = Mfma16<TKV>::from(z);
+          }
+        }
+        continue;
+      }
       f32x8 f[DK];
       if (m < nq) {
         const int t = m / G, g = m % G;
@@ -714,7 +741,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
             __builtin_memcpy(&kvec, &kr[st][j][dk], 16);
             s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
           }
-          sc[qt][j] = s4;
+          sc[qt][j] = QRAW ? s4 * a.scale_log2 : s4;
         }
       // ---- V rows -> LDS (as loaded), then the next tile's loads ----------------------
 #pragma unroll
@@ -836,7 +863,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
     for (int qt = 0; qt < NQT; ++qt) {
       const float total = SPLIT > 1 ? lsum[qt] : xor32_sum(xor16_sum(lsum[qt]));
       const int m = qg + 16 * qt + li;
-      if (m >= nq) continue;
+      if (m >= nq || !unit_ok) continue;
       const int t = m / G, g = m % G;
       const float inv = total > 0.f ? 1.0f / total : 0.f;
       const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st;
@@ -867,6 +894,10 @@ void decode_attention_tr_kernel(AttnArgs a) {
 #ifndef TR_KT
 #define TR_KT 64
 #endif
+// Waves per unit for padded one-query-group runs (decode): 1, 2 or 4.
+#ifndef TR_SPLIT_PADDED
+#define TR_SPLIT_PADDED TR_SPLIT
+#endif
 #ifndef TR_DEPTH
 #define TR_DEPTH 1
 #endif
@@ -874,34 +905,50 @@ void decode_attention_tr_kernel(AttnArgs a) {
 #define TR_ONE_WAVE_ITEMS 2048
 #endif
 
+// The 16-bit-pool kernels for one query form (QRAW: queries stored in the cache type).
+template <typename TKV, int D, bool QRAW>
+void launch_tr(const AttnArgs &a, int queries, hipStream_t s) {
+  const unsigned units = unsigned(int64_t(a.n_seqs) * a.kv_heads);
+  const unsigned tr_grid = (units * TR_SPLIT + 3) / 4;
+  if (queries <= 16 && !a.seq_start && TR_SPLIT_PADDED != TR_SPLIT)
+    decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT_PADDED, TR_KT, TR_DEPTH, QRAW>
+        <<<(units * TR_SPLIT_PADDED + 3) / 4, 256, 0, s>>>(a);
+  else if (queries <= 16)
+    decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT, TR_KT, TR_DEPTH, QRAW><<<tr_grid, 256, 0, s>>>(a);
+  else if (queries <= 32)
+    decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT, TR_KT, TR_DEPTH, QRAW><<<tr_grid, 256, 0, s>>>(a);
+  else {
+    // Multi-token rows (prefill, chunks): one block row per 64 queries of a unit.  With
+    // enough (unit, query group) items to fill the chip, or no query seeing more than one
+    // 64-key tile, one wave takes a whole item (four per block); otherwise four waves
+    // split its key tiles and merge.
+    const dim3 grid_q(1, unsigned(std::min<int64_t>((int64_t(queries) + 63) / 64, 65535)));
+    if (a.span <= 64 || int64_t(units) * grid_q.y >= TR_ONE_WAVE_ITEMS) {
+      decode_attention_tr_kernel<TKV, D, 4, 1, 64, 1, QRAW><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
+    } else {
+      decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1, QRAW><<<dim3(tr_grid, grid_q.y), 256, 0, s>>>(a);
+    }
+  }
+  CG_LAUNCHED();
+}
+
 template <typename TKV, int D>
 void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
   const unsigned grid = unsigned((int64_t(a.n_seqs) * a.kv_heads + 3) / 4);
   if constexpr (sizeof(TKV) == 2) {
     CG_REQUIRE(int64_t(a.max_len) * D * 2 < (int64_t(1) << 31), CG_ERR_UNSUPPORTED,
                "decode attention: one cache row of one head must stay below 2 GiB");
-    const unsigned units = unsigned(int64_t(a.n_seqs) * a.kv_heads);
-    const unsigned tr_grid = (units * TR_SPLIT + 3) / 4;
-    if (queries <= 16) decode_attention_tr_kernel<TKV, D, 1, TR_SPLIT, TR_KT, TR_DEPTH><<<tr_grid, 256, 0, s>>>(a);
-    else if (queries <= 32) decode_attention_tr_kernel<TKV, D, 2, TR_SPLIT, TR_KT, TR_DEPTH><<<tr_grid, 256, 0, s>>>(a);
-    else {
-      // Multi-token rows (prefill, chunks): one block row per 64 queries of a unit.  With
-      // enough (unit, query group) items to fill the chip, or no query seeing more than one
-      // 64-key tile, one wave takes a whole item (four per block); otherwise four waves
-      // split its key tiles and merge.
-      const dim3 grid_q(1, unsigned(std::min<int64_t>((int64_t(queries) + 63) / 64, 65535)));
-      if (a.span <= 64 || int64_t(units) * grid_q.y >= TR_ONE_WAVE_ITEMS) {
-        decode_attention_tr_kernel<TKV, D, 4, 1, 64, 1><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
-      } else {
-        decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1><<<dim3(tr_grid, grid_q.y), 256, 0, s>>>(a);
-      }
-    }
+    constexpr int KV_CODE = std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16;
+    if (a.q_dtype == KV_CODE &&
+        ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 7) | (a.q_sh & 7) | (a.q_st & 7)) == 0)
+      return launch_tr<TKV, D, true>(a, queries, s);
+    return launch_tr<TKV, D, false>(a, queries, s);
   } else {
     if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
     else if (queries <= 32) decode_attention_mfma_kernel<TKV, D, 2><<<grid, 256, 0, s>>>(a);
     else decode_attention_mfma_kernel<TKV, D, 4><<<grid, 256, 0, s>>>(a);
+    CG_LAUNCHED();
   }
-  CG_LAUNCHED();
 }
 
 template <typename TKV, int D>

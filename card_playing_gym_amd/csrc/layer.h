@@ -39,7 +39,8 @@ struct TailArgs {
   int32_t final_ln;
   const float *ln_w, *ln_b;  // next block's ln_attn, or the final norm
   const void *w_qkv;         // [n_qkv, d]
-  float *q;                  // [M, q_cols]
+  void *q;                   // [M, q_cols], type q_dtype (the pool's 16-bit type, or fp32)
+  int32_t q_dtype;
   void *kc, *vc;
   const int32_t *tok_row, *tok_pos;
   const float *vemb;

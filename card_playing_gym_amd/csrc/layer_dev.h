@@ -21,8 +21,18 @@ constexpr int ring_of() { return BM >= 64 ? 1 : TAIL_RING; }
 
 enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
 
+// MLP stage order.  Blocks of up to 32 rows run every up chunk first (each GELU output to
+// its own LDS buffer), one barrier, then every down chunk: one block-wide wait for the MLP
+// instead of one per chunk.  64-row blocks interleave up c, down c through two buffers
+// (four would not fit in LDS beside the panel).
+template <int BM>
+constexpr bool ups_first() { return BM <= 32; }
+template <int BM>
+constexpr int hbufs_of() { return ups_first<BM>() ? 4 : 2; }
+
 struct Plan {
   int nc, nq, n_post, S;
+  bool ups_first;
 };
 
 __device__ __forceinline__ int stage_kind(const Plan &p, int s, int &chunk) {
@@ -30,6 +40,10 @@ __device__ __forceinline__ int stage_kind(const Plan &p, int s, int &chunk) {
     if (s == 0) {
       chunk = 0;
       return ST_OUT;
+    }
+    if (p.ups_first) {
+      chunk = s - 1 < p.nc ? s - 1 : s - 1 - p.nc;
+      return s - 1 < p.nc ? ST_UP : ST_DOWN;
     }
     chunk = (s - 1) >> 1;
     return ((s - 1) & 1) ? ST_DOWN : ST_UP;
@@ -169,7 +183,7 @@ __device__ __forceinline__ void store_kv(void *base, int dtype, int64_t index, f
 // final norm.  NC / NQ: 256-wide chunks of d_ff / of the QKV width.  The stage sequence is
 // a compile-time constant, so the fully unrolled stage loop folds every stage's kind and
 // the weight registers flow from stage to stage without merges.
-// Row block `blk` of one layer tail.  LDS: panel [BM rows of ROWB bytes], hbuf two more,
+// Row block `blk` of one layer tail.  LDS: panel [BM rows of ROWB bytes], hbuf two or four more,
 // red 2 * WAVES * BM floats, dyn the Params (d_ff + 5 PANEL floats, then 3 BM ints).
 template <int BM, int MODE, int NC, int NQ>
 __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned char *panel,
@@ -189,6 +203,9 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   p.nq = FINAL ? 0 : NQ;
   p.n_post = N_POST;
   p.S = S;
+  p.ups_first = ups_first<BM>();
+  constexpr int HB = hbufs_of<BM>();
+  static_assert(!ups_first<BM>() || NC <= HB, "one GELU buffer per d_ff chunk");
   const uint32_t xbytes = uint32_t(a.M) * uint32_t(d) * 4;
 
   // Prologue loads, issued before the weight stream (loads complete in order, so anything
@@ -251,8 +268,8 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   for (int o = tid * 16; o < BM * ROWB; o += THREADS * 16) {
     const uint4 z = {0u, 0u, 0u, 0u};
     *reinterpret_cast<uint4 *>(panel + o) = z;
-    *reinterpret_cast<uint4 *>(hbuf[0] + o) = z;
-    *reinterpret_cast<uint4 *>(hbuf[1] + o) = z;
+#pragma unroll
+    for (int h = 0; h < HB; ++h) *reinterpret_cast<uint4 *>(hbuf[h] + o) = z;
   }
 #pragma unroll
   for (int k = 0; k < NB_UP; ++k) {
@@ -374,7 +391,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
       }
       zero<FM>(acc);
       stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
-      unsigned char *hb = hbuf[c & 1];
+      unsigned char *hb = hbuf[p.ups_first ? c : (c & 1)];
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = cw + 16 * j + li;
@@ -388,7 +405,8 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
             *reinterpret_cast<bf16 *>(hb + row * ROWB + col * 2) = from_f32<bf16>(g);
           }
       }
-      lds_barrier();
+      // Down chunk c reads every wave's columns of GELU chunk c.
+      if (!p.ups_first || c == p.nc - 1) lds_barrier();
     } else if (kind == ST_DOWN) {
       // ---- down chunk c (accumulates); after the last: residual (+PLE), next prologue
       const bool last = c == p.nc - 1;
@@ -413,7 +431,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
         }
       }
       __builtin_amdgcn_sched_barrier(0);  // residual loads ahead of the weight refills
-      stage_mma<FM>(accd, hbuf[c & 1], cur, nx, refill, lane_o);
+      stage_mma<FM>(accd, hbuf[p.ups_first ? c : (c & 1)], cur, nx, refill, lane_o);
       if (last) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -470,7 +488,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
           for (int j = 0; j < FN; ++j) {
             const float v = acc[i][j][r];
             if (role[j] == 0) {
-              gst(a.q + int64_t(m) * a.q_cols + col[j], v);
+              store_kv(a.q, a.q_dtype, int64_t(m) * a.q_cols + col[j], v);
             } else if (role[j] > 0 && trow[i][r] >= 0) {
               float val = v;
               if (role[j] == 2 && a.vemb_off >= 0) val += a.vemb[int64_t(m) * a.ld_vemb + a.vemb_off + col[j]];

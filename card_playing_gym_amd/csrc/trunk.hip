@@ -263,7 +263,11 @@ int cg_trunk_create(const cg_trunk_config *config, const cg_layer_params *layers
       t->down_w[l] = t->layers[l].mlp_down_w;
     }
     if (compute_dtype == CG_BF16) {
+#ifdef CG_TRUNK_NO_FUSED
+      t->fused = false;  // measurement builds only
+#else
       t->fused = tail_supported(c.d_model, c.d_ff, (c.n_heads + 2 * c.n_kv_heads) * hd);
+#endif
       t->wbuf_bytes = weight_bytes_per_layer(*t) * n;
       CG_HIP(hipMalloc(&t->wbuf, t->wbuf_bytes));
       convert_weights(*t, nullptr);
@@ -355,12 +359,20 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
     const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
     return 1.0f / sqrtf(float(repeats));
   }();
+  // Queries of multi-token rows (packed chunks, prefill) are stored in the pool's 16-bit type
+  // by the fused step (the reference rounds q to the cache dtype before the scores,
+  // trunk.py:222), which the attention kernel loads as its MFMA operand as they are:
+  // 139 -> 100 us per layer at config 5.  One-token decode keeps fp32 q, which that kernel
+  // scales and rounds itself (the raw form measured 2.6 us slower per layer there); the
+  // projections of the unfused path write fp32.
+  const bool multi_query = r.seq_start != nullptr || int64_t(H / KVH) * r.T > 16;
+  const int q_dtype = (t.fused && multi_query && cache[0].dtype != CG_F32) ? cache[0].dtype : CG_F32;
   auto attention = [&](int l) {
     const cg_kv_layer &L = cache[l];
     {
       AttnArgs a{};
       a.q = w.q;
-      a.q_dtype = CG_F32;
+      a.q_dtype = q_dtype;
       a.q_st = int64_t(H) * D;
       a.q_sh = D;
       a.q_sb = int64_t(r.T) * H * D;
@@ -407,6 +419,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
       ta.kv_dtype = cache[0].dtype;
       ta.eps = c.eps;
       ta.q = w.q;
+      ta.q_dtype = q_dtype;
       ta.tok_row = w.tok_row;
       ta.tok_pos = w.tok_pos;
       ta.vemb = values;
