@@ -191,7 +191,10 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     dev = bench.device
     games, H, D = bench.games, cfg.n_heads, cfg.head_dim
     tokens = max(p.n_tokens for p in bench.plans[first:first + count])
-    q = torch.randn((tokens, H, D), device=dev, dtype=torch.float32)
+    # The step's query type: packed chunks store q in the pool's 16-bit type, one-token
+    # decode keeps fp32 q (the rule of trunk_forward in csrc/trunk.hip).
+    q_dtype = bench.cache.dtype if bench.chunks and bench.cache.dtype != torch.float32 else torch.float32
+    q = torch.randn((tokens, H, D), device=dev, dtype=torch.float32).to(q_dtype)
     out = torch.empty((tokens, H, D), device=dev, dtype=torch.bfloat16)
     key_lengths = torch.empty(games, dtype=torch.int64, device=dev)
     rows = torch.empty(games, dtype=torch.int64, device=dev)
@@ -220,7 +223,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
                                D ** -0.5)
         ends[i].record(stream)
         kv = kv_bytes(plan, cfg.n_layers, cfg.n_kv_heads, D, itemsize)
-        total_bytes += kv + cfg.n_layers * plan.n_tokens * H * D * (4 + 2)  # + q read (fp32) + out write (bf16)
+        total_bytes += kv + cfg.n_layers * plan.n_tokens * H * D * (q.element_size() + 2)  # + q read + out write (bf16)
     torch.cuda.synchronize()
     ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends))
     launches = count * cfg.n_layers

@@ -21,6 +21,7 @@ import torch
 from torch import nn
 
 from .. import _native as nat
+from ..nn import ops
 from ..nn.derived import DerivedCopies, HandleCache, after_load_hook
 from ..nn.kv_cache import require_device, stream_handle
 from ..nn.trunk import TrunkConfig
@@ -122,7 +123,7 @@ class CardGrid(nn.Module):
         nn.init.normal_(self.summary.weight, std=0.02 * (NUM_FIELDS / (NUM_CARDS * width)) ** 0.5)
 
 
-class PiquetEmbedding(nn.Module):
+class PiquetEmbedding(ops.Registered, nn.Module):
     """Token fields plus the card-grid summary (model.py:286-341), on the HIP path."""
 
     def __init__(self, config: PiquetModelConfig, ple_width: int, value_width: int) -> None:
@@ -142,6 +143,7 @@ class PiquetEmbedding(nn.Module):
         # steps and load_state_dict (card_playing_gym_amd/nn/derived.py).
         self._handles = HandleCache()
         self.register_load_state_dict_post_hook(after_load_hook)
+        self._register_op_key()
 
     def _params(self) -> list[torch.Tensor]:
         g = self.grid
@@ -192,27 +194,34 @@ class PiquetEmbedding(nn.Module):
         if flat.shape[1] != NUM_FIELDS + NUM_CARDS:
             raise ValueError("a Piquet token holds 32 fields and 32 card codes")
         flat = flat.to(torch.int64).contiguous()
-        n = flat.shape[0]
         c = self.config
-        x = torch.empty((n, c.d_model), device=device, dtype=torch.bfloat16)
-        ple = None if self.ple_fields is None else torch.empty((n, self.ple_fields.embedding_dim), device=device,
-                                                               dtype=torch.bfloat16)
-        values = None if self.value_fields is None else torch.empty((n, self.value_fields.embedding_dim),
-                                                                    device=device, dtype=torch.bfloat16)
-        cards = torch.empty((n, NUM_CARDS, c.card_width), device=device, dtype=torch.float32)
-        stream = stream_handle(device)
-        handle = self.native(device)
-        nat.call(
-            "cg_piquet_embed", handle.handle, flat.data_ptr(), flat.shape[1], n, x.data_ptr(),
-            None if ple is None else ple.data_ptr(), None if values is None else values.data_ptr(),
-            cards.data_ptr(), None, stream,
-        )
+        ple_width = 0 if self.ple_fields is None else self.ple_fields.embedding_dim
+        value_width = 0 if self.value_fields is None else self.value_fields.embedding_dim
+        x, ple, values, cards = ops.piquet_embed(flat, self.op_key, c.d_model, ple_width, value_width, c.card_width)
         self.kept = cards.view(*lead, NUM_CARDS, c.card_width)
         return (
             x.view(*lead, -1),
-            None if ple is None else ple.view(*lead, -1),
-            None if values is None else values.view(*lead, -1),
+            None if self.ple_fields is None else ple.view(*lead, -1),
+            None if self.value_fields is None else values.view(*lead, -1),
         )
+
+    def _embed_native(self, flat: torch.Tensor):
+        """The launch behind ``torch.ops.cardgym_hip.piquet_embed`` (flat int64 tokens [n, 64])."""
+
+        device = flat.device
+        n = flat.shape[0]
+        c = self.config
+        widths = [0 if t is None else t.embedding_dim for t in (self.ple_fields, self.value_fields)]
+        x = torch.empty((n, c.d_model), device=device, dtype=torch.bfloat16)
+        ple, values = (torch.empty((n, w), device=device, dtype=torch.bfloat16) for w in widths)
+        cards = torch.empty((n, NUM_CARDS, c.card_width), device=device, dtype=torch.float32)
+        handle = self.native(device)
+        nat.call(
+            "cg_piquet_embed", handle.handle, flat.data_ptr(), flat.shape[1], n, x.data_ptr(),
+            ple.data_ptr() if widths[0] else None, values.data_ptr() if widths[1] else None, cards.data_ptr(), None,
+            stream_handle(device),
+        )
+        return x, ple, values, cards
 
 
 class _NativePiquet(DerivedCopies):

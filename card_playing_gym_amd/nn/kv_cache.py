@@ -132,6 +132,16 @@ class KVCache:
             self._layers = array
         return self._layers
 
+    def pools(self) -> tuple[list[torch.Tensor], list[torch.Tensor]]:
+        """The storage tensors themselves, never views of one another: the stacked
+        [n_layers, capacity, kv_heads, max_len, head_dim] pair when ``stacked``, else the
+        per-layer tensors.  This is what the trunk-step op mutates: a list of views of one
+        base would make torch.compile's functionalisation copy the pool around the call."""
+
+        if self.stacked:
+            return [self._base_k], [self._base_v]
+        return self.k, self.v
+
     def _stream(self) -> int:
         return stream_handle(self.device)
 

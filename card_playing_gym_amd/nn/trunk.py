@@ -26,6 +26,7 @@ import torch
 from torch import nn
 
 from .. import _native as nat
+from . import ops
 from .derived import DerivedCopies, HandleCache, after_load_hook
 from .kv_cache import KVCache, index_tensor, require_device, stream_handle
 
@@ -110,12 +111,7 @@ class RMSNorm(nn.Module):
         bf16 = x.dtype == torch.bfloat16
         flat = x.reshape(-1, x.shape[-1])
         flat = (flat if bf16 else flat.float()).contiguous()
-        out = torch.empty(flat.shape, device=flat.device, dtype=torch.float32)
-        nat.call(
-            "cg_rmsnorm", flat.data_ptr(), nat.CG_BF16 if bf16 else nat.CG_F32, _param(self.weight).data_ptr(),
-            float(self.eps), out.data_ptr(), flat.shape[0], flat.shape[1], stream_handle(x.device),
-        )
-        return out.view(x.shape)
+        return ops.rmsnorm(flat, self.weight, float(self.eps)).view(x.shape)
 
 
 class DecoderBlock(nn.Module):
@@ -208,7 +204,7 @@ def _trunk_tensors(trunk: "Trunk"):
     yield trunk.final_norm.bias
 
 
-class Trunk(nn.Module):
+class Trunk(ops.Registered, nn.Module):
     def __init__(self, config: TrunkConfig) -> None:
         super().__init__()
         config.validate()
@@ -231,6 +227,8 @@ class Trunk(nn.Module):
         # and load_state_dict (card_playing_gym_amd/nn/derived.py).
         self._handles = HandleCache()
         self.register_load_state_dict_post_hook(after_load_hook)
+        # The key naming this trunk inside torch.ops.cardgym_hip.trunk_step.
+        self._register_op_key()
         # The reference's fused Metal trunk (trunk.py:274, model.py:108-115) exists only on
         # MPS; callers read `metal` and `uses_metal` to choose that path.  Here the HIP
         # kernels are the path on every call, so there is never a Metal trunk.
@@ -243,8 +241,11 @@ class Trunk(nn.Module):
 
     # -- native handle ---------------------------------------------------------
 
-    def native(self, device: torch.device) -> _NativeTrunk:
-        compute = compute_dtype_code(device)
+    def native(self, device: torch.device, compute: int | None = None) -> _NativeTrunk:
+        """The handle for ``device`` and a compute type (the autocast state's by default)."""
+
+        if compute is None:
+            compute = compute_dtype_code(device)
         key = (device.index if device.index is not None else torch.cuda.current_device(), compute)
         return self._handles.get(
             key, list(_trunk_tensors(self)), lambda: _NativeTrunk(self, compute, device), stream_handle(device)
@@ -289,13 +290,8 @@ class Trunk(nn.Module):
             bf16 = ple_lookup.dtype == torch.bfloat16
             lookup = ple_lookup.reshape(flat.shape[0], -1)
             lookup = (lookup if bf16 else lookup.float()).contiguous()
-            out = torch.empty(lookup.shape, device=lookup.device, dtype=torch.float32)
-            nat.call(
-                "cg_linear_add_scale", flat.data_ptr(), _param(self.ple_context.weight).data_ptr(),
-                lookup.data_ptr(), nat.CG_BF16 if bf16 else nat.CG_F32, out.data_ptr(), flat.shape[0],
-                lookup.shape[1], flat.shape[1], 1.0 / math.sqrt(2.0), compute_dtype_code(x.device),
-                stream_handle(x.device),
-            )
+            out = ops.ple_context(flat, self.ple_context.weight, lookup, 1.0 / math.sqrt(2.0),
+                                  compute_dtype_code(x.device))
             ple = out.view(*lead, self.config.n_layers, self.config.per_layer_dim)
         values = None
         if self._value_index:
@@ -352,7 +348,11 @@ class Trunk(nn.Module):
         readout: torch.Tensor | None,
         span: int | None,
     ) -> torch.Tensor:
-        require_device(x, cache.k[0])
+        # (The pool is named by its storage tensors only, never by its per-layer views:
+        # see KVCache.pools.)
+        require_device(x)
+        if cache.device.type != "cuda":
+            raise RuntimeError("the KV pool must live on the GPU")
         config = self.config
         if cache.n_layers != config.n_layers or cache.kv_heads != config.n_kv_heads or cache.head_dim != config.head_dim:
             raise ValueError("cache layout does not match the trunk")
@@ -365,24 +365,13 @@ class Trunk(nn.Module):
             raise ValueError("This trunk expects a per-layer embedding lookup.")
         if self._value_index and values_flat is None:
             raise ValueError("This trunk expects a value-embedding lookup.")
-        native = self.native(device)
-        stream = stream_handle(device)
-        rows_out = n_seqs if readout is not None else n_tokens
-        hidden = torch.empty((rows_out, config.d_model), device=device, dtype=torch.float32)
-        size = nat.lib().cg_trunk_workspace_size(native.handle, n_tokens, n_seqs)
-        workspace = torch.empty(max(size, 1), device=device, dtype=torch.uint8)
-        step = nat.Ragged(
-            n_seqs, n_tokens, T, 0 if span is None else int(span),
-            None if seq_start is None else seq_start.data_ptr(), positions.data_ptr(),
-            None if rows is None else rows.data_ptr(), None if readout is None else readout.data_ptr(),
+        # One opaque op per step (torch.ops.cardgym_hip.trunk_step): eager, compiled and
+        # captured calls all launch the same cg_trunk_forward.
+        k_pools, v_pools = cache.pools()
+        return ops.trunk_step(
+            flat, ple_flat, values_flat, k_pools, v_pools, positions, seq_start, rows, readout, self.op_key,
+            compute_dtype_code(device), n_seqs, T, 0 if span is None else int(span),
         )
-        nat.call(
-            "cg_trunk_forward", native.handle, cache.layer_array(), flat.data_ptr(),
-            None if ple_flat is None else ple_flat.data_ptr(),
-            None if values_flat is None else values_flat.data_ptr(),
-            ctypes.byref(step), hidden.data_ptr(), workspace.data_ptr(), size, stream,
-        )
-        return hidden
 
     def forward_ragged(
         self,

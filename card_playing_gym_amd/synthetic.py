@@ -24,14 +24,20 @@ from torch import nn
 from . import _native as nat
 from .nn.derived import DerivedCopies, HandleCache, after_load_hook
 from .nn.kv_cache import require_device, stream_handle
+from .nn import ops
 from .nn.model import SequenceModel, value_mlp
 from .nn.trunk import TrunkConfig, _param, compute_dtype_code, init_weights
 
 VOCAB = 512
 
 
-class SyntheticModel(SequenceModel):
-    """Embedding -> trunk -> (policy logits, seat values)."""
+class SyntheticModel(ops.Registered, SequenceModel):
+    """Embedding -> trunk -> (policy logits, seat values).
+
+    Besides :meth:`heads` it answers the actor interface the reference's decode graphs
+    call (cardgym/games/base.py:25-58: ``policy_heads``, ``graphable_heads``,
+    ``pop_context``, ``policy_logits``, ``player_values``), so
+    ``card_playing_gym_amd.rl.graphs.DecodeGraphs`` runs it as it runs a game's actor."""
 
     graphable_heads = True
     policy_heads = ("policy",)
@@ -46,6 +52,7 @@ class SyntheticModel(SequenceModel):
         init_weights(self.policy_head)
         self.value_head = value_mlp(d, seats)
         self.register_load_state_dict_post_hook(after_load_hook)
+        self._register_op_key()
 
     def embed(self, tokens: torch.Tensor):
         return self.embedding(tokens[..., 0]), None, None
@@ -60,12 +67,7 @@ class SyntheticModel(SequenceModel):
         require_device(tokens)
         ids = tokens[..., 0].reshape(-1).to(torch.int64).contiguous()
         d = self.trunk_config.d_model
-        out = torch.empty((ids.numel(), d), device=tokens.device, dtype=torch.float32)
-        nat.call(
-            "cg_embed_rmsnorm", _param(self.embedding.weight).data_ptr(), self.vocab, ids.data_ptr(),
-            _param(trunk.input_norm.weight).data_ptr(), float(trunk.input_norm.eps), out.data_ptr(),
-            ids.numel(), d, None, stream_handle(tokens.device),
-        )
+        out = ops.embed_rmsnorm(self.embedding.weight, ids, trunk.input_norm.weight, float(trunk.input_norm.eps))
         return out.view(*tokens.shape[:-1], d), None, None
 
     def heads(self, hidden: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -77,10 +79,30 @@ class SyntheticModel(SequenceModel):
         require_device(hidden)
         if torch.is_grad_enabled() and (hidden.requires_grad or any(p.requires_grad for p in self._head_tensors())):
             raise RuntimeError("the fused heads are inference-only: call them under torch.no_grad()")
-        device = hidden.device
-        compute = compute_dtype_code(device)
-        stream = stream_handle(device)
         h = hidden.float().contiguous()
+        return ops.synthetic_heads(h, self.op_key, compute_dtype_code(hidden.device), self.vocab,
+                                   self.value_head[2].out_features)
+
+    # -- the actor interface of the reference's decode graphs ---------------------------
+
+    def pop_context(self) -> torch.Tensor | None:
+        """No per-position features outlive the forward (base.py:48-58)."""
+
+        return None
+
+    def policy_logits(self, hidden, head, features=None, tokens=None, context=None) -> torch.Tensor:
+        if head not in self.policy_heads:
+            raise ValueError(f"Unknown policy head {head!r}.")
+        return self.heads(hidden)[0]
+
+    def player_values(self, hidden: torch.Tensor) -> torch.Tensor:
+        return self.heads(hidden)[1]
+
+    def _run_heads(self, h: torch.Tensor, compute: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The launches behind ``torch.ops.cardgym_hip.synthetic_heads``."""
+
+        device = h.device
+        stream = stream_handle(device)
         m, d = h.shape
         logits = torch.empty((m, self.vocab), device=device, dtype=torch.float32)
         first, last = self.value_head[0], self.value_head[2]

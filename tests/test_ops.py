@@ -1,0 +1,148 @@
+"""The custom-op boundary (card_playing_gym_amd/nn/ops.py) on the CPU: every op is
+registered under ``torch.ops.cardgym_hip``, a whole decode wave (embedding, trunk step,
+heads) traces through the ops' fake implementations without a single library call, and
+the module keys the ops resolve follow copies and die with their modules."""
+
+from __future__ import annotations
+
+import copy
+import gc
+
+import numpy as np
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+from card_playing_gym_amd import _native as nat
+from card_playing_gym_amd.nn import ops
+from card_playing_gym_amd.nn.kv_cache import KVCache
+from card_playing_gym_amd.nn.trunk import TrunkConfig
+from card_playing_gym_amd.synthetic import build_model
+
+OPS = ("rmsnorm", "embed_rmsnorm", "ple_context", "trunk_step", "synthetic_heads", "piquet_embed", "decode_attention")
+
+
+def test_ops_are_registered():
+    import card_playing_gym_amd.nn.decode  # noqa: F401  (registers decode_attention)
+
+    for name in OPS:
+        assert hasattr(torch.ops.cardgym_hip, name), name
+    schema = str(torch.ops.cardgym_hip.trunk_step.default._schema)
+    # The pools are declared mutated (so functionalisation orders them), nothing else is.
+    assert "Tensor(a3!)[] k" in schema and "Tensor(a4!)[] v" in schema, schema
+    assert schema.count("!") == 2, schema
+
+
+@pytest.mark.parametrize("chunks", [False, True])
+def test_wave_traces_through_fake_ops(monkeypatch, chunks):
+    """Under fake tensors the wave runs only the ops' fake implementations: a library
+    call would need real device pointers, and is made to fail here."""
+
+    def refuse(*args, **kwargs):
+        raise AssertionError(f"library call during a fake trace: {args[:1]}")
+
+    monkeypatch.setattr(nat, "call", refuse)
+    config = TrunkConfig(d_model=64, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=128)
+    model = build_model(config, seed=1)
+    rows, run = 6, 3
+    with FakeTensorMode(allow_non_fake_inputs=True), torch.no_grad():
+        cache = KVCache(n_layers=2, kv_heads=2, head_dim=16, capacity=8, max_len=32, device="cuda",
+                        dtype=torch.bfloat16)
+        positions = torch.zeros(rows, dtype=torch.int64, device="cuda")
+        cache_rows = torch.arange(rows, dtype=torch.int64, device="cuda")
+        if chunks:
+            tokens = torch.zeros((10, 1), dtype=torch.int64, device="cuda")
+            seq_start = torch.tensor([0, 1, 3, 4, 6, 9, 10], device="cuda")
+            hidden = model.forward_packed(tokens, seq_start, positions, cache, None, cache_rows)
+            assert hidden.shape == (10, 64)
+        else:
+            tokens = torch.zeros((rows, run, 1), dtype=torch.int64, device="cuda")
+            offsets = torch.full((rows,), run - 1, dtype=torch.int64, device="cuda")
+            hidden = model.forward_ragged(tokens, positions, cache, offsets, span=16, rows=cache_rows)
+            assert hidden.shape == (rows, 64)
+        logits, values = model.heads(hidden)
+        assert logits.shape == (hidden.shape[0], model.vocab) and values.shape == (hidden.shape[0], 2)
+        assert logits.dtype == values.dtype == torch.float32
+        assert logits.device.type == "cuda"
+        assert model.policy_logits(hidden, "policy").shape == logits.shape
+        assert model.player_values(hidden).shape == values.shape
+        with pytest.raises(ValueError):
+            model.policy_logits(hidden, "nope")
+
+
+def test_keys_follow_copies_and_die_with_modules():
+    config = TrunkConfig(d_model=32, n_layers=1, n_heads=2, n_kv_heads=1, d_ff=64)
+    model = build_model(config)
+    assert ops.lookup(model.op_key) is model and ops.lookup(model.trunk.op_key) is model.trunk
+    twin = copy.deepcopy(model)
+    assert twin.op_key != model.op_key and twin.trunk.op_key != model.trunk.op_key
+    assert ops.lookup(twin.op_key) is twin and ops.lookup(twin.trunk.op_key) is twin.trunk
+    key = twin.trunk.op_key
+    del twin
+    gc.collect()
+    with pytest.raises(RuntimeError, match="no live module"):
+        ops.lookup(key)
+    assert ops.lookup(model.trunk.op_key) is model.trunk
+
+
+@pytest.mark.parametrize("stacked", [True, False])
+def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
+    """Inductor (CPU codegen here) compiles the decode body of DecodeGraphs with dynamic
+    shapes and ``fullgraph=True``; the trunk-step op must receive the pool's own storage
+    tensors -- no functional clone around the call (which, over per-layer views of one
+    stacked tensor, read past the pool's end) -- and its appends must land in the pool.
+    CPU stand-in kernels replace the HIP ones for the run (scoped to this test)."""
+
+    import card_playing_gym_amd.nn.trunk as trunk_module
+    import card_playing_gym_amd.synthetic as synthetic_module
+    from card_playing_gym_amd.rl import graphs as graphs_module
+
+    for module in (trunk_module, synthetic_module):
+        monkeypatch.setattr(module, "require_device", lambda *tensors: None)
+    model = build_model(TrunkConfig(d_model=64, n_layers=3, n_heads=4, n_kv_heads=2, d_ff=128), seed=2)
+    cache = model.new_cache(32, 64, torch.bfloat16)
+    cache.device = torch.device("cuda")  # the pool stays in host memory; only its placement check passes
+    if not stacked:  # the layout of pools too large for one tensor: one tensor per layer
+        cache.stacked = False
+        cache.k = [t.clone() for t in cache.k]
+        cache.v = [t.clone() for t in cache.v]
+    storage = [t.data_ptr() for t in cache.pools()[0]]
+    seen = []
+
+    def trunk_cpu(x, ple, values, k, v, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
+        seen.append([t.data_ptr() for t in k])
+        layers = list(k[0].unbind(0)) if k[0].dim() == 5 else list(k)
+        for b in range(int(n_seqs)):
+            for t in range(int(T)):
+                for layer in layers:
+                    layer[int(rows[b]), :, min(int(positions[b]) + t, layer.shape[2] - 1)] = 1.0
+        return x.new_zeros((int(n_seqs), x.shape[1]))
+
+    class Body(graphs_module.DecodeGraphs):
+        def __init__(self):  # the body alone: no graph pool, no capture
+            self.model, self.cache, self.precision, self.values = model, cache, "fp32", True
+            self.heads = tuple(model.policy_heads)
+
+    torch._dynamo.reset()
+    with torch.library._scoped_library("cardgym_hip", "IMPL") as lib:
+        lib.impl("trunk_step", trunk_cpu, "CPU")
+        lib.impl("embed_rmsnorm", lambda table, ids, w, eps: table.new_zeros((ids.numel(), table.shape[1])), "CPU")
+        lib.impl("synthetic_heads", lambda h, m, c, p, n: (h.new_zeros((h.shape[0], p)), h.new_zeros((h.shape[0], n))),
+                 "CPU")
+        body = torch.compile(Body()._outputs, dynamic=True, fullgraph=True)
+        rng = np.random.default_rng(3)
+        written = 0
+        with torch.no_grad():
+            for rows, run in [(16, 1), (12, 2), (16, 1)]:
+                cache_rows = rng.permutation(32)[:rows]
+                positions = rng.integers(0, 50, size=rows)
+                tokens = rng.integers(0, 512, size=(rows, run, 1))
+                offsets = rng.integers(0, run, size=rows)
+                packed = np.concatenate([a.reshape(-1) for a in (tokens, positions, offsets, cache_rows)])
+                out = body(torch.from_numpy(packed.astype(np.int64)), rows, run, 1, 64)
+                assert [tuple(o.shape) for o in out] == [(rows, model.vocab), (rows, 2)]
+                assert seen[-1] == storage
+                written = max(written, int(sum(t.float().sum().item() for t in cache.k)))
+    torch._dynamo.reset()
+    assert len(seen) == 3 and written > 0
+    assert written == int(sum(t.float().sum().item() for t in cache.pools()[0]))
