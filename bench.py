@@ -184,7 +184,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     first..first+count-1, replayed on their own with HIP events on the launch stream
     (packed chunks through the packed entry point, as the step launches them)."""
 
-    from card_playing_gym_amd.nn.decode import attention_into, attention_packed_into
+    from card_playing_gym_amd.nn.decode import attention_into, attention_order, attention_packed_into
     from card_playing_gym_amd.synthetic import kv_bytes
 
     cfg = bench.config
@@ -198,6 +198,14 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     out = torch.empty((tokens, H, D), device=dev, dtype=torch.bfloat16)
     key_lengths = torch.empty(games, dtype=torch.int64, device=dev)
     rows = torch.empty(games, dtype=torch.int64, device=dev)
+    # Decode steps launch the persistent kernel with the step's unit order, computed once per
+    # step (before the layers) by the trunk: here before each step's timed launches.
+    orders = {}
+    if not bench.chunks:
+        for step in range(first, first + count):
+            orders[step] = attention_order(
+                bench.cache.k[0], bench.rows_all[step] if bench.gathered else None, bench.positions_all[step] + 1,
+                games, H, 1, bench.max_len)
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
@@ -220,7 +228,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
             for layer in range(cfg.n_layers):
                 attention_into(out.view(games, H, 1, D), q.view(games, H, 1, D), bench.cache.k[layer],
                                bench.cache.v[layer], rows if bench.gathered else None, key_lengths, bench.max_len,
-                               D ** -0.5)
+                               D ** -0.5, orders[step])
         ends[i].record(stream)
         kv = kv_bytes(plan, cfg.n_layers, cfg.n_kv_heads, D, itemsize)
         total_bytes += kv + cfg.n_layers * plan.n_tokens * H * D * (q.element_size() + 2)  # + q read + out write (bf16)
@@ -233,7 +241,9 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     return {
         # Query tiles of 16 per (row, KV head) unit: one for a decode token's 4 heads, four
         # for chunks of up to 16 tokens.
-        "kernel": "decode_attention_tr_kernel<bf16,32,%d>" % (4 if bench.chunks else 1),
+        "kernel": ("decode_attention_tr_kernel<bf16,32,4>" if bench.chunks else
+                   "decode_attention_stream_kernel<bf16,32>" if all(o is not None for o in orders.values()) else
+                   "decode_attention_tr_kernel<bf16,32,1>"),
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,

@@ -173,6 +173,14 @@ _SIGNATURES = {
         [c_void_p, c_int32, c_int64, c_int64, c_int64, P(KVLayer), c_void_p, c_void_p,
          c_int32, c_int32, c_int32, c_int32, c_float, c_void_p, c_int32, c_void_p],
     ),
+    "cg_decode_attention_order": (
+        c_int32, [P(KVLayer), c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p],
+    ),
+    "cg_decode_attention_ordered": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, c_int64, P(KVLayer), c_void_p, c_void_p,
+         c_int32, c_int32, c_int32, c_int32, c_float, c_void_p, c_int32, c_void_p, c_void_p],
+    ),
     "cg_decode_attention_packed": (
         c_int32,
         [c_void_p, c_int32, c_int64, c_int64, P(KVLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,

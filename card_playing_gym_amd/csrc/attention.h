@@ -28,8 +28,18 @@ struct AttnArgs {
   int32_t n_seqs, n_heads, kv_heads, head_dim, T, max_len, capacity, span;
   int64_t n_tokens;            // packed mode: tokens in q / out (token ranges are clamped to it)
   float scale_log2;            // softmax scale * log2(e)
+  // (row, KV head) units in descending order of key tiles (launch_attention_order), or NULL.
+  // With it, padded runs of up to 16 queries per unit on a 16-bit pool take the persistent
+  // kernel: each wave walks several whole units back to back.
+  const int32_t *order;
 };
 
 void launch_decode_attention(const AttnArgs &a, hipStream_t stream);
+
+// Whether `a` (with an order) takes the persistent kernel, and the order it needs: one int
+// per (row, KV head) unit, written by launch_attention_order from the same rows, key
+// lengths and span (valid for every layer of one step).
+bool attention_streams(const AttnArgs &a);
+void launch_attention_order(const AttnArgs &a, int32_t *order, hipStream_t stream);
 
 }  // namespace cg

@@ -888,6 +888,295 @@ void decode_attention_tr_kernel(AttnArgs a) {
   }
 }
 
+// ---- persistent decode attention ----------------------------------------------------------
+// The split kernel above gives each (row, KV head) unit four waves that stream about one
+// 64-key tile each at decode lengths, so a wave's life is mostly its start (queries, first
+// tile round trip) and the merge.  Here a fixed grid of waves walks whole units back to
+// back: wave w takes units order[w], order[2W - 1 - w], order[2W + w], ... of the units
+// sorted by descending tile count (a snake deal, so every wave gets about the same number
+// of tiles), and while the last tile of one unit is multiplied, the first tile and the
+// queries of its next unit are already in flight.  One wave per unit: no merge.  Same
+// arithmetic per tile as decode_attention_tr_kernel<.., NQT 1, SPLIT 1, KT 64, DEPTH 1>.
+#ifndef STREAM_WAVES_PER_EU
+#define STREAM_WAVES_PER_EU 4
+#endif
+
+// Waves per SIMD the kernel is built for (head_dim 64 needs twice the registers).
+template <int D>
+constexpr int stream_waves_per_eu() { return D == 32 ? STREAM_WAVES_PER_EU : 2; }
+
+template <typename TKV, int D, bool QRAW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<D>())))
+void decode_attention_stream_kernel(AttnArgs a) {
+  constexpr int KT = STREAM_KT;
+  constexpr int NJ = KT / 16;     // 16-key score tiles per key tile
+  constexpr int DK = D / 32;      // 32-dim slices of a key (S^T k-steps)
+  constexpr int DH = D / 16;      // 16-dim slices of the output (O^T row tiles)
+  constexpr int ROW = D * 2 + 8;  // LDS bytes per V row
+  __shared__ __align__(16) unsigned char vtile[4][KT * ROW];
+  typedef typename Mfma16<TKV>::vec QVec;
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int W = int(gridDim.x) * 4, w = int(blockIdx.x) * 4 + wave;
+  const int U = a.n_seqs * a.kv_heads;
+  const int G = a.n_heads / a.kv_heads;
+  const int nq = a.T * G;  // <= 16: query column li is query li (token li / G, head li % G)
+  unsigned char *vt = vtile[wave];
+  const uint32_t seg_bytes = uint32_t(a.max_len) * D * 2;
+
+  // One unit: its pool segment, key range and query / output bases.
+  struct Unit {
+    Rsrc kres, vres;
+    int kend, kfull, lim;
+    int64_t q_base, o_base;
+  };
+  // (An entry outside [0, U) -- an order not written for these arguments -- ends the walk.)
+  auto unit_at = [&](int r) -> int {
+    const int64_t idx = int64_t(r) * W + ((r & 1) ? W - 1 - w : w);
+    const int u = idx < U ? a.order[idx] : -1;
+    return u >= 0 && u < U ? u : -1;
+  };
+  auto describe = [&](int u, Unit &x) {
+    const int b = u / a.kv_heads, h = u % a.kv_heads;
+    const int64_t row = a.rows ? a.rows[b] : int64_t(b);
+    const int64_t kl = a.key_lengths[b] + a.kl_add;
+    const bool row_ok = row >= 0 && row < a.capacity;
+    const int64_t seg = row_ok ? (row * a.kv_heads + h) * int64_t(a.max_len) * D : 0;
+    x.kres = kv_rsrc(static_cast<const TKV *>(a.k) + seg, seg_bytes);
+    x.vres = kv_rsrc(static_cast<const TKV *>(a.v) + seg, seg_bytes);
+    int l = 0;
+    if (li < nq) {
+      int64_t lim64 = kl + li / G;
+      if (lim64 > a.span) lim64 = a.span;
+      l = (row_ok && lim64 > 0) ? int(lim64) : 0;
+    }
+    x.lim = l;
+    x.kend = __builtin_amdgcn_readfirstlane(row16_max(l));
+    x.kfull = __builtin_amdgcn_readfirstlane(row16_min(li < nq ? l : 0x7fffffff));
+    x.q_base = int64_t(b) * a.q_sb + int64_t(h * G) * a.q_sh;
+    x.o_base = int64_t(b) * a.o_sb + int64_t(h * G) * a.o_sh;
+  };
+
+  // Lane l holds key 16 j + l % 16 of a tile at dims 32 dk + 8 (l / 16), for K and V.
+  uint4 kr[NJ][DK], vr[NJ][DK];
+  auto fetch = [&](const Unit &x, int kb) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int key = min(kb + 16 * j + li, x.kend - 1);  // clamped onto the last visible key
+#pragma unroll
+      for (int dk = 0; dk < DK; ++dk) {
+        const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
+        kr[j][dk] = kv_load16(x.kres, off);
+        vr[j][dk] = kv_load16(x.vres, off);
+      }
+    }
+  };
+  // Queries of column li (dims 32 dk + 8 lg .. +7), as loaded; converted at the unit's start.
+  const bool q4 = !QRAW && a.q_dtype == CG_F32 &&
+                  ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 3) | (a.q_sh & 3) | (a.q_st & 3)) == 0;
+  uint4 qraw[QRAW ? DK : 2 * DK];
+  auto load_q = [&](const Unit &x) {
+#pragma unroll
+    for (int dk = 0; dk < (QRAW ? DK : 2 * DK); ++dk) qraw[dk] = uint4{0u, 0u, 0u, 0u};
+    if (li >= nq) return;
+    const int64_t qo = x.q_base + int64_t(li % G) * a.q_sh + int64_t(li / G) * a.q_st;
+    if constexpr (QRAW) {
+#pragma unroll
+      for (int dk = 0; dk < DK; ++dk)
+        qraw[dk] = *reinterpret_cast<const uint4 *>(static_cast<const TKV *>(a.q) + qo + 32 * dk + 8 * lg);
+    } else if (q4) {
+#pragma unroll
+      for (int dk = 0; dk < DK; ++dk) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(static_cast<const float *>(a.q) + qo + 32 * dk + 8 * lg);
+        qraw[2 * dk] = src[0];
+        qraw[2 * dk + 1] = src[1];
+      }
+    } else {
+#pragma unroll
+      for (int dk = 0; dk < DK; ++dk) {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e);
+        qraw[2 * dk] = uint4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+        qraw[2 * dk + 1] = uint4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])};
+      }
+    }
+  };
+  auto queries = [&](QVec (&qv)[DK]) {
+#pragma unroll
+    for (int dk = 0; dk < DK; ++dk) {
+      if constexpr (QRAW) {
+        __builtin_memcpy(&qv[dk], &qraw[dk], 16);
+      } else {
+        const uint4 lo = qraw[2 * dk], hi = qraw[2 * dk + 1];
+        f32x8 f;
+        f[0] = __uint_as_float(lo.x) * a.scale_log2;
+        f[1] = __uint_as_float(lo.y) * a.scale_log2;
+        f[2] = __uint_as_float(lo.z) * a.scale_log2;
+        f[3] = __uint_as_float(lo.w) * a.scale_log2;
+        f[4] = __uint_as_float(hi.x) * a.scale_log2;
+        f[5] = __uint_as_float(hi.y) * a.scale_log2;
+        f[6] = __uint_as_float(hi.z) * a.scale_log2;
+        f[7] = __uint_as_float(hi.w) * a.scale_log2;
+        qv[dk] = Mfma16<TKV>::from(f);
+      }
+    }
+  };
+
+  int r = 0;
+  int u = unit_at(0);
+  if (u < 0) return;
+  Unit cur;
+  describe(u, cur);
+  if (cur.kend > 0) fetch(cur, 0);
+  load_q(cur);
+  const bool o4 = a.out_dtype == (std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16) &&
+                  ((reinterpret_cast<uintptr_t>(a.out) & 7) | (a.o_sb & 3) | (a.o_sh & 3) | (a.o_st & 3)) == 0;
+  while (true) {
+    QVec qv[DK];
+    queries(qv);
+    // The next unit's descriptors are read now, so its first tile can be requested while
+    // this unit's last tile is multiplied.
+    const int un = unit_at(r + 1);
+    Unit nxt;
+    if (un >= 0) describe(un, nxt);
+    bool ahead = false;
+
+    f32x4 acc[DH];
+    float mrun = NEG_BIG, lsum = 0.f;
+#pragma unroll
+    for (int dh = 0; dh < DH; ++dh) acc[dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; kb < cur.kend; kb += KT) {
+      // ---- scores S^T[key, query] -------------------------------------------------------
+      f32x4 sc[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          QVec kvec;
+          __builtin_memcpy(&kvec, &kr[j][dk], 16);
+          s4 = Mfma16<TKV>::mma(kvec, qv[dk], s4);
+        }
+        sc[j] = QRAW ? s4 * a.scale_log2 : s4;
+      }
+      // ---- V rows -> LDS (as loaded), then the next tile: this unit's or the next unit's
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int dk = 0; dk < DK; ++dk) {
+          unsigned char *dst = vt + (16 * j + li) * ROW + (32 * dk + 8 * lg) * 2;
+          reinterpret_cast<uint2 *>(dst)[0] = uint2{vr[j][dk].x, vr[j][dk].y};
+          reinterpret_cast<uint2 *>(dst)[1] = uint2{vr[j][dk].z, vr[j][dk].w};
+        }
+      if (kb + KT < cur.kend) {
+        fetch(cur, kb + KT);
+      } else if (un >= 0) {
+        if (nxt.kend > 0) fetch(nxt, 0);
+        load_q(nxt);
+        ahead = true;
+      }
+      // ---- mask (only tiles reaching past some query's limit) ----------------------------
+      if (kb + KT > cur.kfull) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kb + 16 * j + 4 * lg + i >= cur.lim) sc[j][i] = -INFINITY;
+      }
+      // ---- online softmax per query column -----------------------------------------------
+      float p[NJ][4];
+      float tmax = NEG_BIG;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][i]);
+      tmax = xor32_max(xor16_max(tmax));
+      const float mnew = fmaxf(mrun, tmax);
+      const float corr = fast_exp2(mrun - mnew);
+      float psum = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[j][i] = fast_exp2(sc[j][i] - mnew);
+          psum += p[j][i];
+        }
+      lsum = fmaf(lsum, corr, psum);
+      mrun = mnew;
+#pragma unroll
+      for (int dh = 0; dh < DH; ++dh) acc[dh] *= corr;
+      // ---- O^T += V^T . P^T --------------------------------------------------------------
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int c = 0; c < KT / 32; ++c) {
+        QVec pv;
+        {
+          f32x8 f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = p[2 * c + (e >> 2)][e & 3];
+          pv = Mfma16<TKV>::from(f);
+        }
+#pragma unroll
+        for (int dh = 0; dh < DH; ++dh) {
+          const unsigned char *src = vt + (32 * c + 4 * lg + (li >> 2)) * ROW + (16 * dh + 4 * (li & 3)) * 2;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(src));
+          const s16x4 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)(src + 16 * ROW));
+          QVec vv;
+          __builtin_memcpy(&vv, &lo, 8);
+          __builtin_memcpy(reinterpret_cast<char *>(&vv) + 8, &hi, 8);
+          acc[dh] = Mfma16<TKV>::mma(vv, pv, acc[dh]);
+        }
+      }
+      // The next tile's V rows overwrite this one's only after every lane has read it.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
+    {
+      const float total = xor32_sum(xor16_sum(lsum));
+      if (li < nq) {
+        const float inv = total > 0.f ? 1.0f / total : 0.f;
+        const int64_t oo = cur.o_base + int64_t(li % G) * a.o_sh + int64_t(li / G) * a.o_st;
+        if (o4) {
+#pragma unroll
+          for (int dh = 0; dh < DH; ++dh) {
+            const TKV e0 = from_f32<TKV>(acc[dh][0] * inv), e1 = from_f32<TKV>(acc[dh][1] * inv);
+            const TKV e2 = from_f32<TKV>(acc[dh][2] * inv), e3 = from_f32<TKV>(acc[dh][3] * inv);
+            const uint64_t packed = uint64_t(e0.bits) | uint64_t(e1.bits) << 16 | uint64_t(e2.bits) << 32 |
+                                    uint64_t(e3.bits) << 48;
+            __builtin_nontemporal_store(packed, reinterpret_cast<uint64_t *>(static_cast<TKV *>(a.out) + oo + 16 * dh + 4 * lg));
+          }
+        } else {
+#pragma unroll
+          for (int dh = 0; dh < DH; ++dh)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[dh][i] * inv);
+        }
+      }
+    }
+    if (un < 0) break;
+    if (!ahead) {  // this unit had no key: nothing was requested for the next one yet
+      if (nxt.kend > 0) fetch(nxt, 0);
+      load_q(nxt);
+    }
+    cur = nxt;
+    ++r;
+  }
+}
+
+// order = the units sorted by descending tile count (attn_dev.h: order_units).  One block.
+__global__ __launch_bounds__(1024) void attention_order_kernel(const AttnArgs a, int32_t *__restrict__ order) {
+  order_units(a, order);
+}
+
 #ifndef TR_SPLIT
 #define TR_SPLIT 4
 #endif
@@ -932,6 +1221,27 @@ void launch_tr(const AttnArgs &a, int queries, hipStream_t s) {
   CG_LAUNCHED();
 }
 
+int attention_cus() {
+  static thread_local int dev = -1, cus = 256;
+  int d = 0;
+  if (hipGetDevice(&d) == hipSuccess && d != dev) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, d) == hipSuccess && n > 0) cus = n;
+    dev = d;
+  }
+  return cus;
+}
+
+// The persistent kernel: as many blocks of four waves per CU (one wave per SIMD each) as
+// its registers let reside, never more waves than units.
+template <typename TKV, int D, bool QRAW>
+void launch_stream(const AttnArgs &a, hipStream_t s) {
+  const int64_t units = int64_t(a.n_seqs) * a.kv_heads;
+  const int64_t blocks = std::min<int64_t>((units + 3) / 4, int64_t(attention_cus()) * stream_waves_per_eu<D>());
+  decode_attention_stream_kernel<TKV, D, QRAW><<<unsigned(blocks), 256, 0, s>>>(a);
+  CG_LAUNCHED();
+}
+
 template <typename TKV, int D>
 void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
   const unsigned grid = unsigned((int64_t(a.n_seqs) * a.kv_heads + 3) / 4);
@@ -939,9 +1249,11 @@ void launch_mfma(const AttnArgs &a, int queries, hipStream_t s) {
     CG_REQUIRE(int64_t(a.max_len) * D * 2 < (int64_t(1) << 31), CG_ERR_UNSUPPORTED,
                "decode attention: one cache row of one head must stay below 2 GiB");
     constexpr int KV_CODE = std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16;
-    if (a.q_dtype == KV_CODE &&
-        ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 7) | (a.q_sh & 7) | (a.q_st & 7)) == 0)
-      return launch_tr<TKV, D, true>(a, queries, s);
+    const bool qraw = a.q_dtype == KV_CODE &&
+                      ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 7) | (a.q_sh & 7) | (a.q_st & 7)) == 0;
+    if (a.order && attention_streams(a))
+      return qraw ? launch_stream<TKV, D, true>(a, s) : launch_stream<TKV, D, false>(a, s);
+    if (qraw) return launch_tr<TKV, D, true>(a, queries, s);
     return launch_tr<TKV, D, false>(a, queries, s);
   } else {
     if (queries <= 16) decode_attention_mfma_kernel<TKV, D, 1><<<grid, 256, 0, s>>>(a);
@@ -983,6 +1295,29 @@ void launch_kv(const AttnArgs &a, hipStream_t s) {
 
 }  // namespace
 
+// Spans from which the persistent kernel is taken.  Measured on MI355X (bf16 pool, head_dim
+// 32, 4 query heads per KV head): with up to 8-9 tiles per unit (config 3, span 538) both
+// kernels stream at the same rate (50.2 / 50.4 us per launch) and the order costs a launch
+// per step; with rows of up to 32 tiles and a wide spread of lengths (config 4, span 2048:
+// restarted games beside long ones) the split kernel's longest blocks finish last, and the
+// sorted deal takes 87.4 -> 80.8 us per launch (2.09 -> 1.98 ms per step).
+#ifndef STREAM_MIN_SPAN
+#define STREAM_MIN_SPAN 1024
+#endif
+
+bool attention_streams(const AttnArgs &a) {
+  return a.span >= STREAM_MIN_SPAN && (a.kv_dtype == CG_BF16 || a.kv_dtype == CG_F16) &&
+         (a.head_dim == 32 || a.head_dim == 64) && !a.seq_start && a.T >= 1 && a.kv_heads > 0 &&
+         a.n_heads % a.kv_heads == 0 && int64_t(a.n_heads / a.kv_heads) * a.T <= 16 &&
+         int64_t(a.max_len) * a.head_dim * 2 < (int64_t(1) << 31);
+}
+
+void launch_attention_order(const AttnArgs &a, int32_t *order, hipStream_t s) {
+  if (int64_t(a.n_seqs) * a.kv_heads <= 0) return;
+  attention_order_kernel<<<1, 1024, 0, s>>>(a, order);
+  CG_LAUNCHED();
+}
+
 void launch_decode_attention(const AttnArgs &a, hipStream_t s) {
   CG_REQUIRE(a.n_heads > 0 && a.kv_heads > 0 && a.n_heads % a.kv_heads == 0, CG_ERR_INVALID,
              "n_heads must be a positive multiple of kv_heads");
@@ -1003,11 +1338,56 @@ void launch_decode_attention(const AttnArgs &a, hipStream_t s) {
 
 using namespace cg;
 
+namespace {
+// The arguments of a padded run [B, n_heads, T, head_dim] (cg_decode_attention's layout).
+AttnArgs padded_args(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                     const cg_kv_layer *layer, const int64_t *rows, const int64_t *key_lengths, int32_t B,
+                     int32_t n_heads, int32_t T, int32_t span, float scale, void *out, int32_t out_dtype) {
+  AttnArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_st = q_st;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.o_st = layer->head_dim;
+  a.o_sh = int64_t(T) * layer->head_dim;
+  a.o_sb = int64_t(n_heads) * T * layer->head_dim;
+  a.k = layer->k;
+  a.v = layer->v;
+  a.kv_dtype = layer->dtype;
+  a.rows = rows;
+  a.key_lengths = key_lengths;
+  a.kl_add = 0;
+  a.seq_start = nullptr;
+  a.n_seqs = B;
+  a.n_heads = n_heads;
+  a.kv_heads = layer->kv_heads;
+  a.head_dim = layer->head_dim;
+  a.T = T;
+  a.max_len = layer->max_len;
+  a.capacity = layer->capacity;
+  a.span = (span <= 0 || span > layer->max_len) ? layer->max_len : span;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return a;
+}
+}  // namespace
+
 extern "C" int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_sh,
                                    int64_t q_st, const cg_kv_layer *layer, const int64_t *rows,
                                    const int64_t *key_lengths, int32_t B, int32_t n_heads,
                                    int32_t T, int32_t span, float scale, void *out,
                                    int32_t out_dtype, void *stream) {
+  return cg_decode_attention_ordered(q, q_dtype, q_sb, q_sh, q_st, layer, rows, key_lengths, B, n_heads, T, span,
+                                     scale, out, out_dtype, nullptr, stream);
+}
+
+extern "C" int cg_decode_attention_ordered(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_sh,
+                                           int64_t q_st, const cg_kv_layer *layer, const int64_t *rows,
+                                           const int64_t *key_lengths, int32_t B, int32_t n_heads, int32_t T,
+                                           int32_t span, float scale, void *out, int32_t out_dtype,
+                                           const int32_t *order, void *stream) {
   return guarded([&] {
     check_layer(layer);
     dtype_size(q_dtype);
@@ -1015,34 +1395,28 @@ extern "C" int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb,
     CG_REQUIRE(B >= 0 && T >= 0, CG_ERR_INVALID, "B and T must be non-negative");
     if (B == 0 || T == 0) return;  // empty tensors may carry NULL data pointers
     CG_REQUIRE(q && out && key_lengths, CG_ERR_INVALID, "q, out and key_lengths are required");
-    AttnArgs a{};
-    a.q = q;
-    a.q_dtype = q_dtype;
-    a.q_sb = q_sb;
-    a.q_sh = q_sh;
-    a.q_st = q_st;
-    a.out = out;
-    a.out_dtype = out_dtype;
-    a.o_st = layer->head_dim;
-    a.o_sh = int64_t(T) * layer->head_dim;
-    a.o_sb = int64_t(n_heads) * T * layer->head_dim;
-    a.k = layer->k;
-    a.v = layer->v;
-    a.kv_dtype = layer->dtype;
-    a.rows = rows;
-    a.key_lengths = key_lengths;
-    a.kl_add = 0;
-    a.seq_start = nullptr;
-    a.n_seqs = B;
-    a.n_heads = n_heads;
-    a.kv_heads = layer->kv_heads;
-    a.head_dim = layer->head_dim;
-    a.T = T;
-    a.max_len = layer->max_len;
-    a.capacity = layer->capacity;
-    a.span = (span <= 0 || span > layer->max_len) ? layer->max_len : span;
-    a.scale_log2 = scale * 1.4426950408889634f;
+    AttnArgs a = padded_args(q, q_dtype, q_sb, q_sh, q_st, layer, rows, key_lengths, B, n_heads, T, span, scale,
+                             out, out_dtype);
+    a.order = order;
     launch_decode_attention(a, as_stream(stream));
+  });
+}
+
+extern "C" int cg_decode_attention_order(const cg_kv_layer *layer, const int64_t *rows,
+                                         const int64_t *key_lengths, int32_t B, int32_t n_heads, int32_t T,
+                                         int32_t span, int32_t *order, int32_t *streams, void *stream) {
+  return guarded([&] {
+    check_layer(layer);
+    CG_REQUIRE(B >= 0 && T >= 0, CG_ERR_INVALID, "B and T must be non-negative");
+    CG_REQUIRE(n_heads > 0 && n_heads % layer->kv_heads == 0, CG_ERR_INVALID,
+               "n_heads must be a positive multiple of kv_heads");
+    AttnArgs a = padded_args(nullptr, CG_F32, 0, 0, 0, layer, rows, key_lengths, B, n_heads, T, span, 1.0f,
+                             nullptr, CG_F32);
+    const bool on = B > 0 && T > 0 && attention_streams(a);
+    if (streams) *streams = on ? 1 : 0;
+    if (!on) return;
+    CG_REQUIRE(order && key_lengths, CG_ERR_INVALID, "order and key_lengths are required");
+    launch_attention_order(a, order, as_stream(stream));
   });
 }
 

@@ -5,6 +5,7 @@
 // fused layer-step kernel (layer.hip).
 #pragma once
 
+#include "attention.h"
 #include "common.h"
 
 namespace cg {
@@ -115,6 +116,46 @@ __device__ __forceinline__ int row16_min(int v) {
   return v;
 }
 
+// ---- the unit order of the persistent decode-attention kernel ---------------------------
+constexpr int STREAM_KT = 64;       // keys per tile of the persistent kernel
+constexpr int ORDER_BUCKETS = 256;  // tile counts >= 255 share the last bucket
+
+// Tile count of a (row, KV head) unit: its widest query's visible keys, in 64-key tiles.
+__device__ __forceinline__ int unit_tiles(const AttnArgs &a, int u) {
+  const int b = u / a.kv_heads;
+  const int64_t row = a.rows ? a.rows[b] : int64_t(b);
+  int64_t kend = a.key_lengths[b] + a.kl_add + (a.T - 1);
+  if (kend > a.span) kend = a.span;
+  if (row < 0 || row >= a.capacity || kend < 0) kend = 0;
+  return int(min<int64_t>(ORDER_BUCKETS - 1, (kend + STREAM_KT - 1) / STREAM_KT));
+}
+
+// order = the units sorted by descending tile count: a counting sort by one whole block
+// (any size; ties land in any order, which changes only which wave computes a unit, not its
+// result).  Called by every thread of the block.
+__device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restrict__ order) {
+  __shared__ int hist[ORDER_BUCKETS], scan[2][ORDER_BUCKETS];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int U = a.n_seqs * a.kv_heads;
+  for (int i = tid; i < ORDER_BUCKETS; i += nt) hist[i] = 0;
+  __syncthreads();
+  for (int u = tid; u < U; u += nt) atomicAdd(&hist[unit_tiles(a, u)], 1);
+  __syncthreads();
+  // Exclusive suffix sums (bucket k starts after every larger bucket): Hillis-Steele over
+  // the reversed histogram.
+  int src = 0;
+  for (int i = tid; i < ORDER_BUCKETS; i += nt) scan[0][i] = hist[ORDER_BUCKETS - 1 - i];
+  __syncthreads();
+  for (int off = 1; off < ORDER_BUCKETS; off <<= 1) {
+    for (int i = tid; i < ORDER_BUCKETS; i += nt) scan[src ^ 1][i] = scan[src][i] + (i >= off ? scan[src][i - off] : 0);
+    __syncthreads();
+    src ^= 1;
+  }
+  // scan[src][i]: inclusive sum of reversed buckets 0..i, i.e. of buckets K - 1 - i .. K - 1.
+  for (int k = tid; k < ORDER_BUCKETS; k += nt) hist[k] = scan[src][ORDER_BUCKETS - 1 - k] - hist[k];
+  __syncthreads();
+  for (int u = tid; u < U; u += nt) order[atomicAdd(&hist[unit_tiles(a, u)], 1)] = u;
+}
 
 }  // namespace
 }  // namespace cg

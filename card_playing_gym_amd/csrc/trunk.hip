@@ -48,6 +48,7 @@ struct Workspace {
   int32_t *tok_pos;
   int32_t *readout_tok;
   int32_t *tok_out;
+  int32_t *order;  // (row, KV head) units by descending key tiles (the persistent attention)
   size_t bytes;
 };
 
@@ -70,6 +71,7 @@ Workspace carve(const cg_trunk &t, int32_t n_tokens, int32_t n_seqs, char *base)
   w.tok_pos = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
   w.readout_tok = reinterpret_cast<int32_t *>(take(size_t(n_seqs > 0 ? n_seqs : 1) * 4));
   w.tok_out = reinterpret_cast<int32_t *>(take(size_t(n_tokens) * 4));
+  w.order = reinterpret_cast<int32_t *>(take(size_t(n_seqs > 0 ? n_seqs : 1) * t.cfg.n_kv_heads * 4));
   w.bytes = off;
   return w;
 }
@@ -346,14 +348,6 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
   const int span = (r.span <= 0 || r.span > max_len) ? max_len : r.span;
   const int act_dtype = t.compute == CG_BF16 ? CG_BF16 : CG_F32;
 
-  {
-    const int n = N > r.n_seqs ? N : r.n_seqs;
-    plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout,
-                                                r.n_seqs, N, r.T, max_len, cache[0].capacity,
-                                                w.tok_row, w.tok_pos, w.readout_tok, w.tok_out,
-                                                hidden, d);
-    CG_LAUNCHED();
-  }
   const float ple_scale = [&] {
     if (c.per_layer_dim == 0 || c.per_layer_dim == d) return 1.0f;
     const int repeats = (d + c.per_layer_dim - 1) / c.per_layer_dim;
@@ -367,39 +361,53 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
   // projections of the unfused path write fp32.
   const bool multi_query = r.seq_start != nullptr || int64_t(H / KVH) * r.T > 16;
   const int q_dtype = (t.fused && multi_query && cache[0].dtype != CG_F32) ? cache[0].dtype : CG_F32;
-  auto attention = [&](int l) {
+  auto attn_args = [&](int l) {
     const cg_kv_layer &L = cache[l];
-    {
-      AttnArgs a{};
-      a.q = w.q;
-      a.q_dtype = q_dtype;
-      a.q_st = int64_t(H) * D;
-      a.q_sh = D;
-      a.q_sb = int64_t(r.T) * H * D;
-      a.out = w.attn;
-      a.out_dtype = act_dtype;
-      a.o_st = int64_t(H) * D;
-      a.o_sh = D;
-      a.o_sb = int64_t(r.T) * H * D;
-      a.k = L.k;
-      a.v = L.v;
-      a.kv_dtype = L.dtype;
-      a.rows = r.rows;
-      a.key_lengths = r.positions;
-      a.kl_add = 1;
-      a.seq_start = r.seq_start;
-      a.n_tokens = N;
-      a.n_seqs = r.n_seqs;
-      a.n_heads = H;
-      a.kv_heads = KVH;
-      a.head_dim = D;
-      a.T = r.T;
-      a.max_len = max_len;
-      a.capacity = L.capacity;
-      a.span = span;
-      a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
-      launch_decode_attention(a, s);
-    }
+    AttnArgs a{};
+    a.q = w.q;
+    a.q_dtype = q_dtype;
+    a.q_st = int64_t(H) * D;
+    a.q_sh = D;
+    a.q_sb = int64_t(r.T) * H * D;
+    a.out = w.attn;
+    a.out_dtype = act_dtype;
+    a.o_st = int64_t(H) * D;
+    a.o_sh = D;
+    a.o_sb = int64_t(r.T) * H * D;
+    a.k = L.k;
+    a.v = L.v;
+    a.kv_dtype = L.dtype;
+    a.rows = r.rows;
+    a.key_lengths = r.positions;
+    a.kl_add = 1;
+    a.seq_start = r.seq_start;
+    a.n_tokens = N;
+    a.n_seqs = r.n_seqs;
+    a.n_heads = H;
+    a.kv_heads = KVH;
+    a.head_dim = D;
+    a.T = r.T;
+    a.max_len = max_len;
+    a.capacity = L.capacity;
+    a.span = span;
+    a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
+    return a;
+  };
+  {
+    const int n = N > r.n_seqs ? N : r.n_seqs;
+    plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout, r.n_seqs, N, r.T,
+                                                max_len, cache[0].capacity, w.tok_row, w.tok_pos, w.readout_tok,
+                                                w.tok_out, hidden, d);
+    CG_LAUNCHED();
+  }
+  // Decode runs with long possible rows take the persistent attention kernel, whose unit
+  // order (by key tiles) is the same for every layer of the step: computed once here.
+  const bool streams = attention_streams(attn_args(0));
+  if (streams) launch_attention_order(attn_args(0), w.order, s);
+  auto attention = [&](int l) {
+    AttnArgs a = attn_args(l);
+    a.order = streams ? w.order : nullptr;
+    launch_decode_attention(a, s);
   };
 
   const int n_qkv = (H + 2 * KVH) * D;

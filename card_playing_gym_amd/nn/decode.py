@@ -44,9 +44,12 @@ def attention_into(
     key_lengths: torch.Tensor,
     span: int,
     scale: float,
+    order: torch.Tensor | None = None,
 ) -> None:
     """Writes attention of q [B, H, T, D] (any strides, unit last stride) into out
-    [B, H, T, D] (contiguous)."""
+    [B, H, T, D] (contiguous).  ``order`` (from :func:`attention_order` for the same rows,
+    key lengths, T and span) makes decode runs take the persistent kernel, as the trunk
+    step does."""
 
     import ctypes
 
@@ -58,11 +61,43 @@ def attention_into(
     lengths = key_lengths.to(torch.int64).contiguous()
     batch, heads, steps, _ = q.shape
     layer = _layer(k, v)
+    if order is not None and (order.dtype != torch.int32 or order.numel() < batch * k.shape[1]):
+        raise ValueError("order must be an int32 tensor of batch * kv_heads entries (attention_order)")
     nat.call(
-        "cg_decode_attention", q.data_ptr(), dtype_code(q.dtype), q.stride(0), q.stride(1), q.stride(2),
+        "cg_decode_attention_ordered", q.data_ptr(), dtype_code(q.dtype), q.stride(0), q.stride(1), q.stride(2),
         ctypes.byref(layer), None if rows is None else rows.data_ptr(), lengths.data_ptr(), batch, heads,
-        steps, int(span), float(scale), out.data_ptr(), dtype_code(out.dtype), stream_handle(q.device),
+        steps, int(span), float(scale), out.data_ptr(), dtype_code(out.dtype),
+        None if order is None else order.data_ptr(), stream_handle(q.device),
     )
+
+
+def attention_order(
+    k: torch.Tensor,
+    rows: torch.Tensor | None,
+    key_lengths: torch.Tensor,
+    batch: int,
+    heads: int,
+    steps: int,
+    span: int,
+) -> torch.Tensor | None:
+    """The (row, KV head) units of a padded run sorted by key tiles (int32 [batch * kv_heads]),
+    for :func:`attention_into`; None when the persistent kernel does not apply (fp32 pool,
+    head_dim other than 32 / 64, more than 16 queries per unit, span below 1024 keys)."""
+
+    import ctypes
+
+    require_device(k, key_lengths)
+    if rows is not None and (rows.dtype != torch.int64 or not rows.is_contiguous()):
+        rows = rows.to(torch.int64).contiguous()
+    lengths = key_lengths.to(torch.int64).contiguous()
+    layer = _layer(k, k)
+    order = torch.empty(max(batch * k.shape[1], 1), dtype=torch.int32, device=k.device)
+    streams = ctypes.c_int32(0)
+    nat.call(
+        "cg_decode_attention_order", ctypes.byref(layer), None if rows is None else rows.data_ptr(), lengths.data_ptr(),
+        batch, heads, steps, int(span), order.data_ptr(), ctypes.byref(streams), stream_handle(k.device),
+    )
+    return order if streams.value else None
 
 
 def attention_packed_into(

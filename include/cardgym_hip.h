@@ -140,6 +140,23 @@ int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_
                         int32_t B, int32_t n_heads, int32_t T, int32_t span, float scale, void *out,
                         int32_t out_dtype, void *stream);
 
+/* cg_decode_attention with a work order, as the trunk step launches it for decode waves
+ * (same op and meaning, cardgym/nn/cuda_decode.py:188-202).  cg_decode_attention_order
+ * writes order (int32 [B * kv_heads]: the (row, KV head) units sorted by their number of
+ * 64-key tiles, longest first) for these rows, key lengths, T and span, and sets *streams
+ * (if not NULL) to 1 when the persistent kernel applies (16-bit pool, head_dim 32 or 64,
+ * G * T <= 16 queries per unit, span of at least 1024 keys: below it both kernels stream at
+ * the same rate) -- otherwise it writes nothing and the ordered call runs the split kernel.  The order stays valid for every layer and call with the same rows,
+ * key lengths, T and span; results do not depend on it beyond its being a permutation of
+ * the units. */
+int cg_decode_attention_order(const cg_kv_layer *layer, const int64_t *rows, const int64_t *key_lengths,
+                              int32_t B, int32_t n_heads, int32_t T, int32_t span, int32_t *order,
+                              int32_t *streams, void *stream);
+int cg_decode_attention_ordered(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                                const cg_kv_layer *layer, const int64_t *rows, const int64_t *key_lengths,
+                                int32_t B, int32_t n_heads, int32_t T, int32_t span, float scale, void *out,
+                                int32_t out_dtype, const int32_t *order, void *stream);
+
 /* The packed-row form of cg_decode_attention, as the trunk step launches it: the
  * chunks of cardgym/nn/packing.py:36-40 ([start, end) bounds) instead of a padded run, with
  * the visibility rule of DecoderBlock.forward_ragged / _grouped_attention
