@@ -559,8 +559,12 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
 // QRAW: the queries are stored in the cache type (16-byte aligned rows); they load as they
 // are and the softmax scale multiplies the fp32 scores.  Otherwise any query type is read,
 // scaled and rounded to the cache type.
+// Waves per SIMD the split kernel is built for: multi-tile forms at head_dim 32 keep two.
+template <int NQT, int D>
+constexpr int tr_waves_per_eu() { return D == 32 ? (NQT == 1 ? TR_WAVES_PER_EU : 2) : 1; }
+
 template <typename TKV, int D, int NQT, int SPLIT, int KT, int DEPTH, bool QRAW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NQT == 1 && D == 32 ? TR_WAVES_PER_EU : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(tr_waves_per_eu<NQT, D>())))
 void decode_attention_tr_kernel(AttnArgs a) {
   static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "a block holds 4 / SPLIT whole units");
   static_assert(KT % 32 == 0, "key tiles are whole 32-key MFMA steps");
@@ -632,258 +636,276 @@ void decode_attention_tr_kernel(AttnArgs a) {
     const int kend = __builtin_amdgcn_readfirstlane(row16_max(kmax));
     const int kfull = __builtin_amdgcn_readfirstlane(row16_min(kmin));
 
-    // Lane l holds key 16 j + l % 16 of a tile at dims 32 dk + 8 (l / 16), for K and V.
-    uint4 kr[DEPTH][NJ][DK], vr[DEPTH][NJ][DK];
-    auto fetch = [&](int st, int kb) {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int key = min(kb + 16 * j + li, kend - 1);
-#pragma unroll
-        for (int dk = 0; dk < DK; ++dk) {
-          const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
-          kr[st][j][dk] = kv_load16(kres, off);
-          vr[st][j][dk] = kv_load16(vres, off);
+    // Only the query tiles holding a query of the group run (a packed chunk of a few tokens
+    // fills one or two of four): the group's body is instantiated for each live-tile count,
+    // so every tile loop keeps a compile-time bound.
+    const int live = (nq - qg + 15) / 16;
+    auto group = [&](auto live_tiles) {
+    constexpr int L = decltype(live_tiles)::value;
+      // Lane l holds key 16 j + l % 16 of a tile at dims 32 dk + 8 (l / 16), for K and V.
+      uint4 kr[DEPTH][NJ][DK], vr[DEPTH][NJ][DK];
+      auto fetch = [&](int st, int kb) {
+  #pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int key = min(kb + 16 * j + li, kend - 1);
+  #pragma unroll
+          for (int dk = 0; dk < DK; ++dk) {
+            const uint32_t off = uint32_t(key * D + 32 * dk + 8 * lg) * 2;
+            kr[st][j][dk] = kv_load16(kres, off);
+            vr[st][j][dk] = kv_load16(vres, off);
+          }
+        }
+      };
+      // The first DEPTH key tiles are requested before the queries, so the latencies overlap.
+      if (part * KT < kend) {
+  #pragma unroll
+        for (int st = 0; st < DEPTH; ++st) fetch(st, part * KT + st * SPLIT * KT);
+      }
+
+      // ---- queries.  QRAW: already rounded to the cache type unscaled, as the reference rounds
+      //      q (q.to(cache.dtype), trunk.py:222), loaded 16 bytes per 8 dims; the scale (times
+      //      log2 e) then multiplies the fp32 scores.  Otherwise scaled by the softmax scale *
+      //      log2 e and rounded to the cache type; fp32 rows at 16-byte alignment load as two
+      //      float4 per 8 dims. ----------------------------------------------------------------
+      const bool q4 = !QRAW && a.q_dtype == CG_F32 &&
+                      ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 3) | (a.q_sh & 3) | (a.q_st & 3) | (q_base & 3)) == 0;
+      typename Mfma16<TKV>::vec qv[NQT][DK];
+  #pragma unroll
+      for (int qt = 0; qt < L; ++qt) {
+        const int m = qg + 16 * qt + li;
+        if constexpr (QRAW) {
+  #pragma unroll
+          for (int dk = 0; dk < DK; ++dk) {
+            if (m < nq) {
+              const int64_t qo = q_base + int64_t(h * G + m % G) * a.q_sh + int64_t(m / G) * a.q_st;
+              qv[qt][dk] = *reinterpret_cast<const typename Mfma16<TKV>::vec *>(static_cast<const TKV *>(a.q) + qo +
+                                                                                 32 * dk + 8 * lg);
+            } else {
+              f32x8 z;
+  #pragma unroll
+              for (int e = 0; e < 8; ++e) z[e] = 0.f;
+              qv[qt][dk] = Mfma16<TKV>::from(z);
+            }
+          }
+          continue;
+        }
+        f32x8 f[DK];
+        if (m < nq) {
+          const int t = m / G, g = m % G;
+          const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st;
+          if (q4) {
+  #pragma unroll
+            for (int dk = 0; dk < DK; ++dk) {
+              const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.q) + qo + 32 * dk + 8 * lg);
+              const float4 x0 = src[0], x1 = src[1];
+              f[dk][0] = x0.x * a.scale_log2;
+              f[dk][1] = x0.y * a.scale_log2;
+              f[dk][2] = x0.z * a.scale_log2;
+              f[dk][3] = x0.w * a.scale_log2;
+              f[dk][4] = x1.x * a.scale_log2;
+              f[dk][5] = x1.y * a.scale_log2;
+              f[dk][6] = x1.z * a.scale_log2;
+              f[dk][7] = x1.w * a.scale_log2;
+            }
+          } else {
+  #pragma unroll
+            for (int dk = 0; dk < DK; ++dk)
+  #pragma unroll
+              for (int e = 0; e < 8; ++e) f[dk][e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e) * a.scale_log2;
+          }
+        } else {
+  #pragma unroll
+          for (int dk = 0; dk < DK; ++dk)
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) f[dk][e] = 0.f;
+        }
+  #pragma unroll
+        for (int dk = 0; dk < DK; ++dk) qv[qt][dk] = Mfma16<TKV>::from(f[dk]);
+      }
+
+      f32x4 acc[NQT][DH];
+      float mrun[NQT], lsum[NQT];
+  #pragma unroll
+      for (int qt = 0; qt < L; ++qt) {
+        mrun[qt] = NEG_BIG;
+        lsum[qt] = 0.f;
+  #pragma unroll
+        for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+
+      for (int kb0 = part * KT; kb0 < kend; kb0 += DEPTH * SPLIT * KT) {
+  #pragma unroll
+       for (int st = 0; st < DEPTH; ++st) {
+        const int kb = kb0 + st * SPLIT * KT;
+        if (st > 0 && kb >= kend) break;
+        // ---- scores S^T[key, query] -----------------------------------------------------
+        f32x4 sc[NQT][NJ];
+  #pragma unroll
+        for (int qt = 0; qt < L; ++qt)
+  #pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+            for (int dk = 0; dk < DK; ++dk) {
+              typename Mfma16<TKV>::vec kvec;
+              __builtin_memcpy(&kvec, &kr[st][j][dk], 16);
+              s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
+            }
+            sc[qt][j] = QRAW ? s4 * a.scale_log2 : s4;
+          }
+        // ---- V rows -> LDS (as loaded), then the next tile's loads ----------------------
+  #pragma unroll
+        for (int j = 0; j < NJ; ++j)
+  #pragma unroll
+          for (int dk = 0; dk < DK; ++dk) {
+            unsigned char *dst = vt + (16 * j + li) * ROW + (32 * dk + 8 * lg) * 2;
+            reinterpret_cast<uint2 *>(dst)[0] = uint2{vr[st][j][dk].x, vr[st][j][dk].y};
+            reinterpret_cast<uint2 *>(dst)[1] = uint2{vr[st][j][dk].z, vr[st][j][dk].w};
+          }
+        fetch(st, kb + DEPTH * SPLIT * KT);  // clamped: past kend it re-reads the last visible key
+
+        // ---- mask (only tiles reaching past some query's limit) --------------------------
+        if (kb + KT > kfull) {
+  #pragma unroll
+          for (int qt = 0; qt < L; ++qt)
+  #pragma unroll
+            for (int j = 0; j < NJ; ++j)
+  #pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (kb + 16 * j + 4 * lg + i >= lim[qt]) sc[qt][j][i] = -INFINITY;
+        }
+        // ---- online softmax per query column ----------------------------------------------
+        float p[NQT][NJ][4];
+  #pragma unroll
+        for (int qt = 0; qt < L; ++qt) {
+          float tmax = NEG_BIG;
+  #pragma unroll
+          for (int j = 0; j < NJ; ++j)
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[qt][j][i]);
+          tmax = xor32_max(xor16_max(tmax));
+          const float mnew = fmaxf(mrun[qt], tmax);
+          const float corr = fast_exp2(mrun[qt] - mnew);
+          float psum = 0.f;
+  #pragma unroll
+          for (int j = 0; j < NJ; ++j)
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              p[qt][j][i] = fast_exp2(sc[qt][j][i] - mnew);
+              psum += p[qt][j][i];
+            }
+          lsum[qt] = fmaf(lsum[qt], corr, psum);
+          mrun[qt] = mnew;
+  #pragma unroll
+          for (int dh = 0; dh < DH; ++dh) acc[qt][dh] *= corr;
+        }
+        // ---- O^T += V^T . P^T (k slot 8 (l / 16) + e of chunk c is key
+        //      32 c + 16 (e / 4) + 4 (l / 16) + e % 4) ------------------------------------------
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  #pragma unroll
+        for (int c = 0; c < KT / 32; ++c) {
+          typename Mfma16<TKV>::vec pv[NQT];
+  #pragma unroll
+          for (int qt = 0; qt < L; ++qt) {
+            f32x8 f;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = p[qt][2 * c + (e >> 2)][e & 3];
+            pv[qt] = Mfma16<TKV>::from(f);
+          }
+  #pragma unroll
+          for (int dh = 0; dh < DH; ++dh) {
+            const unsigned char *src = vt + (32 * c + 4 * lg + (li >> 2)) * ROW + (16 * dh + 4 * (li & 3)) * 2;
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(src));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4 *)(src + 16 * ROW));
+            typename Mfma16<TKV>::vec vv;
+            __builtin_memcpy(&vv, &lo, 8);
+            __builtin_memcpy(reinterpret_cast<char *>(&vv) + 8, &hi, 8);
+  #pragma unroll
+            for (int qt = 0; qt < L; ++qt) acc[qt][dh] = Mfma16<TKV>::mma(vv, pv[qt], acc[qt][dh]);
+          }
+        }
+       }
+      }
+
+      if constexpr (SPLIT > 1) {
+        // ---- merge the unit's SPLIT partial softmax states (log-sum-exp) ------------------
+  #pragma unroll
+        for (int qt = 0; qt < L; ++qt) {
+          lsum[qt] = xor32_sum(xor16_sum(lsum[qt]));
+          if (lg == 0) {
+            part_m[wave][qt][li] = mrun[qt];
+            part_l[wave][qt][li] = lsum[qt];
+          }
+  #pragma unroll
+          for (int dh = 0; dh < DH; ++dh) part_o[wave][qt][dh][lane] = acc[qt][dh];
+        }
+        __syncthreads();
+        if (part == 0) {
+  #pragma unroll
+          for (int qt = 0; qt < L; ++qt) {
+            float mm = part_m[wave][qt][li];
+  #pragma unroll
+            for (int w = 1; w < SPLIT; ++w) mm = fmaxf(mm, part_m[wave + w][qt][li]);
+            float l = 0.f;
+  #pragma unroll
+            for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+            for (int w = 0; w < SPLIT; ++w) {
+              const float c = fast_exp2(part_m[wave + w][qt][li] - mm);
+              l = fmaf(part_l[wave + w][qt][li], c, l);
+  #pragma unroll
+              for (int dh = 0; dh < DH; ++dh) acc[qt][dh] += part_o[wave + w][qt][dh][lane] * c;
+            }
+            lsum[qt] = l;
+          }
+        }
+        __syncthreads();  // partials consumed before the next query group reuses them
+        if (part != 0) return;
+      }
+      // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
+      const bool o4 = a.out_dtype == (sizeof(TKV) == 2 && std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16) &&
+                      ((reinterpret_cast<uintptr_t>(a.out) & 7) | (a.o_sb & 3) | (a.o_sh & 3) | (a.o_st & 3) | (o_base & 3)) == 0;
+  #pragma unroll
+      for (int qt = 0; qt < L; ++qt) {
+        const float total = SPLIT > 1 ? lsum[qt] : xor32_sum(xor16_sum(lsum[qt]));
+        const int m = qg + 16 * qt + li;
+        if (m >= nq || !unit_ok) continue;
+        const int t = m / G, g = m % G;
+        const float inv = total > 0.f ? 1.0f / total : 0.f;
+        const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st;
+        if (o4) {
+          // 16-bit output: each lane's 4 consecutive dims as one 8-byte non-temporal store (a
+          // dirty line left in L2 is written back while the next kernel streams).
+  #pragma unroll
+          for (int dh = 0; dh < DH; ++dh) {
+            const TKV e0 = from_f32<TKV>(acc[qt][dh][0] * inv), e1 = from_f32<TKV>(acc[qt][dh][1] * inv);
+            const TKV e2 = from_f32<TKV>(acc[qt][dh][2] * inv), e3 = from_f32<TKV>(acc[qt][dh][3] * inv);
+            const uint64_t packed = uint64_t(e0.bits) | uint64_t(e1.bits) << 16 | uint64_t(e2.bits) << 32 |
+                                    uint64_t(e3.bits) << 48;
+            __builtin_nontemporal_store(packed, reinterpret_cast<uint64_t *>(static_cast<TKV *>(a.out) + oo + 16 * dh + 4 * lg));
+          }
+        } else {
+  #pragma unroll
+          for (int dh = 0; dh < DH; ++dh)
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[qt][dh][i] * inv);
         }
       }
     };
-    // The first DEPTH key tiles are requested before the queries, so the latencies overlap.
-    if (part * KT < kend) {
-#pragma unroll
-      for (int st = 0; st < DEPTH; ++st) fetch(st, part * KT + st * SPLIT * KT);
-    }
-
-    // ---- queries.  QRAW: already rounded to the cache type unscaled, as the reference rounds
-    //      q (q.to(cache.dtype), trunk.py:222), loaded 16 bytes per 8 dims; the scale (times
-    //      log2 e) then multiplies the fp32 scores.  Otherwise scaled by the softmax scale *
-    //      log2 e and rounded to the cache type; fp32 rows at 16-byte alignment load as two
-    //      float4 per 8 dims. ----------------------------------------------------------------
-    const bool q4 = !QRAW && a.q_dtype == CG_F32 &&
-                    ((reinterpret_cast<uintptr_t>(a.q) & 15) | (a.q_sb & 3) | (a.q_sh & 3) | (a.q_st & 3) | (q_base & 3)) == 0;
-    typename Mfma16<TKV>::vec qv[NQT][DK];
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-      const int m = qg + 16 * qt + li;
-      if constexpr (QRAW) {
-#pragma unroll
-        for (int dk = 0; dk < DK; ++dk) {
-          if (m < nq) {
-            const int64_t qo = q_base + int64_t(h * G + m % G) * a.q_sh + int64_t(m / G) * a.q_st;
-            qv[qt][dk] = *reinterpret_cast<const typename Mfma16<TKV>::vec *>(static_cast<const TKV *>(a.q) + qo +
-                                                                               32 * dk + 8 * lg);
-          } else {
-            f32x8 z;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) z[e] = 0.f;
-            qv[qt][dk] = Mfma16<TKV>::from(z);
-          }
-        }
-        continue;
-      }
-      f32x8 f[DK];
-      if (m < nq) {
-        const int t = m / G, g = m % G;
-        const int64_t qo = q_base + int64_t(h * G + g) * a.q_sh + int64_t(t) * a.q_st;
-        if (q4) {
-#pragma unroll
-          for (int dk = 0; dk < DK; ++dk) {
-            const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(a.q) + qo + 32 * dk + 8 * lg);
-            const float4 x0 = src[0], x1 = src[1];
-            f[dk][0] = x0.x * a.scale_log2;
-            f[dk][1] = x0.y * a.scale_log2;
-            f[dk][2] = x0.z * a.scale_log2;
-            f[dk][3] = x0.w * a.scale_log2;
-            f[dk][4] = x1.x * a.scale_log2;
-            f[dk][5] = x1.y * a.scale_log2;
-            f[dk][6] = x1.z * a.scale_log2;
-            f[dk][7] = x1.w * a.scale_log2;
-          }
-        } else {
-#pragma unroll
-          for (int dk = 0; dk < DK; ++dk)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) f[dk][e] = load_any(a.q, a.q_dtype, qo + 32 * dk + 8 * lg + e) * a.scale_log2;
-        }
-      } else {
-#pragma unroll
-        for (int dk = 0; dk < DK; ++dk)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[dk][e] = 0.f;
-      }
-#pragma unroll
-      for (int dk = 0; dk < DK; ++dk) qv[qt][dk] = Mfma16<TKV>::from(f[dk]);
-    }
-
-    f32x4 acc[NQT][DH];
-    float mrun[NQT], lsum[NQT];
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-      mrun[qt] = NEG_BIG;
-      lsum[qt] = 0.f;
-#pragma unroll
-      for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    for (int kb0 = part * KT; kb0 < kend; kb0 += DEPTH * SPLIT * KT) {
-#pragma unroll
-     for (int st = 0; st < DEPTH; ++st) {
-      const int kb = kb0 + st * SPLIT * KT;
-      if (st > 0 && kb >= kend) break;
-      // ---- scores S^T[key, query] -----------------------------------------------------
-      f32x4 sc[NQT][NJ];
-#pragma unroll
-      for (int qt = 0; qt < NQT; ++qt)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          f32x4 s4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int dk = 0; dk < DK; ++dk) {
-            typename Mfma16<TKV>::vec kvec;
-            __builtin_memcpy(&kvec, &kr[st][j][dk], 16);
-            s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
-          }
-          sc[qt][j] = QRAW ? s4 * a.scale_log2 : s4;
-        }
-      // ---- V rows -> LDS (as loaded), then the next tile's loads ----------------------
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int dk = 0; dk < DK; ++dk) {
-          unsigned char *dst = vt + (16 * j + li) * ROW + (32 * dk + 8 * lg) * 2;
-          reinterpret_cast<uint2 *>(dst)[0] = uint2{vr[st][j][dk].x, vr[st][j][dk].y};
-          reinterpret_cast<uint2 *>(dst)[1] = uint2{vr[st][j][dk].z, vr[st][j][dk].w};
-        }
-      fetch(st, kb + DEPTH * SPLIT * KT);  // clamped: past kend it re-reads the last visible key
-
-      // ---- mask (only tiles reaching past some query's limit) --------------------------
-      if (kb + KT > kfull) {
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt)
-#pragma unroll
-          for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (kb + 16 * j + 4 * lg + i >= lim[qt]) sc[qt][j][i] = -INFINITY;
-      }
-      // ---- online softmax per query column ----------------------------------------------
-      float p[NQT][NJ][4];
-#pragma unroll
-      for (int qt = 0; qt < NQT; ++qt) {
-        float tmax = NEG_BIG;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[qt][j][i]);
-        tmax = xor32_max(xor16_max(tmax));
-        const float mnew = fmaxf(mrun[qt], tmax);
-        const float corr = fast_exp2(mrun[qt] - mnew);
-        float psum = 0.f;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            p[qt][j][i] = fast_exp2(sc[qt][j][i] - mnew);
-            psum += p[qt][j][i];
-          }
-        lsum[qt] = fmaf(lsum[qt], corr, psum);
-        mrun[qt] = mnew;
-#pragma unroll
-        for (int dh = 0; dh < DH; ++dh) acc[qt][dh] *= corr;
-      }
-      // ---- O^T += V^T . P^T (k slot 8 (l / 16) + e of chunk c is key
-      //      32 c + 16 (e / 4) + 4 (l / 16) + e % 4) ------------------------------------------
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int c = 0; c < KT / 32; ++c) {
-        typename Mfma16<TKV>::vec pv[NQT];
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-          f32x8 f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = p[qt][2 * c + (e >> 2)][e & 3];
-          pv[qt] = Mfma16<TKV>::from(f);
-        }
-#pragma unroll
-        for (int dh = 0; dh < DH; ++dh) {
-          const unsigned char *src = vt + (32 * c + 4 * lg + (li >> 2)) * ROW + (16 * dh + 4 * (li & 3)) * 2;
-          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4 *)(src));
-          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) s16x4 *)(src + 16 * ROW));
-          typename Mfma16<TKV>::vec vv;
-          __builtin_memcpy(&vv, &lo, 8);
-          __builtin_memcpy(reinterpret_cast<char *>(&vv) + 8, &hi, 8);
-#pragma unroll
-          for (int qt = 0; qt < NQT; ++qt) acc[qt][dh] = Mfma16<TKV>::mma(vv, pv[qt], acc[qt][dh]);
-        }
-      }
-     }
-    }
-
-    if constexpr (SPLIT > 1) {
-      // ---- merge the unit's SPLIT partial softmax states (log-sum-exp) ------------------
-#pragma unroll
-      for (int qt = 0; qt < NQT; ++qt) {
-        lsum[qt] = xor32_sum(xor16_sum(lsum[qt]));
-        if (lg == 0) {
-          part_m[wave][qt][li] = mrun[qt];
-          part_l[wave][qt][li] = lsum[qt];
-        }
-#pragma unroll
-        for (int dh = 0; dh < DH; ++dh) part_o[wave][qt][dh][lane] = acc[qt][dh];
-      }
-      __syncthreads();
-      if (part == 0) {
-#pragma unroll
-        for (int qt = 0; qt < NQT; ++qt) {
-          float mm = part_m[wave][qt][li];
-#pragma unroll
-          for (int w = 1; w < SPLIT; ++w) mm = fmaxf(mm, part_m[wave + w][qt][li]);
-          float l = 0.f;
-#pragma unroll
-          for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int w = 0; w < SPLIT; ++w) {
-            const float c = fast_exp2(part_m[wave + w][qt][li] - mm);
-            l = fmaf(part_l[wave + w][qt][li], c, l);
-#pragma unroll
-            for (int dh = 0; dh < DH; ++dh) acc[qt][dh] += part_o[wave + w][qt][dh][lane] * c;
-          }
-          lsum[qt] = l;
-        }
-      }
-      __syncthreads();  // partials consumed before the next query group reuses them
-      if (part != 0) continue;
-    }
-    // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
-    const bool o4 = a.out_dtype == (sizeof(TKV) == 2 && std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16) &&
-                    ((reinterpret_cast<uintptr_t>(a.out) & 7) | (a.o_sb & 3) | (a.o_sh & 3) | (a.o_st & 3) | (o_base & 3)) == 0;
-#pragma unroll
-    for (int qt = 0; qt < NQT; ++qt) {
-      const float total = SPLIT > 1 ? lsum[qt] : xor32_sum(xor16_sum(lsum[qt]));
-      const int m = qg + 16 * qt + li;
-      if (m >= nq || !unit_ok) continue;
-      const int t = m / G, g = m % G;
-      const float inv = total > 0.f ? 1.0f / total : 0.f;
-      const int64_t oo = o_base + int64_t(h * G + g) * a.o_sh + int64_t(t) * a.o_st;
-      if (o4) {
-        // 16-bit output: each lane's 4 consecutive dims as one 8-byte non-temporal store (a
-        // dirty line left in L2 is written back while the next kernel streams).
-#pragma unroll
-        for (int dh = 0; dh < DH; ++dh) {
-          const TKV e0 = from_f32<TKV>(acc[qt][dh][0] * inv), e1 = from_f32<TKV>(acc[qt][dh][1] * inv);
-          const TKV e2 = from_f32<TKV>(acc[qt][dh][2] * inv), e3 = from_f32<TKV>(acc[qt][dh][3] * inv);
-          const uint64_t packed = uint64_t(e0.bits) | uint64_t(e1.bits) << 16 | uint64_t(e2.bits) << 32 |
-                                  uint64_t(e3.bits) << 48;
-          __builtin_nontemporal_store(packed, reinterpret_cast<uint64_t *>(static_cast<TKV *>(a.out) + oo + 16 * dh + 4 * lg));
-        }
-      } else {
-#pragma unroll
-        for (int dh = 0; dh < DH; ++dh)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) store_any(a.out, a.out_dtype, oo + 16 * dh + 4 * lg + i, acc[qt][dh][i] * inv);
-      }
+    if constexpr (NQT == 1) {
+      group(std::integral_constant<int, 1>{});
+    } else if constexpr (NQT == 2) {
+      if (live >= 2) group(std::integral_constant<int, 2>{});
+      else group(std::integral_constant<int, 1>{});
+    } else {
+      if (live >= 4) group(std::integral_constant<int, NQT>{});
+      else if (live == 3) group(std::integral_constant<int, 3>{});
+      else if (live == 2) group(std::integral_constant<int, 2>{});
+      else group(std::integral_constant<int, 1>{});
     }
   }
 }

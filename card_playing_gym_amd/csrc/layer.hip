@@ -37,7 +37,7 @@ template <int BM, int MODE, int NC, int NQ>
 __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   __shared__ __align__(16) unsigned char panel[BM * ROWB];
   __shared__ __align__(16) unsigned char hbuf[hbufs_of<BM>()][BM * ROWB];
-  __shared__ float red[2 * WAVES * BM];
+  __shared__ float red[2 * WAVES * BM + 2 * BM];
   extern __shared__ float dyn[];
   tail_body<BM, MODE, NC, NQ>(a, blockIdx.x, panel, hbuf, red, dyn);
 }

@@ -70,8 +70,10 @@ __device__ __forceinline__ Slice stage_slice(const TailArgs &a, const Plan &p, i
 // LayerNorm statistics of rows held in the MFMA layout: v[i][j][r] is row 16 i + 4 lg + r,
 // column cw + 16 j + li (columns >= d hold 0 and are excluded).  Each wave first takes the
 // exact two-pass mean and centred sum of squares of its own columns (DPP sums over the
-// fragment's 16 lanes, no barrier), then the waves' (count, mean, M2) triples merge with
-// Chan et al.'s pairwise formula, M2 = sum_w [M2_w + n_w (mean_w - mean)^2]: one barrier.
+// fragment's 16 lanes, no barrier); then one thread per row merges the waves' (count, mean,
+// M2) triples with Chan et al.'s pairwise formula, M2 = sum_w [M2_w + n_w (mean_w - mean)^2],
+// and leaves (mean, rstd) in LDS: every lane then reads two values per row instead of
+// repeating the merge (sixteen reads per row).  red holds 2 WAVES BM + 2 BM floats.
 template <int BM>
 __device__ __forceinline__ void row_stats(const f32x4 (&v)[BM / 16][FN], int cw, int d, float eps,
                                           float (&mean)[BM / 16][4], float (&rstd)[BM / 16][4],
@@ -101,26 +103,33 @@ __device__ __forceinline__ void row_stats(const f32x4 (&v)[BM / 16][FN], int cw,
       }
     }
   lds_barrier();
-  const float inv_d = 1.0f / float(d);
+  float *stat = red + 2 * WAVES * BM;  // [mean | rstd] x BM
+  const int tid = threadIdx.x;
+  if (tid < BM) {
+    const float inv_d = 1.0f / float(d);
+    float total = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w)
+      total = fmaf(float(max(0, min(16 * FN, d - 16 * FN * w))), red[(0 * WAVES + w) * BM + tid], total);
+    const float mu = total * inv_d;
+    float m2 = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const float n = float(max(0, min(16 * FN, d - 16 * FN * w)));
+      const float dm = red[(0 * WAVES + w) * BM + tid] - mu;
+      m2 += fmaf(n * dm, dm, red[(1 * WAVES + w) * BM + tid]);
+    }
+    stat[tid] = mu;
+    stat[BM + tid] = rsqrtf(m2 * inv_d + eps);
+  }
+  lds_barrier();
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * i + 4 * lg + r;
-      float total = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w)
-        total = fmaf(float(max(0, min(16 * FN, d - 16 * FN * w))), red[(0 * WAVES + w) * BM + row], total);
-      const float mu = total * inv_d;
-      float m2 = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        const float n = float(max(0, min(16 * FN, d - 16 * FN * w)));
-        const float dm = red[(0 * WAVES + w) * BM + row] - mu;
-        m2 += fmaf(n * dm, dm, red[(1 * WAVES + w) * BM + row]);
-      }
-      mean[i][r] = mu;
-      rstd[i][r] = rsqrtf(m2 * inv_d + eps);
+      mean[i][r] = stat[row];
+      rstd[i][r] = stat[BM + row];
     }
 }
 
@@ -184,7 +193,7 @@ __device__ __forceinline__ void store_kv(void *base, int dtype, int64_t index, f
 // a compile-time constant, so the fully unrolled stage loop folds every stage's kind and
 // the weight registers flow from stage to stage without merges.
 // Row block `blk` of one layer tail.  LDS: panel [BM rows of ROWB bytes], hbuf two or four more,
-// red 2 * WAVES * BM floats, dyn the Params (d_ff + 5 PANEL floats, then 3 BM ints).
+// red 2 * WAVES * BM + 2 * BM floats, dyn the Params (d_ff + 5 PANEL floats, then 3 BM ints).
 template <int BM, int MODE, int NC, int NQ>
 __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned char *panel,
                                           unsigned char (*hbuf)[BM * ROWB], float *red, float *dyn) {
