@@ -35,6 +35,7 @@ struct TailArgs {
 
   const float *x_src;  // residual stream read
   float *x;            // residual stream written (may alias x_src)
+  int32_t x_src_vec;   // x_src is 16-byte aligned (the first block reads it as float4 runs)
 
   int32_t final_ln;
   const float *ln_w, *ln_b;  // next block's ln_attn, or the final norm
@@ -47,6 +48,7 @@ struct TailArgs {
   int64_t ld_vemb;
   int32_t vemb_off;  // < 0: none
   float *hidden;     // final_ln: [rows, d]
+  int32_t hidden_vec;  // hidden is 16-byte aligned (rows written as float4 runs)
   const int32_t *tok_out;
 };
 
@@ -56,8 +58,9 @@ size_t packed_fragment_bytes(int N, int K);
 void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_t stream);
 
 // Shapes the fused kernel is built for: d_model <= 256 and a multiple of 16, d_ff <= 1024
-// and n_qkv <= 768, both multiples of 16; bf16 projections.
-bool tail_supported(int d, int d_ff, int n_qkv);
+// and n_qkv <= 768, both multiples of 16, head_dim a multiple of 4 (each lane's run of four
+// output columns stays inside one head); bf16 projections.
+bool tail_supported(int d, int d_ff, int n_qkv, int head_dim);
 
 void launch_tail(const TailArgs &a, hipStream_t stream);
 

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(THREADS) void layer_tail_kernel(const TailArgs a) {
   __shared__ __align__(16) unsigned char panel[BM * ROWB];
   __shared__ __align__(16) unsigned char hbuf[hbufs_of<BM>()][BM * ROWB];
   __shared__ float red[2 * WAVES * BM + 2 * BM];
-  extern __shared__ float dyn[];
+  extern __shared__ __align__(16) float dyn[];
   tail_body<BM, MODE, NC, NQ>(a, blockIdx.x, panel, hbuf, red, dyn);
 }
 
@@ -71,9 +71,9 @@ void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_
   CG_LAUNCHED();
 }
 
-bool tail_supported(int d, int d_ff, int n_qkv) {
+bool tail_supported(int d, int d_ff, int n_qkv, int head_dim) {
   return d > 0 && d <= PANEL && d % 16 == 0 && d_ff > 0 && d_ff % 16 == 0 && d_ff <= 4 * PANEL &&
-         n_qkv > 0 && n_qkv % 16 == 0 && n_qkv <= 3 * PANEL;
+         n_qkv > 0 && n_qkv % 16 == 0 && n_qkv <= 3 * PANEL && head_dim > 0 && head_dim % 4 == 0;
 }
 
 namespace {
@@ -114,13 +114,19 @@ int tail_rows_per_block(int64_t M) {
 }  // namespace
 
 void launch_tail(const TailArgs &a, hipStream_t s) {
-  CG_REQUIRE(tail_supported(a.d, a.d_ff, a.n_qkv), CG_ERR_UNSUPPORTED, "fused layer: unsupported shape");
+  CG_REQUIRE(tail_supported(a.d, a.d_ff, a.n_qkv, a.head_dim), CG_ERR_UNSUPPORTED, "fused layer: unsupported shape");
   if (a.M <= 0) return;
+  // 32-bit offsets: residual rows and queries through buffer descriptors and unsigned
+  // products, slot-row offsets of the pool as int.
+  CG_REQUIRE(int64_t(a.M) * a.d * 4 < (int64_t(1) << 32) && int64_t(a.M) * a.q_cols * 4 < (int64_t(1) << 32) &&
+                 int64_t(a.kv_heads) * a.max_len * a.head_dim < (int64_t(1) << 31),
+             CG_ERR_RANGE, "fused layer: step too large for 32-bit row offsets");
   const int bm = tail_rows_per_block(a.M);
   const int nc = (a.d_ff + PANEL - 1) / PANEL, nq = (a.n_qkv + PANEL - 1) / PANEL;
   const int mode = !a.do_post ? 0 : (a.final_ln ? 2 : 1);
   auto go = [&](auto k16, auto k32, auto k64) {
-    const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + 3 * size_t(bm) * 4;
+    // Params (layer_dev.h): d_ff + 5 PANEL floats, the QKV column map, token slots and rows.
+    const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + (3 * PANEL / 4) * 8 + size_t(bm) * (8 + 4);
     const unsigned grid = unsigned((a.M + bm - 1) / bm);
     if (bm == 64) k64<<<grid, THREADS, dyn, s>>>(a);
     else if (bm == 32) k32<<<grid, THREADS, dyn, s>>>(a);

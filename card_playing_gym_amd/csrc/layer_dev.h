@@ -1,6 +1,15 @@
 // Device code of the fused per-layer tail (gfx950): the stage plan, LayerNorm statistics,
 // GELU, the per-layer parameters staged in LDS and tail_body, the whole tail of one row
 // block (launched by layer.hip's layer_tail_kernel).
+//
+// Every stage product is formed transposed, out^T = W . A^T: the weight fragment is the
+// MFMA's A operand and the LDS panel fragment its B operand (both keep the layouts the
+// untransposed product uses, so the fragment-order weights are the same).  Lane (li, lg)
+// of row tile i and column tile j then holds row 16 i + li at the four consecutive columns
+// cw + 16 j + 4 lg .. +3, so every epilogue works on 16-byte runs of one row: residual rows
+// load and store as float4, GELU / LayerNorm outputs go to LDS as one 8-byte write, q and
+// the appended K / V leave as one 16- or 8-byte store per run, and a row's LayerNorm sums
+// need two lane swaps (the four lane groups) instead of a 16-lane DPP reduction.
 #pragma once
 
 #include "common.h"
@@ -67,41 +76,129 @@ __device__ __forceinline__ Slice stage_slice(const TailArgs &a, const Plan &p, i
   return Slice{rsrc(opaque_ptr(a.w_qkv), uint32_t(a.n_qkv) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
 }
 
-// LayerNorm statistics of rows held in the MFMA layout: v[i][j][r] is row 16 i + 4 lg + r,
-// column cw + 16 j + li (columns >= d hold 0 and are excluded).  Each wave first takes the
-// exact two-pass mean and centred sum of squares of its own columns (DPP sums over the
-// fragment's 16 lanes, no barrier); then one thread per row merges the waves' (count, mean,
+// acc[i][j] += (W fragment j) x (panel rows 16 i + li)^T over all 256 k: the product of
+// stage_mma (fragment.h) with the operands swapped, so the result tile is transposed
+// (lane (li, lg) holds row 16 i + li, columns 4 lg .. +3 of the 16-column fragment j).
+// The weight registers are refilled with the next stage's fragments as in stage_mma.
+template <int FM>
+__device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned char *lds,
+                                            uint4 (&w)[KS][FN], const Slice &next, bool refill, int lane) {
+  const int li = lane & 15, lg = lane >> 4;
+  uint32_t base[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) base[j] = slice_base(next, j, lane);
+  auto a_frag = [&](int ks, int i) {
+    return *reinterpret_cast<const uint4 *>(lds + (16 * i + li) * ROWB + (32 * ks + 8 * lg) * 2);
+  };
+  if constexpr (FM == 1) {
+    uint4 af[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) af[ks] = a_frag(ks, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[0][j] = mma(w[ks][j], af[ks], acc[0][j]);
+      if (refill) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+      }
+    }
+  } else {
+    uint4 af[2][FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = a_frag(0, i);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[(ks + 1) & 1][i] = a_frag(ks + 1, i);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mma(w[ks][j], af[ks & 1][i], acc[i][j]);
+      if (refill) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+      }
+    }
+  }
+}
+
+// Sum over the four lane groups (lanes l, l ^ 16, l ^ 32, l ^ 48): the columns of one row.
+// v_permlane16/32_swap hand each lane its partner's value beside its own.
+__device__ __forceinline__ float lane_groups_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+// Four values rounded to bf16 (nearest even; two v_cvt_pk_bf16_f32) as 8 bytes.  For the
+// LDS panels only: a NaN keeps whatever quiet-NaN pattern the instruction gives.
+__device__ __forceinline__ u32x2 pack_bf16x4(f32x4 v) {
+  const bf16x4 h = __builtin_convertvector(v, bf16x4);
+  return __builtin_bit_cast(u32x2, h);
+}
+// The same with Tensor.to's rounding exactly (NaN -> 0x7fc0; fp16 nearest even), for what
+// is stored in the pool or as the queries.
+template <typename T>
+__device__ __forceinline__ u32x2 pack16x4(f32x4 v) {
+  const T e0 = from_f32<T>(v[0]), e1 = from_f32<T>(v[1]), e2 = from_f32<T>(v[2]), e3 = from_f32<T>(v[3]);
+  return u32x2{uint32_t(e0.bits) | uint32_t(e1.bits) << 16, uint32_t(e2.bits) | uint32_t(e3.bits) << 16};
+}
+
+__device__ __forceinline__ void st_nt(float *p, f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p)); }
+__device__ __forceinline__ void st_nt(void *p, u32x2 v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x2 *>(p)); }
+
+__device__ __forceinline__ f32x4 bload4f(Rsrc r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ f32x4 lds4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+
+// Four consecutive values of `dtype` (fp32, bf16 or fp16) stored at p (aligned to their size).
+__device__ __forceinline__ void store4(void *p, int dtype, f32x4 v) {
+  if (dtype == CG_BF16) st_nt(p, pack16x4<bf16>(v));
+  else if (dtype == CG_F16) st_nt(p, pack16x4<f16>(v));
+  else st_nt(static_cast<float *>(p), v);
+}
+
+// LayerNorm statistics of rows held transposed: v[i][j] is row 16 i + li at columns
+// cw + 16 j + 4 lg .. +3 (16-column tiles at or past d hold 0 and are excluded).  Each wave
+// first takes the exact two-pass mean and centred sum of squares of its own columns (in-lane
+// sums, then the four lane groups); then one thread per row merges the waves' (count, mean,
 // M2) triples with Chan et al.'s pairwise formula, M2 = sum_w [M2_w + n_w (mean_w - mean)^2],
-// and leaves (mean, rstd) in LDS: every lane then reads two values per row instead of
-// repeating the merge (sixteen reads per row).  red holds 2 WAVES BM + 2 BM floats.
+// and leaves (mean, rstd) in LDS for every lane to read.  red holds 2 WAVES BM + 2 BM floats.
 template <int BM>
-__device__ __forceinline__ void row_stats(const f32x4 (&v)[BM / 16][FN], int cw, int d, float eps,
-                                          float (&mean)[BM / 16][4], float (&rstd)[BM / 16][4],
-                                          float *red, int wave, int li, int lg) {
+__device__ __forceinline__ void row_stats_t(const f32x4 (&v)[BM / 16][FN], int cw, int d, float eps,
+                                            float (&mean)[BM / 16], float (&rstd)[BM / 16], float *red,
+                                            int wave, int li, int lg) {
   constexpr int FM = BM / 16;
-  // Columns this wave holds (the same for every row): cw .. cw + 16 FN - 1, capped at d.
   const int nw = max(0, min(16 * FN, d - cw));
   const float inv_nw = nw > 0 ? 1.0f / float(nw) : 0.f;
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < FM; ++i) {
+    float sum = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float sum = 0.f;
+    for (int j = 0; j < FN; ++j)
+      if (cw + 16 * j < d) sum += (v[i][j][0] + v[i][j][1]) + (v[i][j][2] + v[i][j][3]);
+    const float mw = lane_groups_sum(sum) * inv_nw;
+    float sq = 0.f;
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        if (cw + 16 * j + li < d) sum += v[i][j][r];
-      const float mw = sum16(sum) * inv_nw;
-      float sq = 0.f;
+    for (int j = 0; j < FN; ++j)
+      if (cw + 16 * j < d) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        if (cw + 16 * j + li < d) sq += (v[i][j][r] - mw) * (v[i][j][r] - mw);
-      const float m2 = sum16(sq);
-      if (li == 0) {
-        const int row = 16 * i + 4 * lg + r;
-        red[(0 * WAVES + wave) * BM + row] = mw;
-        red[(1 * WAVES + wave) * BM + row] = m2;
+        for (int r = 0; r < 4; ++r) sq = fmaf(v[i][j][r] - mw, v[i][j][r] - mw, sq);
       }
+    const float m2 = lane_groups_sum(sq);
+    if (lg == 0) {
+      red[(0 * WAVES + wave) * BM + 16 * i + li] = mw;
+      red[(1 * WAVES + wave) * BM + 16 * i + li] = m2;
     }
+  }
   lds_barrier();
   float *stat = red + 2 * WAVES * BM;  // [mean | rstd] x BM
   const int tid = threadIdx.x;
@@ -124,68 +221,77 @@ __device__ __forceinline__ void row_stats(const f32x4 (&v)[BM / 16][FN], int cw,
   }
   lds_barrier();
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * i + 4 * lg + r;
-      mean[i][r] = stat[row];
-      rstd[i][r] = stat[BM + row];
-    }
+  for (int i = 0; i < FM; ++i) {
+    mean[i] = stat[16 * i + li];
+    rstd[i] = stat[BM + 16 * i + li];
+  }
 }
 
-// LN(v) -> the panel (bf16, the next QKV stage's A operand), or, for the last block, the
-// final norm -> hidden rows of readout tokens.
-// Per-layer vectors and the block's token slots, staged in LDS by the kernel prologue.
+// Per-layer vectors, the QKV column map and the block's token slots, staged in LDS by the
+// kernel prologue (layout: params_floats / params_bytes below).
 struct Params {
   float *b_up, *b_down, *ln2_w, *ln2_b, *ln_w, *ln_b;  // [d_ff] and [PANEL] each
-  int *tok_row, *tok_pos, *tok_out;                    // [BM] each
+  int2 *qkv_map;     // [3 PANEL / 4]: per run of four QKV columns {role (0 q, 1 k, 2 v, -1 none),
+                     // offset (q: column; k / v: element offset inside a pool slot row)}
+  int64_t *tok_slot;  // [BM]: element offset of the token's pool slot (head 0), -1: no write
+  int *tok_out;       // [BM]
 };
 
+// LN(v; w, b) of the held rows -> the panel (bf16, the next stage's B operand).
 template <int BM>
-__device__ __forceinline__ void next_prologue(const TailArgs &a, const Params &prm, const f32x4 (&v)[BM / 16][FN],
-                                              unsigned char *panel, float *red, int m0, int cw,
-                                              int wave, int li, int lg) {
+__device__ __forceinline__ void ln_to_panel(const f32x4 (&v)[BM / 16][FN], const float (&mean)[BM / 16],
+                                            const float (&rstd)[BM / 16], const float *w, const float *b,
+                                            unsigned char *panel, int cw, int d, int li, int lg) {
   constexpr int FM = BM / 16;
-  float mean[FM][4], rstd[FM][4];
-  float lw[FN], lb[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int n = cw + 16 * j + li;
-    lw[j] = prm.ln_w[n];
-    lb[j] = prm.ln_b[n];
+    if (cw + 16 * j >= d) continue;
+    const int c0 = cw + 16 * j + 4 * lg;
+    const f32x4 lw = lds4(w + c0), lb = lds4(b + c0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      f32x4 y;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = fmaf((v[i][j][r] - mean[i]) * rstd[i], lw[r], lb[r]);
+      *reinterpret_cast<u32x2 *>(panel + (16 * i + li) * ROWB + c0 * 2) = pack_bf16x4(y);
+    }
   }
-  int out_row[FM][4];
-  if (a.final_ln) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) out_row[i][r] = prm.tok_out[16 * i + 4 * lg + r];
-  }
-  row_stats<BM>(v, cw, a.d, a.eps, mean, rstd, red, wave, li, lg);
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int n = cw + 16 * j + li;
-    if (n >= a.d) continue;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * i + 4 * lg + r;
-        const float y = fmaf((v[i][j][r] - mean[i][r]) * rstd[i][r], lw[j], lb[j]);
-        if (a.final_ln) {
-          if (out_row[i][r] >= 0) gst(a.hidden + int64_t(out_row[i][r]) * a.d + n, y);
-        } else {
-          *reinterpret_cast<bf16 *>(panel + row * ROWB + n * 2) = from_f32<bf16>(y);
-        }
-      }
-  }
-  if (!a.final_ln) lds_barrier();
 }
 
-__device__ __forceinline__ void store_kv(void *base, int dtype, int64_t index, float v) {
-  if (dtype == CG_BF16) gst(static_cast<bf16 *>(base) + index, from_f32<bf16>(v));
-  else if (dtype == CG_F16) gst(static_cast<f16 *>(base) + index, from_f32<f16>(v));
-  else gst(static_cast<float *>(base) + index, v);
+// The next block's LayerNorm of the residual rows -> the panel, or, for the last block, the
+// final norm -> hidden rows of readout tokens.
+template <int BM>
+__device__ __forceinline__ void next_prologue(const TailArgs &a, const Params &prm, const f32x4 (&v)[BM / 16][FN],
+                                              unsigned char *panel, float *red, int cw, int wave, int li, int lg) {
+  constexpr int FM = BM / 16;
+  float mean[FM], rstd[FM];
+  row_stats_t<BM>(v, cw, a.d, a.eps, mean, rstd, red, wave, li, lg);
+  if (!a.final_ln) {
+    ln_to_panel<BM>(v, mean, rstd, prm.ln_w, prm.ln_b, panel, cw, a.d, li, lg);
+    lds_barrier();
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int out_row = prm.tok_out[16 * i + li];
+    if (out_row < 0) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if (cw + 16 * j >= a.d) continue;
+      const int c0 = cw + 16 * j + 4 * lg;
+      const f32x4 lw = lds4(prm.ln_w + c0), lb = lds4(prm.ln_b + c0);
+      f32x4 y;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = fmaf((v[i][j][r] - mean[i]) * rstd[i], lw[r], lb[r]);
+      float *dst = a.hidden + int64_t(out_row) * a.d + c0;
+      if (a.hidden_vec) {
+        st_nt(dst, y);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gst(dst + r, y[r]);
+      }
+    }
+  }
 }
 
 // MODE: 0 = first block's prologue (x = x_src, LN + QKV), 1 = post + next QKV, 2 = post +
@@ -236,6 +342,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   constexpr int NB_UP = (4 * PANEL + THREADS - 1) / THREADS;
   float v_up[NB_UP], v_vec[5];
   int v_tok[3];
+  int2 v_map = int2{-1, 0};
 #pragma unroll
   for (int k = 0; k < NB_UP; ++k) {
     const int i = tid + k * THREADS;
@@ -252,6 +359,18 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     v_tok[0] = tin && !a.final_ln ? a.tok_row[m0_ + tid] : -1;
     v_tok[1] = tin && !a.final_ln ? a.tok_pos[m0_ + tid] : 0;
     v_tok[2] = tin && a.final_ln ? a.tok_out[m0_ + tid] : -1;
+    // QKV column runs: role and offset of columns 4 tid .. +3 (head_dim is a multiple of 4).
+    const int n = 4 * tid, kvw = a.kv_heads * a.head_dim;
+    if (!a.final_ln && n < a.n_qkv) {
+      if (n < a.q_cols) {
+        v_map = int2{0, n};
+      } else {
+        const int role = n < a.q_cols + kvw ? 1 : 2;
+        const int kvc = n - a.q_cols - (role == 2 ? kvw : 0);
+        const int h = kvc / a.head_dim;
+        v_map = int2{role, h * a.max_len * a.head_dim + (kvc - h * a.head_dim)};
+      }
+    }
   }
 
   // RING stages of weights in flight: stage s computes from wbuf[s % RING] and refills it
@@ -269,9 +388,9 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   prm.ln2_b = prm.ln2_w + PANEL;
   prm.ln_w = prm.ln2_b + PANEL;
   prm.ln_b = prm.ln_w + PANEL;
-  prm.tok_row = reinterpret_cast<int *>(prm.ln_b + PANEL);
-  prm.tok_pos = prm.tok_row + BM;
-  prm.tok_out = prm.tok_pos + BM;
+  prm.qkv_map = reinterpret_cast<int2 *>(prm.ln_b + PANEL);
+  prm.tok_slot = reinterpret_cast<int64_t *>(prm.qkv_map + 3 * PANEL / 4);
+  prm.tok_out = reinterpret_cast<int *>(prm.tok_slot + BM);
 
   // Zero the LDS panels once: padding columns (k >= d, or past d_ff) stay zero.
   for (int o = tid * 16; o < BM * ROWB; o += THREADS * 16) {
@@ -292,14 +411,17 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     prm.ln_w[tid] = v_vec[3];
     prm.ln_b[tid] = v_vec[4];
   }
+  if (tid < 3 * PANEL / 4) prm.qkv_map[tid] = v_map;
   if (tid < BM) {
-    prm.tok_row[tid] = v_tok[0];
-    prm.tok_pos[tid] = v_tok[1];
+    prm.tok_slot[tid] = v_tok[0] < 0 ? int64_t(-1)
+                                     : (int64_t(v_tok[0]) * a.kv_heads * a.max_len + v_tok[1]) * a.head_dim;
     prm.tok_out[tid] = v_tok[2];
   }
   lds_barrier();
 
-  f32x4 acc[FM][FN], accd[FM][FN];
+  // x1 (the residual after the out-projection) stays in registers until the MLP's residual
+  // add: it is never written to or read back from memory.
+  f32x4 acc[FM][FN], accd[FM][FN], x1[FM][FN];
   zero<FM>(accd);
   {
     const int m0 = blk * BM;
@@ -318,16 +440,22 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+        for (int j = 0; j < FN; ++j) {
+          const int m = m0 + 16 * i + li, c0 = cw + 16 * j + 4 * lg;
+          const uint32_t off = (uint32_t(m) * d + c0) * 4;
+          f32x4 v;
+          if (a.x_src_vec) {
+            v = bload4f(rs, off);
+          } else {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 16 * i + 4 * lg + r, n = cw + 16 * j + li;
-            const float v = bloadf(rs, (uint32_t(m) * d + n) * 4);
-            const bool ok = m < a.M && n < d;
-            if (ok && a.x != a.x_src) gst(a.x + int64_t(m) * d + n, v);
-            acc[i][j][r] = ok ? v : 0.f;
+            for (int r = 0; r < 4; ++r) v[r] = bloadf(rs, off + 4 * r);
           }
-      next_prologue<BM>(a, prm, acc, panel, red, m0, cw, wave, li, lg);
+          const bool ok = m < a.M && cw + 16 * j < d;
+          if (!ok) v = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (ok && a.x != a.x_src) st_nt(a.x + int64_t(m) * d + c0, v);
+          acc[i][j] = v;
+        }
+      next_prologue<BM>(a, prm, acc, panel, red, cw, wave, li, lg);
     }
   }
 
@@ -342,174 +470,128 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     const Slice nx = stage_slice(a, p, refill ? s + RING : s, cw);
     uint4(&cur)[KS][FN] = wbuf[s % RING];
     if (kind == ST_OUT) {
-      // ---- out-proj + residual, then LN(ln_mlp) -> panel
+      // ---- out-proj + residual (x1, kept), then LN(ln_mlp) -> panel
       const Rsrc rs = rsrc(opaque_ptr(a.x_src), xbytes);
-      float xr[FM][FN][4], lw[FN], lb[FN];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = cw + 16 * j + li;
-        lw[j] = prm.ln2_w[n];
-        lb[j] = prm.ln2_b[n];
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xr[i][j][r] = bloadf(rs, (uint32_t(m0 + 16 * i + 4 * lg + r) * d + n) * 4);
-      }
-      // Issue the residual loads ahead of this stage's weight refills: loads complete in
-      // order, so the epilogue then waits only for them, not for the next stage's weights.
-      __builtin_amdgcn_sched_barrier(0);
-      zero<FM>(acc);
-      stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
+      f32x4 xr[FM][FN];
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
+          xr[i][j] = bload4f(rs, (uint32_t(m0 + 16 * i + li) * d + cw + 16 * j + 4 * lg) * 4);
+      // Issue the residual loads ahead of this stage's weight refills: loads complete in
+      // order, so the epilogue then waits only for them, not for the next stage's weights.
+      __builtin_amdgcn_sched_barrier(0);
+      zero<FM>(acc);
+      stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = m0 + 16 * i + 4 * lg + r, n = cw + 16 * j + li;
-            float v = 0.f;
-            if (m < a.M && n < d) {
-              v = acc[i][j][r] + xr[i][j][r];
-              gst(a.x + int64_t(m) * d + n, v);
-            }
-            acc[i][j][r] = v;
-          }
-      float mean[FM][4], rstd[FM][4];
-      row_stats<BM>(acc, cw, d, a.eps, mean, rstd, red, wave, li, lg);
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = cw + 16 * j + li;
-        if (n >= d) continue;
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = 16 * i + 4 * lg + r;
-            const float y = fmaf((acc[i][j][r] - mean[i][r]) * rstd[i][r], lw[j], lb[j]);
-            *reinterpret_cast<bf16 *>(panel + row * ROWB + n * 2) = from_f32<bf16>(y);
-          }
-      }
+        for (int j = 0; j < FN; ++j) {
+          const bool ok = m0 + 16 * i + li < a.M && cw + 16 * j < d;
+          x1[i][j] = ok ? acc[i][j] + xr[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      float mean[FM], rstd[FM];
+      row_stats_t<BM>(x1, cw, d, a.eps, mean, rstd, red, wave, li, lg);
+      ln_to_panel<BM>(x1, mean, rstd, prm.ln2_w, prm.ln2_b, panel, cw, d, li, lg);
       lds_barrier();
     } else if (kind == ST_UP) {
-      // ---- up chunk c + GELU -> hbuf[c & 1]
-      float bias[FN];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = PANEL * c + cw + 16 * j + li;
-        bias[j] = n < a.d_ff ? prm.b_up[n] : 0.f;
-      }
+      // ---- up chunk c + GELU -> hbuf[c] (or hbuf[c & 1] when interleaved)
       zero<FM>(acc);
-      stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
+      stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
       unsigned char *hb = hbuf[p.ups_first ? c : (c & 1)];
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int col = cw + 16 * j + li;
-        const bool ok = PANEL * c + col < a.d_ff;
+        const int col = cw + 16 * j + 4 * lg;
+        // Columns past d_ff (a partial last chunk) must stay exactly 0: the down projection's
+        // fragments for those k are not zero.  Uniform per (wave, j): a multiply, no branch.
+        const bool ok = PANEL * c + cw + 16 * j < a.d_ff;
+        const float keep = ok ? 1.f : 0.f;
+        const f32x4 bias = lds4(prm.b_up + (ok ? PANEL * c + col : 0));
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i) {
+          f32x4 g;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = 16 * i + 4 * lg + r;
-            const float g = ok ? gelu_fast(acc[i][j][r] + bias[j]) : 0.f;
-            *reinterpret_cast<bf16 *>(hb + row * ROWB + col * 2) = from_f32<bf16>(g);
-          }
+          for (int r = 0; r < 4; ++r) g[r] = gelu_fast(acc[i][j][r] + bias[r]) * keep;
+          *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + col * 2) = pack_bf16x4(g);
+        }
       }
       // Down chunk c reads every wave's columns of GELU chunk c.
       if (!p.ups_first || c == p.nc - 1) lds_barrier();
     } else if (kind == ST_DOWN) {
       // ---- down chunk c (accumulates); after the last: residual (+PLE), next prologue
       const bool last = c == p.nc - 1;
-      float xr[FM][FN][4], bias[FN];
-      if (last) {
-        const Rsrc rx = rsrc(opaque_ptr(a.x), xbytes);
-        const Rsrc rp = rsrc(opaque_ptr(a.ple), a.ple ? uint32_t(a.M) * uint32_t(a.ld_ple) * 4 : 0u);
+      f32x4 pl[FM][FN];
+      if (last && a.ple) {
+        const Rsrc rp = rsrc(opaque_ptr(a.ple), uint32_t(a.M) * uint32_t(a.ld_ple) * 4);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int n = cw + 16 * j + li;
-          bias[j] = prm.b_down[n];
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const uint32_t m = uint32_t(m0 + 16 * i + 4 * lg + r);
-              float v = bloadf(rx, (m * d + n) * 4);
-              if (a.ple)
-                v = fmaf(bloadf(rp, (m * uint32_t(a.ld_ple) + a.ple_off + n % a.ple_dim) * 4), a.ple_scale, v);
-              xr[i][j][r] = v;
-            }
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);  // residual loads ahead of the weight refills
-      stage_mma<FM>(accd, hbuf[p.ups_first ? c : (c & 1)], cur, nx, refill, lane_o);
-      if (last) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int n = cw + 16 * j + li;
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int m = m0 + 16 * i + 4 * lg + r;
-              float v = 0.f;
-              if (m < a.M && n < d) {
-                v = xr[i][j][r] + accd[i][j][r] + bias[j];
-                gst(a.x + int64_t(m) * d + n, v);
-              }
-              accd[i][j][r] = v;
-            }
-        }
-        next_prologue<BM>(a, prm, accd, panel, red, m0, cw, wave, li, lg);
-      }
-    } else {
-      // ---- qkv chunk: q stored, k / v appended to the pool
-      int trow[FM][4], tpos[FM][4];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          trow[i][r] = prm.tok_row[16 * i + 4 * lg + r];
-          tpos[i][r] = prm.tok_pos[16 * i + 4 * lg + r];
-        }
-      zero<FM>(acc);
-      stage_mma<FM>(acc, panel, cur, nx, refill, lane_o);
-      // Per output column: its role (q / k / v / none) and, for k and v, the offset of its
-      // (head, dim) inside a pool slot row; per token row: the slot's base offset.
-      const int kvw = a.kv_heads * a.head_dim;
-      int role[FN], col[FN];
-      int64_t coff[FN];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = PANEL * c + cw + 16 * j + li;
-        role[j] = n >= a.n_qkv ? -1 : (n < a.q_cols ? 0 : (n < a.q_cols + kvw ? 1 : 2));
-        const int kvc = n - a.q_cols - (role[j] == 2 ? kvw : 0);
-        const int h = kvc / a.head_dim;
-        col[j] = role[j] == 0 ? n : kvc;
-        coff[j] = int64_t(h) * a.max_len * a.head_dim + (kvc - h * a.head_dim);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + 16 * i + 4 * lg + r;
-          if (m >= a.M) continue;
-          const int64_t slot = (int64_t(trow[i][r]) * a.kv_heads * a.max_len + tpos[i][r]) * a.head_dim;
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < FN; ++j) {
-            const float v = acc[i][j][r];
-            if (role[j] == 0) {
-              store_kv(a.q, a.q_dtype, int64_t(m) * a.q_cols + col[j], v);
-            } else if (role[j] > 0 && trow[i][r] >= 0) {
-              float val = v;
-              if (role[j] == 2 && a.vemb_off >= 0) val += a.vemb[int64_t(m) * a.ld_vemb + a.vemb_off + col[j]];
-              store_kv(role[j] == 2 ? a.vc : a.kc, a.kv_dtype, slot + coff[j], val);
+            const uint32_t m = uint32_t(m0 + 16 * i + li);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int n = cw + 16 * j + 4 * lg + r;
+              pl[i][j][r] = bloadf(rp, (m * uint32_t(a.ld_ple) + a.ple_off + n % a.ple_dim) * 4);
             }
           }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // per-layer embedding loads ahead of the weight refills
+      stage_mma_t<FM>(accd, hbuf[p.ups_first ? c : (c & 1)], cur, nx, refill, lane_o);
+      if (last) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int c0 = cw + 16 * j + 4 * lg;
+          const f32x4 bias = lds4(prm.b_down + c0);
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            const int m = m0 + 16 * i + li;
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (m < a.M && cw + 16 * j < d) {
+              v = x1[i][j] + accd[i][j] + bias;
+              if (a.ple) v += pl[i][j] * a.ple_scale;
+              st_nt(a.x + int64_t(m) * d + c0, v);
+            }
+            accd[i][j] = v;
+          }
         }
+        next_prologue<BM>(a, prm, accd, panel, red, cw, wave, li, lg);
+      }
+    } else {
+      // ---- qkv chunk: q stored, k / v appended to the pool (four consecutive columns of one
+      //      row per lane: one head's dims, head_dim being a multiple of 4)
+      int64_t slot[FM];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) slot[i] = prm.tok_slot[16 * i + li];
+      zero<FM>(acc);
+      stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
+      const int es = a.kv_dtype == CG_F32 ? 4 : 2;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int run = (PANEL * c + cw + 16 * j) / 4 + lg;
+        const int2 e = prm.qkv_map[run];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int m = m0 + 16 * i + li;
+          if (m >= a.M) continue;
+          if (e.x == 0) {
+            const uint32_t qo = uint32_t(m) * uint32_t(a.q_cols) + uint32_t(e.y);
+            if (a.q_dtype == CG_F32) st_nt(static_cast<float *>(a.q) + qo, acc[i][j]);
+            else store4(static_cast<char *>(a.q) + size_t(qo) * 2, a.q_dtype, acc[i][j]);
+          } else if (e.x > 0 && slot[i] >= 0) {
+            f32x4 val = acc[i][j];
+            if (e.x == 2 && a.vemb_off >= 0) {
+              const float *ve = a.vemb + int64_t(m) * a.ld_vemb + a.vemb_off +
+                                (4 * run - a.q_cols - a.kv_heads * a.head_dim);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) val[r] += ve[r];
+            }
+            store4(static_cast<char *>(e.x == 2 ? a.vc : a.kc) + (slot[i] + e.y) * es, a.kv_dtype, val);
+          }
+        }
+      }
     }
   }
 }
-
-
 
 }  // namespace
 }  // namespace cg

@@ -268,7 +268,7 @@ int cg_trunk_create(const cg_trunk_config *config, const cg_layer_params *layers
 #ifdef CG_TRUNK_NO_FUSED
       t->fused = false;  // measurement builds only
 #else
-      t->fused = tail_supported(c.d_model, c.d_ff, (c.n_heads + 2 * c.n_kv_heads) * hd);
+      t->fused = tail_supported(c.d_model, c.d_ff, (c.n_heads + 2 * c.n_kv_heads) * hd, hd);
 #endif
       t->wbuf_bytes = weight_bytes_per_layer(*t) * n;
       CG_HIP(hipMalloc(&t->wbuf, t->wbuf_bytes));
@@ -434,6 +434,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
       ta.ld_vemb = c.value_width;
       ta.vemb_off = -1;
       ta.hidden = hidden;
+      ta.hidden_vec = (reinterpret_cast<uintptr_t>(hidden) & 15) == 0;
       ta.tok_out = w.tok_out;
       return ta;
     };
@@ -457,6 +458,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
       TailArgs ta = base();
       ta.do_post = 0;
       ta.x_src = x;
+      ta.x_src_vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
       ta.x = w.x;
       set_next(ta, 0);
       launch_tail(ta, s);
@@ -483,6 +485,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
         ta.ple_scale = ple_scale;
       }
       ta.x_src = w.x;
+      ta.x_src_vec = 1;
       ta.x = w.x;
       set_next(ta, l + 1);
       return ta;
