@@ -195,19 +195,19 @@ __device__ __forceinline__ float sum16(float v) {
 
 // GELU with erf (torch.nn.GELU()): 0.5 x (1 + erf(x / sqrt 2)), erf from the rational
 // approximation of Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7, far below the bf16
-// rounding the result gets): erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-z^2},
-// t = 1 / (1 + p |z|), sign restored for z < 0.  About a dozen VALU instructions.
+// rounding the result gets): erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-z^2},
+// t = 1 / (1 + p z) for z = |x| / sqrt 2 >= 0.  With q = erfc(z) / 2 (the halves folded into
+// the coefficients), GELU(x) = x (1 - q) for x >= 0 and x q for x < 0 (GELU(+inf) = +inf,
+// GELU(-inf) = NaN, as torch's formula gives).  About fifteen VALU instructions.
 __device__ __forceinline__ float gelu_fast(float x) {
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
-  const float erf_abs = fmaf(-poly * t, e, 1.0f);
-  const float erf_z = x < 0.f ? -erf_abs : erf_abs;
-  return 0.5f * x * (1.0f + erf_z);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, fabsf(x), 1.0f));
+  float poly = fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
+  poly = fmaf(poly, t, 0.5f * 1.421413741f);
+  poly = fmaf(poly, t, 0.5f * -0.284496736f);
+  poly = fmaf(poly, t, 0.5f * 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f((x * (-0.5f * 1.4426950408889634f)) * x);
+  const float q = (poly * t) * e;
+  return x * (x >= 0.f ? 1.0f - q : q);
 }
 
 

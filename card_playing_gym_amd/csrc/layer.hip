@@ -90,10 +90,13 @@ int device_cus() {
 }
 
 // Rows per block: one block per CU at a time (eight waves), so a launch takes
-// ceil(blocks / CUs) rounds of one block's life, measured on MI355X at d 256 / d_ff 1024 as
-// about 9.5 us + 13.5 us per 16 rows (weights streamed once per block, epilogues and
-// row traffic per row).  16 rows keep the decode step (4096 rows) at one round of 256
-// blocks; taller blocks pay off once the rows fill several rounds (prefill, packed chunks).
+// ceil(blocks / CUs) rounds of one block's life, measured on MI355X at d 256 / d_ff 1024
+// (kernel trace, configs 3 and 5 with the height forced) as about 17.5 us + 0.28 us per row:
+// 22.6 / 25.7 / 30.5 / 35.4 us at 16 / 32 / 48 / 64 rows.  Most of a block's life is the
+// weight stream (the layer's 1.38 MB from L2 into every CU), which does not grow with the
+// rows.  16 rows keep the decode step (4096 rows) at one round of 256 blocks; config 4's
+// 8192 rows take one round of 32-row blocks, config 5's ~35k packed rows three rounds of
+// 48-row blocks (102 us against 122 at 32 rows and 120 at 64), prefill-sized launches 64.
 int tail_rows_per_block(int64_t M) {
 #ifdef CG_TAIL_FORCE_BM
   if (M >= 0) return CG_TAIL_FORCE_BM;  // measurement builds only
@@ -101,9 +104,9 @@ int tail_rows_per_block(int64_t M) {
   const int64_t cus = device_cus();
   int best = 16;
   double best_t = 1e30;
-  for (int bm : {16, 32, 64}) {
+  for (int bm : {16, 32, 48, 64}) {
     const int64_t rounds = ((M + bm - 1) / bm + cus - 1) / cus;
-    const double t = double(rounds) * (9.5 + 13.5 * bm / 16);
+    const double t = double(rounds) * (17.5 + 0.28 * bm);
     if (t < best_t - 1e-9) {
       best_t = t;
       best = bm;
@@ -124,11 +127,12 @@ void launch_tail(const TailArgs &a, hipStream_t s) {
   const int bm = tail_rows_per_block(a.M);
   const int nc = (a.d_ff + PANEL - 1) / PANEL, nq = (a.n_qkv + PANEL - 1) / PANEL;
   const int mode = !a.do_post ? 0 : (a.final_ln ? 2 : 1);
-  auto go = [&](auto k16, auto k32, auto k64) {
+  auto go = [&](auto k16, auto k32, auto k48, auto k64) {
     // Params (layer_dev.h): d_ff + 5 PANEL floats, the QKV column map, token slots and rows.
     const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + (3 * PANEL / 4) * 8 + size_t(bm) * (8 + 4);
     const unsigned grid = unsigned((a.M + bm - 1) / bm);
     if (bm == 64) k64<<<grid, THREADS, dyn, s>>>(a);
+    else if (bm == 48) k48<<<grid, THREADS, dyn, s>>>(a);
     else if (bm == 32) k32<<<grid, THREADS, dyn, s>>>(a);
     else k16<<<grid, THREADS, dyn, s>>>(a);
     CG_LAUNCHED();
@@ -136,7 +140,7 @@ void launch_tail(const TailArgs &a, hipStream_t s) {
 #define CG_TAIL_CASE(MODE, NC, NQ)                                                       \
   if (mode == MODE && (MODE == 0 || nc == NC) && (MODE == 2 || nq == NQ))                \
     return go(layer_tail_kernel<16, MODE, NC, NQ>, layer_tail_kernel<32, MODE, NC, NQ>, \
-              layer_tail_kernel<64, MODE, NC, NQ>)
+              layer_tail_kernel<48, MODE, NC, NQ>, layer_tail_kernel<64, MODE, NC, NQ>)
   CG_TAIL_CASE(0, 1, 1); CG_TAIL_CASE(0, 1, 2); CG_TAIL_CASE(0, 1, 3);
   CG_TAIL_CASE(1, 1, 1); CG_TAIL_CASE(1, 1, 2); CG_TAIL_CASE(1, 1, 3);
   CG_TAIL_CASE(1, 2, 1); CG_TAIL_CASE(1, 2, 2); CG_TAIL_CASE(1, 2, 3);

@@ -22,18 +22,18 @@ namespace {
 #ifndef TAIL_RING
 #define TAIL_RING 2
 #endif
-// Stages of weights in flight per wave: two for 16- and 32-row blocks; one for 64-row
-// blocks, whose four row tiles per fragment keep each stage's MFMAs busy four times as long
-// (and whose accumulators leave no room for a second ring stage).
+// Stages of weights in flight per wave: two for 16- and 32-row blocks; one for 48- and
+// 64-row blocks, whose three or four row tiles per fragment keep each stage's MFMAs busy
+// that much longer (and whose accumulators leave no room for a second ring stage).
 template <int BM>
-constexpr int ring_of() { return BM >= 64 ? 1 : TAIL_RING; }
+constexpr int ring_of() { return BM >= 48 ? 1 : TAIL_RING; }
 
 enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
 
 // MLP stage order.  Blocks of up to 32 rows run every up chunk first (each GELU output to
 // its own LDS buffer), one barrier, then every down chunk: one block-wide wait for the MLP
-// instead of one per chunk.  64-row blocks interleave up c, down c through two buffers
-// (four would not fit in LDS beside the panel).
+// instead of one per chunk.  48- and 64-row blocks interleave up c, down c through two
+// buffers (four would not fit in LDS beside the panel).
 template <int BM>
 constexpr bool ups_first() { return BM <= 32; }
 template <int BM>
@@ -178,7 +178,8 @@ __device__ __forceinline__ void row_stats_t(const f32x4 (&v)[BM / 16][FN], int c
                                             int wave, int li, int lg) {
   constexpr int FM = BM / 16;
   const int nw = max(0, min(16 * FN, d - cw));
-  const float inv_nw = nw > 0 ? 1.0f / float(nw) : 0.f;
+  // Reciprocals of the column counts: exact for the powers of two of the usual widths.
+  const float inv_nw = nw > 0 ? __builtin_amdgcn_rcpf(float(nw)) : 0.f;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     float sum = 0.f;
@@ -203,7 +204,7 @@ __device__ __forceinline__ void row_stats_t(const f32x4 (&v)[BM / 16][FN], int c
   float *stat = red + 2 * WAVES * BM;  // [mean | rstd] x BM
   const int tid = threadIdx.x;
   if (tid < BM) {
-    const float inv_d = 1.0f / float(d);
+    const float inv_d = __builtin_amdgcn_rcpf(float(d));
     float total = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w)
