@@ -97,6 +97,8 @@ int device_cus() {
 // rows.  16 rows keep the decode step (4096 rows) at one round of 256 blocks; config 4's
 // 8192 rows take one round of 32-row blocks, config 5's ~35k packed rows three rounds of
 // 48-row blocks (102 us against 122 at 32 rows and 120 at 64), prefill-sized launches 64.
+// Taller blocks (80 and 96 rows, one weight stage in flight) measured 52 and 59 us per block
+// and lost at both config 5 and prefill.
 int tail_rows_per_block(int64_t M) {
 #ifdef CG_TAIL_FORCE_BM
   if (M >= 0) return CG_TAIL_FORCE_BM;  // measurement builds only

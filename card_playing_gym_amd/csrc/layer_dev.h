@@ -22,22 +22,23 @@ namespace {
 #ifndef TAIL_RING
 #define TAIL_RING 2
 #endif
-// Stages of weights in flight per wave: two for 16- and 32-row blocks; one for 48- and
-// 64-row blocks, whose three or four row tiles per fragment keep each stage's MFMAs busy
-// that much longer (and whose accumulators leave no room for a second ring stage).
+// Stages of weights in flight per wave: two up to 48-row blocks; one for taller blocks,
+// whose four or more row tiles per fragment keep each stage's MFMAs busy that much longer
+// (and whose accumulators leave no room for a second ring stage).
 template <int BM>
-constexpr int ring_of() { return BM >= 48 ? 1 : TAIL_RING; }
+constexpr int ring_of() { return BM > 48 ? 1 : TAIL_RING; }
 
 enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
 
 // MLP stage order.  Blocks of up to 32 rows run every up chunk first (each GELU output to
 // its own LDS buffer), one barrier, then every down chunk: one block-wide wait for the MLP
 // instead of one per chunk.  48- and 64-row blocks interleave up c, down c through two
-// buffers (four would not fit in LDS beside the panel).
+// buffers (four would not fit in LDS beside the panel); a taller block would use one, with
+// a barrier before each GELU chunk overwrites the one the last down chunk read.
 template <int BM>
 constexpr bool ups_first() { return BM <= 32; }
 template <int BM>
-constexpr int hbufs_of() { return ups_first<BM>() ? 4 : 2; }
+constexpr int hbufs_of() { return ups_first<BM>() ? 4 : (BM <= 64 ? 2 : 1); }
 
 struct Plan {
   int nc, nq, n_post, S;
@@ -420,9 +421,10 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   }
   lds_barrier();
 
-  // x1 (the residual after the out-projection) stays in registers until the MLP's residual
-  // add: it is never written to or read back from memory.
-  f32x4 acc[FM][FN], accd[FM][FN], x1[FM][FN];
+  // x1 (the residual after the out-projection) stays in registers: the down projection's
+  // chunks accumulate onto it (accd starts as x1), so it is never written to or read back
+  // from memory and needs no registers of its own.
+  f32x4 acc[FM][FN], accd[FM][FN];
   zero<FM>(accd);
   {
     const int m0 = blk * BM;
@@ -489,17 +491,19 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const bool ok = m0 + 16 * i + li < a.M && cw + 16 * j < d;
-          x1[i][j] = ok ? acc[i][j] + xr[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
+          accd[i][j] = ok ? acc[i][j] + xr[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
       float mean[FM], rstd[FM];
-      row_stats_t<BM>(x1, cw, d, a.eps, mean, rstd, red, wave, li, lg);
-      ln_to_panel<BM>(x1, mean, rstd, prm.ln2_w, prm.ln2_b, panel, cw, d, li, lg);
+      row_stats_t<BM>(accd, cw, d, a.eps, mean, rstd, red, wave, li, lg);
+      ln_to_panel<BM>(accd, mean, rstd, prm.ln2_w, prm.ln2_b, panel, cw, d, li, lg);
       lds_barrier();
     } else if (kind == ST_UP) {
       // ---- up chunk c + GELU -> hbuf[c] (or hbuf[c & 1] when interleaved)
       zero<FM>(acc);
       stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
-      unsigned char *hb = hbuf[p.ups_first ? c : (c & 1)];
+      unsigned char *hb = hbuf[p.ups_first ? c : (c % HB)];
+      // One GELU buffer: every wave has finished down chunk c - 1's reads of it.
+      if (HB == 1 && c > 0) lds_barrier();
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = cw + 16 * j + 4 * lg;
@@ -537,7 +541,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
           }
       }
       __builtin_amdgcn_sched_barrier(0);  // per-layer embedding loads ahead of the weight refills
-      stage_mma_t<FM>(accd, hbuf[p.ups_first ? c : (c & 1)], cur, nx, refill, lane_o);
+      stage_mma_t<FM>(accd, hbuf[p.ups_first ? c : (c % HB)], cur, nx, refill, lane_o);
       if (last) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -548,7 +552,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
             const int m = m0 + 16 * i + li;
             f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
             if (m < a.M && cw + 16 * j < d) {
-              v = x1[i][j] + accd[i][j] + bias;
+              v = accd[i][j] + bias;
               if (a.ple) v += pl[i][j] * a.ple_scale;
               st_nt(a.x + int64_t(m) * d + c0, v);
             }
