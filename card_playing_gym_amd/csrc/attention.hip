@@ -725,6 +725,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
 
       f32x4 acc[NQT][DH];
       float mrun[NQT], lsum[NQT];
+      const float sm = QRAW ? a.scale_log2 : 1.0f;  // score scale applied in the exponent
   #pragma unroll
       for (int qt = 0; qt < L; ++qt) {
         mrun[qt] = NEG_BIG;
@@ -751,7 +752,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
               __builtin_memcpy(&kvec, &kr[st][j][dk], 16);
               s4 = Mfma16<TKV>::mma(kvec, qv[qt][dk], s4);
             }
-            sc[qt][j] = QRAW ? s4 * a.scale_log2 : s4;
+            sc[qt][j] = s4;  // QRAW: raw q.k; the scale joins the exponent below
           }
         // ---- V rows -> LDS (as loaded), then the next tile's loads ----------------------
   #pragma unroll
@@ -783,7 +784,9 @@ void decode_attention_tr_kernel(AttnArgs a) {
           for (int j = 0; j < NJ; ++j)
   #pragma unroll
             for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[qt][j][i]);
-          tmax = xor32_max(xor16_max(tmax));
+          // QRAW scores are unscaled: the maximum is taken on them (the scale is positive) and
+          // the scale multiplies inside the exponent's FMA, p = 2^(s * scale - max).
+          tmax = xor32_max(xor16_max(tmax)) * sm;
           const float mnew = fmaxf(mrun[qt], tmax);
           const float corr = fast_exp2(mrun[qt] - mnew);
           float psum = 0.f;
@@ -791,7 +794,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
           for (int j = 0; j < NJ; ++j)
   #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              p[qt][j][i] = fast_exp2(sc[qt][j][i] - mnew);
+              p[qt][j][i] = fast_exp2(fmaf(sc[qt][j][i], sm, -mnew));
               psum += p[qt][j][i];
             }
           lsum[qt] = fmaf(lsum[qt], corr, psum);
@@ -1212,6 +1215,10 @@ __global__ __launch_bounds__(1024) void attention_order_kernel(const AttnArgs a,
 #ifndef TR_DEPTH
 #define TR_DEPTH 1
 #endif
+// Key tiles in flight per wave when one wave takes a whole multi-token item.
+#ifndef TR_MQ_DEPTH
+#define TR_MQ_DEPTH 1
+#endif
 #ifndef TR_ONE_WAVE_ITEMS
 #define TR_ONE_WAVE_ITEMS 2048
 #endif
@@ -1235,7 +1242,7 @@ void launch_tr(const AttnArgs &a, int queries, hipStream_t s) {
     // split its key tiles and merge.
     const dim3 grid_q(1, unsigned(std::min<int64_t>((int64_t(queries) + 63) / 64, 65535)));
     if (a.span <= 64 || int64_t(units) * grid_q.y >= TR_ONE_WAVE_ITEMS) {
-      decode_attention_tr_kernel<TKV, D, 4, 1, 64, 1, QRAW><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
+      decode_attention_tr_kernel<TKV, D, 4, 1, 64, TR_MQ_DEPTH, QRAW><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
     } else {
       decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1, QRAW><<<dim3(tr_grid, grid_q.y), 256, 0, s>>>(a);
     }

@@ -357,8 +357,9 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
   // by the fused step (the reference rounds q to the cache dtype before the scores,
   // trunk.py:222), which the attention kernel loads as its MFMA operand as they are:
   // 139 -> 100 us per layer at config 5.  One-token decode keeps fp32 q, which that kernel
-  // scales and rounds itself (the raw form measured 2.6 us slower per layer there); the
-  // projections of the unfused path write fp32.
+  // scales and rounds itself (the raw form measured 1-2.6 us slower per layer there, also
+  // with the score scale folded into the exponent); the projections of the unfused path
+  // write fp32.
   const bool multi_query = r.seq_start != nullptr || int64_t(H / KVH) * r.T > 16;
   const int q_dtype = (t.fused && multi_query && cache[0].dtype != CG_F32) ? cache[0].dtype : CG_F32;
   auto attn_args = [&](int l) {
