@@ -28,9 +28,10 @@ struct AttnArgs {
   int32_t n_seqs, n_heads, kv_heads, head_dim, T, max_len, capacity, span;
   int64_t n_tokens;            // packed mode: tokens in q / out (token ranges are clamped to it)
   float scale_log2;            // softmax scale * log2(e)
-  // (row, KV head) units in descending order of key tiles (launch_attention_order), or NULL.
+  // (row, KV head) units in descending order of work (launch_attention_order), or NULL.
   // With it, padded runs of up to 16 queries per unit on a 16-bit pool take the persistent
-  // kernel: each wave walks several whole units back to back.
+  // kernel (each wave walks several whole units back to back), and packed runs deal their
+  // units longest first.
   const int32_t *order;
 };
 

@@ -580,7 +580,15 @@ void decode_attention_tr_kernel(AttnArgs a) {
   // The wave index is uniform: readfirstlane lets the compiler keep everything derived
   // from it (unit, row, descriptors) in scalar registers.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int unit = blockIdx.x * (4 / SPLIT) + wave / SPLIT;
+  // Packed chunks with an order (the units by descending work, written for this step) deal
+  // the longest units first, so the launch does not end on a few long ones.  An entry
+  // outside [0, U) computes nothing.
+  int unit = blockIdx.x * (4 / SPLIT) + wave / SPLIT;
+  if (a.order && a.seq_start) {
+    const int U = a.n_seqs * a.kv_heads;
+    unit = unit < U ? a.order[unit] : U;
+    if (unit < 0) unit = U;
+  }
   const int part = wave % SPLIT;
   // Block barriers below must be reached by every wave of the block the same number of
   // times.  SPLIT 4: the block is one unit, whose waves all leave together.  SPLIT 1: no

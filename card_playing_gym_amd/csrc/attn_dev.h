@@ -116,21 +116,31 @@ __device__ __forceinline__ int row16_min(int v) {
   return v;
 }
 
-// ---- the unit order of the persistent decode-attention kernel ---------------------------
+// ---- the unit order of the persistent decode-attention kernel (and of packed chunks) -----
 constexpr int STREAM_KT = 64;       // keys per tile of the persistent kernel
 constexpr int ORDER_BUCKETS = 256;  // tile counts >= 255 share the last bucket
 
-// Tile count of a (row, KV head) unit: its widest query's visible keys, in 64-key tiles.
+// Work of a (row, KV head) unit: its widest query's visible keys in 64-key tiles, times its
+// 16-query tiles (one for the decode runs of the persistent kernel; a packed chunk of c
+// tokens has G c queries).
 __device__ __forceinline__ int unit_tiles(const AttnArgs &a, int u) {
   const int b = u / a.kv_heads;
   const int64_t row = a.rows ? a.rows[b] : int64_t(b);
-  int64_t kend = a.key_lengths[b] + a.kl_add + (a.T - 1);
+  int64_t count = a.T;
+  if (a.seq_start) {
+    int64_t lo = a.seq_start[b], hi = a.seq_start[b + 1];
+    lo = lo < 0 ? 0 : (lo > a.n_tokens ? a.n_tokens : lo);
+    hi = hi < lo ? lo : (hi > a.n_tokens ? a.n_tokens : hi);
+    count = hi - lo;
+  }
+  int64_t kend = a.key_lengths[b] + a.kl_add + (count - 1);
   if (kend > a.span) kend = a.span;
   if (row < 0 || row >= a.capacity || kend < 0) kend = 0;
-  return int(min<int64_t>(ORDER_BUCKETS - 1, (kend + STREAM_KT - 1) / STREAM_KT));
+  const int64_t qtiles = (int64_t(a.n_heads / a.kv_heads) * count + 15) / 16;
+  return int(min<int64_t>(ORDER_BUCKETS - 1, (kend + STREAM_KT - 1) / STREAM_KT * qtiles));
 }
 
-// order = the units sorted by descending tile count: a counting sort by one whole block
+// order = the units sorted by descending work: a counting sort by one whole block
 // (any size; ties land in any order, which changes only which wave computes a unit, not its
 // result).  Called by every thread of the block.
 __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restrict__ order) {

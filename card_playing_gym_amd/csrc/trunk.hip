@@ -401,13 +401,19 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
                                                 w.tok_out, hidden, d);
     CG_LAUNCHED();
   }
-  // Decode runs with long possible rows take the persistent attention kernel, whose unit
-  // order (by key tiles) is the same for every layer of the step: computed once here.
+  // Decode runs with long possible rows take the persistent attention kernel, and packed
+  // chunks on a 16-bit pool deal their units longest first; either way the unit order (by
+  // work) is the same for every layer of the step: computed once here.
+#ifndef CG_PACKED_ORDER
+#define CG_PACKED_ORDER 1
+#endif
   const bool streams = attention_streams(attn_args(0));
-  if (streams) launch_attention_order(attn_args(0), w.order, s);
+  const bool ordered = streams || (CG_PACKED_ORDER && r.seq_start && (cache[0].dtype == CG_BF16 || cache[0].dtype == CG_F16) &&
+                                   (D == 32 || D == 64));
+  if (ordered) launch_attention_order(attn_args(0), w.order, s);
   auto attention = [&](int l) {
     AttnArgs a = attn_args(l);
-    a.order = streams ? w.order : nullptr;
+    a.order = ordered ? w.order : nullptr;
     launch_decode_attention(a, s);
   };
 
