@@ -149,7 +149,20 @@ __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restri
   const int U = a.n_seqs * a.kv_heads;
   for (int i = tid; i < ORDER_BUCKETS; i += nt) hist[i] = 0;
   __syncthreads();
-  for (int u = tid; u < U; u += nt) atomicAdd(&hist[unit_tiles(a, u)], 1);
+  // Each pass takes eight units per thread at a time, so their loads (lengths, rows, chunk
+  // bounds) are in flight together instead of one round trip per unit.
+  constexpr int PER = 8;
+  for (int base = 0; base < U; base += PER * nt) {
+    int w[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int u = base + tid + k * nt;
+      w[k] = u < U ? unit_tiles(a, u) : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (w[k] >= 0) atomicAdd(&hist[w[k]], 1);
+  }
   __syncthreads();
   // Exclusive suffix sums (bucket k starts after every larger bucket): Hillis-Steele over
   // the reversed histogram.
@@ -164,7 +177,17 @@ __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restri
   // scan[src][i]: inclusive sum of reversed buckets 0..i, i.e. of buckets K - 1 - i .. K - 1.
   for (int k = tid; k < ORDER_BUCKETS; k += nt) hist[k] = scan[src][ORDER_BUCKETS - 1 - k] - hist[k];
   __syncthreads();
-  for (int u = tid; u < U; u += nt) order[atomicAdd(&hist[unit_tiles(a, u)], 1)] = u;
+  for (int base = 0; base < U; base += PER * nt) {
+    int w[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int u = base + tid + k * nt;
+      w[k] = u < U ? unit_tiles(a, u) : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+      if (w[k] >= 0) order[atomicAdd(&hist[w[k]], 1)] = base + tid + k * nt;
+  }
 }
 
 }  // namespace
