@@ -67,6 +67,11 @@ def parse() -> argparse.Namespace:
         "(for rocprofv3 --pmc passes over the GEMM kernels)",
     )
     p.add_argument(
+        "--step-probe", action="store_true",
+        help="run only the workload's graph-replayed steps (no baselines, no other rows), print their timing "
+        "and exit (for rocprofv3 counter and trace passes over the step's kernels)",
+    )
+    p.add_argument(
         "--train-probe", action="store_true",
         help="run only the fp32 training step (our path, no reference) and print its timings, then exit "
         "(for a rocprofv3 kernel trace of the training kernels)",
@@ -913,6 +918,20 @@ def main() -> int:
     with torch.no_grad():
         bench.load(0)
         bench.capture(tuple(range(args.warmup + args.steps)) if bench.chunks else (0,))
+        if args.step_probe:
+            for s in range(args.warmup):
+                bench.step(s)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for s in range(args.warmup, args.warmup + args.steps):
+                bench.step(s)
+            torch.cuda.synchronize()
+            per_step = (time.perf_counter() - t0) / args.steps
+            print(json.dumps({"probe": "step", "workload": args.workload, "steps": args.steps, "warmup": args.warmup,
+                              "ms_per_step": round(per_step * 1e3, 4),
+                              "game_tokens_per_s": round(bench.tokens_in(args.warmup, args.steps) / args.steps / per_step, 1)}),
+                  flush=True)
+            return 0
         torch.cuda.synchronize()
         for s in range(args.warmup):
             bench.step(s)
