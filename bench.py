@@ -1021,7 +1021,19 @@ def main() -> int:
         **extra,
     }
     print(json.dumps(result), flush=True)
+    _stop_compile_workers()
     return 0
+
+
+def _stop_compile_workers() -> None:
+    """The compiled reference leg starts Inductor's compile worker processes; end them so
+    that no process outlives the benchmark."""
+
+    try:
+        from torch._inductor.async_compile import shutdown_compile_workers
+    except ImportError:
+        return
+    shutdown_compile_workers()
 
 
 if __name__ == "__main__":
