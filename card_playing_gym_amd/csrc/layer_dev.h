@@ -77,6 +77,23 @@ __device__ __forceinline__ Slice stage_slice(const TailArgs &a, const Plan &p, i
   return Slice{rsrc(opaque_ptr(a.w_qkv), uint32_t(a.n_qkv) * kd * 64), kd, (PANEL * c + cw) / 16, 0};
 }
 
+// Weight fragment loads (cache-policy bits of the buffer instruction: 1 sc0, 2 nt).
+#ifndef CG_W_CPOL
+#define CG_W_CPOL 0
+#endif
+__device__ __forceinline__ uint4 wload16(Rsrc r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CG_W_CPOL);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ void load_wslice(uint4 (&buf)[KS][FN], const Slice &s, int lane) {
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const uint32_t base = slice_base(s, j, lane);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) buf[ks][j] = wload16(s.w, base + 1024 * ks);
+  }
+}
+
 // acc[i][j] += (W fragment j) x (panel rows 16 i + li)^T over all 256 k: the product of
 // stage_mma (fragment.h) with the operands swapped, so the result tile is transposed
 // (lane (li, lg) holds row 16 i + li, columns 4 lg .. +3 of the 16-column fragment j).
@@ -101,7 +118,7 @@ __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned
       for (int j = 0; j < FN; ++j) acc[0][j] = mma(w[ks][j], af[ks], acc[0][j]);
       if (refill) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+        for (int j = 0; j < FN; ++j) w[ks][j] = wload16(next.w, base[j] + 1024 * ks);
       }
     }
   } else {
@@ -120,7 +137,7 @@ __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned
         for (int j = 0; j < FN; ++j) acc[i][j] = mma(w[ks][j], af[ks & 1][i], acc[i][j]);
       if (refill) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
+        for (int j = 0; j < FN; ++j) w[ks][j] = wload16(next.w, base[j] + 1024 * ks);
       }
     }
   }
@@ -381,7 +398,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   uint4 wbuf[RING][KS][FN];
 #pragma unroll
   for (int r = 0; r < RING; ++r)
-    if (S > r) load_slice(wbuf[r], stage_slice(a, p, r, cw), lane);
+    if (S > r) load_wslice(wbuf[r], stage_slice(a, p, r, cw), lane);
 
   Params prm;
   prm.b_up = dyn;
