@@ -355,12 +355,14 @@ def test_bf16_trunk_shapes_with_conditioning(device, shape, packed):
     assert err <= BF16_TOL, err
 
 
+@pytest.mark.parametrize("games,T", [(1024, 32), (640, 16), (384, 16)], ids=["rows64", "rows48", "rows32"])
 @pytest.mark.parametrize("shape", SHAPES, ids=["d64", "d240", "d256mha"])
-def test_bf16_tall_prefill_with_conditioning(device, shape):
-    """Prefill of 1024 rows x 32 tokens (32768 token rows): the fused layer kernel runs in
-    its taller row blocks, here with per-layer and value embeddings, partial FF chunks and
-    uneven column splits.  The last tokens' hidden states and the written keys / values
-    against the oracle's bf16 rounding path."""
+def test_bf16_tall_prefill_with_conditioning(device, shape, games, T):
+    """Prefill of 1024 rows x 32 tokens (32768 token rows: 64-row blocks of the fused layer
+    kernel on 256 CUs), 640 x 16 (10240 rows: 48-row blocks) and 384 x 16 (6144 rows: 32-row
+    blocks), here with per-layer and value embeddings, partial FF chunks and uneven column
+    splits.  The last tokens' hidden states and the written keys / values against the
+    oracle's bf16 rounding path."""
 
     config = TrunkConfig(**shape)
     state = random_trunk(config, seed=6)
@@ -368,7 +370,6 @@ def test_bf16_tall_prefill_with_conditioning(device, shape):
     trunk.load_state_dict({k[len("trunk."):]: v for k, v in state.items()})
     trunk = trunk.to(device)
     ref = RefTrunk(state, ref_config_of(config), "bf16")
-    games, T = 1024, 32
     native_cache, ref_cache = cache_pair(config, games, T, torch.bfloat16, device)
     gen = torch.Generator().manual_seed(7)
     raw = torch.randn(games, T, config.d_model, generator=gen)
@@ -381,7 +382,7 @@ def test_bf16_tall_prefill_with_conditioning(device, shape):
             dev = lambda t: None if t is None else t.to(device)  # noqa: E731
             got = trunk.forward_prefill(*trunk.condition(dev(raw), dev(ple_l), dev(ve_l)), native_cache, rows.to(device))
     err = max_err(got, want)
-    sample = torch.tensor([0, 5, 511, 1023])
+    sample = torch.tensor([0, 5, games // 2 - 1, games - 1])
 
     def rel_err(a, b):
         # Cache entries are bf16 values of any magnitude (value embeddings are added before
