@@ -17,14 +17,15 @@
 //                                               embedding) written to the pool
 //
 // Work split: the block's eight waves split every stage's output columns (32 each); the
-// A operand (BM rows x 256 k, bf16) is read from LDS by all eight waves, the B operand
-// (weights) streams from L2 straight into each wave's registers: lane l loads 16 bytes of
-// W row (col 16 j + l % 16) at k = 32 ks + 8 (l / 16), exactly the
-// v_mfma_f32_16x16x32_bf16 B-fragment, so weights never touch LDS.  Each fragment
-// register is refilled with stage s+2's fragment right after its MFMAs of stage s, which
-// keeps up to two stages of weights (256 KB per block) in flight.  Row statistics of the
-// LayerNorms reduce over the 16 lanes of a fragment row with shuffles, then over the
-// eight waves in LDS.
+// panel (BM rows x 256 k, bf16) is read from LDS by all eight waves, the weights stream
+// from L2 straight into each wave's registers: lane l loads 16 bytes of W row
+// (col 16 j + l % 16) at k = 32 ks + 8 (l / 16), one v_mfma_f32_16x16x32_bf16 operand
+// fragment, so weights never touch LDS.  Every product is formed transposed (W . A^T: the
+// weight fragment is the MFMA's A operand), so a lane ends up holding four consecutive
+// columns of one row (layer_dev.h).  Each fragment register is refilled with the next
+// stage's fragment right after its MFMAs, so a stage of weights (128 KB per block) is in
+// flight while the current one multiplies.  Row statistics of the LayerNorms reduce over
+// the four lane groups with lane swaps, then over the eight waves in LDS.
 #include "common.h"
 #include "fragment.h"
 #include "layer.h"

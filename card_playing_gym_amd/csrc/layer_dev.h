@@ -20,11 +20,13 @@ namespace cg {
 namespace {
 
 #ifndef TAIL_RING
-#define TAIL_RING 2
+#define TAIL_RING 1
 #endif
-// Stages of weights in flight per wave: two up to 48-row blocks; one for taller blocks,
-// whose four or more row tiles per fragment keep each stage's MFMAs busy that much longer
-// (and whose accumulators leave no room for a second ring stage).
+// Stages of weights in flight per wave beyond the one being multiplied.  One is enough:
+// measured with two (128 more VGPRs per wave) against one, the kernel ran 21.5 / 21.3 us per
+// decode layer (16 rows), 28.5 / 28.4 at 32 rows and 100.6 / 99.0 at 48 (the weight stream
+// is bound by the L1 return path, not by the loads in flight); 64-row blocks have no room
+// for two.
 template <int BM>
 constexpr int ring_of() { return BM > 48 ? 1 : TAIL_RING; }
 
