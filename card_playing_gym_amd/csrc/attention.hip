@@ -556,6 +556,9 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
 #ifndef TR_WAVES_PER_EU
 #define TR_WAVES_PER_EU 4
 #endif
+#ifndef TR_LAST_MERGES
+#define TR_LAST_MERGES 1
+#endif
 // QRAW: the queries are stored in the cache type (16-byte aligned rows); they load as they
 // are and the softmax scale multiplies the fp32 scores.  Otherwise any query type is read,
 // scaled and rounded to the cache type.
@@ -597,6 +600,19 @@ void decode_attention_tr_kernel(AttnArgs a) {
   // no visible key and no store.
   const bool unit_ok = unit < a.n_seqs * a.kv_heads;
   if (!unit_ok && SPLIT != 2) return;
+  // One unit per block whose queries form a single group: its waves merge through an LDS
+  // counter (the last one merges) instead of two block barriers.  The counter is cleared
+  // behind one barrier that every wave of the block reaches (they all have the same unit).
+  __shared__ int merge_count;
+  bool last_merges = false;
+  if constexpr (SPLIT == 4 && TR_LAST_MERGES) {
+    const int nq0 = int(a.seq_start ? 0 : a.T) * (a.n_heads / a.kv_heads);
+    last_merges = !a.seq_start && gridDim.y == 1 && nq0 <= NQT * 16;
+    if (last_merges) {
+      if (threadIdx.x == 0) merge_count = 0;
+      __syncthreads();
+    }
+  }
   const int b = unit_ok ? unit / a.kv_heads : 0, h = unit_ok ? unit % a.kv_heads : 0;
   const int li = lane & 15, lg = lane >> 4;
   const int G = a.n_heads / a.kv_heads;
@@ -854,6 +870,33 @@ void decode_attention_tr_kernel(AttnArgs a) {
   #pragma unroll
           for (int dh = 0; dh < DH; ++dh) part_o[wave][qt][dh][lane] = acc[qt][dh];
         }
+        if (last_merges) {
+          // The unit's last wave to get here merges and stores; the others leave at once
+          // (no block barrier: a wave with one key tile does not wait for one with two).
+          // One increment per wave (lane 0), its result broadcast to the wave.
+          int done = 0;
+          if (lane == 0) done = __hip_atomic_fetch_add(&merge_count, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+          done = __builtin_amdgcn_readfirstlane(done);
+          if (done != SPLIT - 1) return;
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  #pragma unroll
+          for (int qt = 0; qt < L; ++qt) {
+            float mm = part_m[0][qt][li];
+  #pragma unroll
+            for (int w = 1; w < SPLIT; ++w) mm = fmaxf(mm, part_m[w][qt][li]);
+            float l = 0.f;
+  #pragma unroll
+            for (int dh = 0; dh < DH; ++dh) acc[qt][dh] = f32x4{0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+            for (int w = 0; w < SPLIT; ++w) {
+              const float c = fast_exp2(part_m[w][qt][li] - mm);
+              l = fmaf(part_l[w][qt][li], c, l);
+  #pragma unroll
+              for (int dh = 0; dh < DH; ++dh) acc[qt][dh] += part_o[w][qt][dh][lane] * c;
+            }
+            lsum[qt] = l;
+          }
+        } else {
         __syncthreads();
         if (part == 0) {
   #pragma unroll
@@ -876,6 +919,7 @@ void decode_attention_tr_kernel(AttnArgs a) {
         }
         __syncthreads();  // partials consumed before the next query group reuses them
         if (part != 0) return;
+        }
       }
       // ---- normalise and store: lane l holds dims 16 dh + 4 (l / 16) + i of query column l % 16
       const bool o4 = a.out_dtype == (sizeof(TKV) == 2 && std::is_same<TKV, bf16>::value ? CG_BF16 : CG_F16) &&
