@@ -189,7 +189,8 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     first..first+count-1, replayed on their own with HIP events on the launch stream
     (packed chunks through the packed entry point, as the step launches them)."""
 
-    from card_playing_gym_amd.nn.decode import attention_into, attention_order, attention_packed_into
+    from card_playing_gym_amd.nn.decode import (
+        attention_into, attention_order, attention_packed_into, attention_packed_order)
     from card_playing_gym_amd.synthetic import kv_bytes
 
     cfg = bench.config
@@ -203,11 +204,15 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     out = torch.empty((tokens, H, D), device=dev, dtype=torch.bfloat16)
     key_lengths = torch.empty(games, dtype=torch.int64, device=dev)
     rows = torch.empty(games, dtype=torch.int64, device=dev)
-    # Decode steps launch the persistent kernel with the step's unit order, computed once per
-    # step (before the layers) by the trunk: here before each step's timed launches.
+    # The trunk computes each step's unit order once, before the layers (decode steps: for the
+    # persistent kernel; packed chunks: longest units first): here before the timed launches.
     orders = {}
-    if not bench.chunks:
-        for step in range(first, first + count):
+    for step in range(first, first + count):
+        if bench.chunks:
+            orders[step] = attention_packed_order(
+                bench.cache.k[0], bench.rows_all[step], bench.positions_all[step], bench.seq_starts[step],
+                bench.plans[step].n_tokens, H, bench.max_len)
+        else:
             orders[step] = attention_order(
                 bench.cache.k[0], bench.rows_all[step] if bench.gathered else None, bench.positions_all[step] + 1,
                 games, H, 1, bench.max_len)
@@ -226,7 +231,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
             starts[i].record(stream)
             for layer in range(cfg.n_layers):
                 attention_packed_into(out[:n], q[:n], bench.cache.k[layer], bench.cache.v[layer], rows, key_lengths,
-                                      bench.seq_starts[step], bench.max_len, D ** -0.5)
+                                      bench.seq_starts[step], bench.max_len, D ** -0.5, orders[step])
         else:
             key_lengths.copy_(bench.positions_all[step] + 1)
             starts[i].record(stream)

@@ -186,6 +186,14 @@ _SIGNATURES = {
         [c_void_p, c_int32, c_int64, c_int64, P(KVLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
          c_int32, c_float, c_void_p, c_int32, c_void_p],
     ),
+    "cg_decode_attention_packed_order": (
+        c_int32, [P(KVLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p],
+    ),
+    "cg_decode_attention_packed_ordered": (
+        c_int32,
+        [c_void_p, c_int32, c_int64, c_int64, P(KVLayer), c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
+         c_int32, c_float, c_void_p, c_int32, c_void_p, c_void_p],
+    ),
     "cg_trunk_create": (c_int32, [P(TrunkConfig), P(LayerParams), c_void_p, c_void_p, c_int32, P(c_void_p)]),
     "cg_trunk_refresh": (c_int32, [c_void_p, c_void_p]),
     "cg_trunk_destroy": (c_int32, [c_void_p]),

@@ -1503,11 +1503,58 @@ extern "C" int cg_decode_attention_order(const cg_kv_layer *layer, const int64_t
   });
 }
 
+namespace {
+// The arguments of a packed run (cg_decode_attention_packed's layout).
+AttnArgs packed_args(const void *q, int32_t q_dtype, int64_t q_st, int64_t q_sh, const cg_kv_layer *layer,
+                     const int64_t *rows, const int64_t *positions, const int64_t *seq_start, int32_t n_seqs,
+                     int32_t n_tokens, int32_t n_heads, int32_t span, float scale, void *out, int32_t out_dtype) {
+  AttnArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_st = q_st;
+  a.q_sh = q_sh;
+  a.q_sb = 0;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.o_st = int64_t(n_heads) * layer->head_dim;
+  a.o_sh = layer->head_dim;
+  a.o_sb = 0;
+  a.k = layer->k;
+  a.v = layer->v;
+  a.kv_dtype = layer->dtype;
+  a.rows = rows;
+  a.key_lengths = positions;
+  a.kl_add = 1;
+  a.seq_start = seq_start;
+  a.n_tokens = n_tokens;
+  a.n_seqs = n_seqs;
+  a.n_heads = n_heads;
+  a.kv_heads = layer->kv_heads;
+  a.head_dim = layer->head_dim;
+  a.T = 0;
+  a.max_len = layer->max_len;
+  a.capacity = layer->capacity;
+  a.span = (span <= 0 || span > layer->max_len) ? layer->max_len : span;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return a;
+}
+}  // namespace
+
 extern "C" int cg_decode_attention_packed(const void *q, int32_t q_dtype, int64_t q_st, int64_t q_sh,
                                           const cg_kv_layer *layer, const int64_t *rows,
                                           const int64_t *positions, const int64_t *seq_start,
                                           int32_t n_seqs, int32_t n_tokens, int32_t n_heads, int32_t span,
                                           float scale, void *out, int32_t out_dtype, void *stream) {
+  return cg_decode_attention_packed_ordered(q, q_dtype, q_st, q_sh, layer, rows, positions, seq_start, n_seqs,
+                                            n_tokens, n_heads, span, scale, out, out_dtype, nullptr, stream);
+}
+
+extern "C" int cg_decode_attention_packed_ordered(const void *q, int32_t q_dtype, int64_t q_st, int64_t q_sh,
+                                                  const cg_kv_layer *layer, const int64_t *rows,
+                                                  const int64_t *positions, const int64_t *seq_start,
+                                                  int32_t n_seqs, int32_t n_tokens, int32_t n_heads,
+                                                  int32_t span, float scale, void *out, int32_t out_dtype,
+                                                  const int32_t *order, void *stream) {
   return guarded([&] {
     check_layer(layer);
     dtype_size(q_dtype);
@@ -1515,34 +1562,26 @@ extern "C" int cg_decode_attention_packed(const void *q, int32_t q_dtype, int64_
     CG_REQUIRE(n_seqs >= 0 && n_tokens >= 0, CG_ERR_INVALID, "n_seqs and n_tokens must be non-negative");
     if (n_seqs == 0 || n_tokens == 0) return;
     CG_REQUIRE(q && out && positions && seq_start, CG_ERR_INVALID, "q, out, positions and seq_start are required");
-    AttnArgs a{};
-    a.q = q;
-    a.q_dtype = q_dtype;
-    a.q_st = q_st;
-    a.q_sh = q_sh;
-    a.q_sb = 0;
-    a.out = out;
-    a.out_dtype = out_dtype;
-    a.o_st = int64_t(n_heads) * layer->head_dim;
-    a.o_sh = layer->head_dim;
-    a.o_sb = 0;
-    a.k = layer->k;
-    a.v = layer->v;
-    a.kv_dtype = layer->dtype;
-    a.rows = rows;
-    a.key_lengths = positions;
-    a.kl_add = 1;
-    a.seq_start = seq_start;
-    a.n_tokens = n_tokens;
-    a.n_seqs = n_seqs;
-    a.n_heads = n_heads;
-    a.kv_heads = layer->kv_heads;
-    a.head_dim = layer->head_dim;
-    a.T = 0;
-    a.max_len = layer->max_len;
-    a.capacity = layer->capacity;
-    a.span = (span <= 0 || span > layer->max_len) ? layer->max_len : span;
-    a.scale_log2 = scale * 1.4426950408889634f;
+    AttnArgs a = packed_args(q, q_dtype, q_st, q_sh, layer, rows, positions, seq_start, n_seqs, n_tokens, n_heads,
+                             span, scale, out, out_dtype);
+    a.order = order;
     launch_decode_attention(a, as_stream(stream));
+  });
+}
+
+extern "C" int cg_decode_attention_packed_order(const cg_kv_layer *layer, const int64_t *rows,
+                                                const int64_t *positions, const int64_t *seq_start,
+                                                int32_t n_seqs, int32_t n_tokens, int32_t n_heads, int32_t span,
+                                                int32_t *order, void *stream) {
+  return guarded([&] {
+    check_layer(layer);
+    CG_REQUIRE(n_seqs >= 0 && n_tokens >= 0, CG_ERR_INVALID, "n_seqs and n_tokens must be non-negative");
+    CG_REQUIRE(n_heads > 0 && n_heads % layer->kv_heads == 0, CG_ERR_INVALID,
+               "n_heads must be a positive multiple of kv_heads");
+    if (n_seqs == 0) return;
+    CG_REQUIRE(order && positions && seq_start, CG_ERR_INVALID, "order, positions and seq_start are required");
+    AttnArgs a = packed_args(nullptr, CG_F32, 0, 0, layer, rows, positions, seq_start, n_seqs, n_tokens, n_heads, span,
+                             1.0f, nullptr, CG_F32);
+    launch_attention_order(a, order, as_stream(stream));
   });
 }

@@ -110,11 +110,14 @@ def attention_packed_into(
     seq_start: torch.Tensor,
     span: int,
     scale: float,
+    order: torch.Tensor | None = None,
 ) -> None:
     """Packed chunks: q [N, H, D] (unit last stride), sequence b owning tokens
     ``seq_start[b] .. seq_start[b+1]-1`` (packing.py:36-40 bounds) at cache row ``rows[b]``;
     its token t sees keys below ``positions[b] + 1 + t`` (its prefix and its own chunk,
-    already in the pool).  Writes out [N, H, D] (contiguous)."""
+    already in the pool).  Writes out [N, H, D] (contiguous).  ``order`` (from
+    :func:`attention_packed_order` for the same rows, positions, bounds and span) deals the
+    units longest first, as the trunk step does."""
 
     import ctypes
 
@@ -125,12 +128,42 @@ def attention_packed_into(
     rows = None if rows is None else index(rows)
     positions, seq_start = index(positions), index(seq_start)
     layer = _layer(k, v)
+    if order is not None and (order.dtype != torch.int32 or order.numel() < positions.numel() * k.shape[1]):
+        raise ValueError("order must be an int32 tensor of n_seqs * kv_heads entries (attention_packed_order)")
     nat.call(
-        "cg_decode_attention_packed", q.data_ptr(), dtype_code(q.dtype), q.stride(0), q.stride(1),
+        "cg_decode_attention_packed_ordered", q.data_ptr(), dtype_code(q.dtype), q.stride(0), q.stride(1),
         ctypes.byref(layer), None if rows is None else rows.data_ptr(), positions.data_ptr(), seq_start.data_ptr(),
         positions.numel(), q.shape[0], q.shape[1], int(span), float(scale), out.data_ptr(), dtype_code(out.dtype),
-        stream_handle(q.device),
+        None if order is None else order.data_ptr(), stream_handle(q.device),
     )
+
+
+def attention_packed_order(
+    k: torch.Tensor,
+    rows: torch.Tensor | None,
+    positions: torch.Tensor,
+    seq_start: torch.Tensor,
+    n_tokens: int,
+    heads: int,
+    span: int,
+) -> torch.Tensor:
+    """The (row, KV head) units of a packed run sorted by work, most first (int32
+    [n_seqs * kv_heads]), for :func:`attention_packed_into`."""
+
+    import ctypes
+
+    require_device(k, positions, seq_start)
+    index = lambda t: t.to(torch.int64).contiguous()  # noqa: E731
+    rows = None if rows is None else index(rows)
+    positions, seq_start = index(positions), index(seq_start)
+    layer = _layer(k, k)
+    order = torch.empty(max(positions.numel() * k.shape[1], 1), dtype=torch.int32, device=k.device)
+    nat.call(
+        "cg_decode_attention_packed_order", ctypes.byref(layer), None if rows is None else rows.data_ptr(),
+        positions.data_ptr(), seq_start.data_ptr(), positions.numel(), int(n_tokens), heads, int(span),
+        order.data_ptr(), stream_handle(k.device),
+    )
+    return order
 
 
 @torch.library.custom_op("cardgym_hip::decode_attention", mutates_args=())

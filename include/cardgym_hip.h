@@ -170,6 +170,21 @@ int cg_decode_attention_packed(const void *q, int32_t q_dtype, int64_t q_st, int
                                const cg_kv_layer *layer, const int64_t *rows, const int64_t *positions,
                                const int64_t *seq_start, int32_t n_seqs, int32_t n_tokens, int32_t n_heads,
                                int32_t span, float scale, void *out, int32_t out_dtype, void *stream);
+/* The unit order the trunk step uses for a packed run (no counterpart in the reference: a
+ * scheduling aid).  cg_decode_attention_packed_order writes order (int32 [n_seqs * kv_heads]:
+ * the (row, KV head) units sorted by 64-key tiles x 16-query tiles, most work first) for
+ * these rows, positions, chunk bounds and span; cg_decode_attention_packed_ordered then deals
+ * the units in that order (16-bit pools, head_dim 32 / 64; other pools ignore it).  Results
+ * do not depend on the order beyond its being a permutation of the units, and it stays valid
+ * for every layer of one step. */
+int cg_decode_attention_packed_order(const cg_kv_layer *layer, const int64_t *rows, const int64_t *positions,
+                                     const int64_t *seq_start, int32_t n_seqs, int32_t n_tokens, int32_t n_heads,
+                                     int32_t span, int32_t *order, void *stream);
+int cg_decode_attention_packed_ordered(const void *q, int32_t q_dtype, int64_t q_st, int64_t q_sh,
+                                       const cg_kv_layer *layer, const int64_t *rows, const int64_t *positions,
+                                       const int64_t *seq_start, int32_t n_seqs, int32_t n_tokens,
+                                       int32_t n_heads, int32_t span, float scale, void *out,
+                                       int32_t out_dtype, const int32_t *order, void *stream);
 
 /* ---- fused trunk ------------------------------------------------------------------ */
 

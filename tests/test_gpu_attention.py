@@ -169,3 +169,45 @@ def test_packed_decode_attention_matches_oracle(device, dtype, D, heads, kv_head
     want = torch.cat([exact[b, :, : counts[b]].transpose(0, 1) for b in range(B)])
     err = (got - want).abs().max().item()
     assert err <= TOL[dtype], f"vs float64: {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,heads,kv_heads", [(32, 8, 2), (64, 4, 1), (16, 4, 2)])
+def test_packed_order_is_a_work_sort_and_keeps_results(device, dtype, D, heads, kv_heads):
+    """cg_decode_attention_packed_order / _ordered: the order is a permutation of the
+    (row, KV head) units with non-increasing work (64-key tiles of the last token's keys,
+    capped at the span, x 16-query tiles; a row outside the pool counts 0), and dealing the
+    units in it leaves every output bit as the unordered launch writes it."""
+
+    from card_playing_gym_amd.nn.decode import attention_packed_into, attention_packed_order
+
+    gen = torch.Generator().manual_seed(D * 11 + heads)
+    capacity, max_len, B = 70, 600, 61
+    k_cache = torch.randn(capacity, kv_heads, max_len, D, generator=gen).to(dtype)
+    v_cache = torch.randn(capacity, kv_heads, max_len, D, generator=gen).to(dtype)
+    rows = torch.randperm(capacity, generator=gen)[:B]
+    counts = torch.randint(1, 17, (B,), generator=gen)
+    positions = torch.randint(0, max_len - 17, (B,), generator=gen)
+    positions[:4] = torch.tensor([0, 63, 64, max_len - 17])  # tile boundaries and the pool's end
+    seq_start = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(counts, 0)])
+    n = int(seq_start[-1])
+    span = 500  # below the longest rows: the cap shows in the work
+    q = torch.randn(n, heads, D, generator=gen).to(device)
+    args = (k_cache.to(device), v_cache.to(device), rows.to(device), positions.to(device), seq_start.to(device))
+
+    order = attention_packed_order(args[0], args[2], args[3], args[4], n, heads, span).cpu()
+    assert sorted(order.tolist()) == list(range(B * kv_heads))
+    g = heads // kv_heads
+    kend = torch.clamp(positions + counts, max=span)  # keys of the chunk's last token
+    work = (kend + 63) // 64 * ((g * counts + 15) // 16)
+    unit_work = work.repeat_interleave(kv_heads)
+    seq = unit_work[order.long()]
+    assert bool((seq[:-1] >= seq[1:]).all()), seq.tolist()
+
+    plain = torch.empty(n, heads, D, dtype=dtype, device=device)
+    ordered = torch.empty_like(plain)
+    attention_packed_into(plain, q, *args, span, 1.0 / math.sqrt(D))
+    attention_packed_into(ordered, q, *args, span, 1.0 / math.sqrt(D), order.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(plain.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       ordered.view(torch.int16 if dtype != torch.float32 else torch.int32))
