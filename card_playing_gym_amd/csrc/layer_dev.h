@@ -96,6 +96,17 @@ __device__ __forceinline__ void load_wslice(uint4 (&buf)[KS][FN], const Slice &s
   }
 }
 
+// Keeps k-step ks's refill loads where they are written, right after the MFMAs that read
+// the registers.  Left to itself the scheduler sinks a stage's refills below most of its
+// MFMAs (the wave waited down to 3 loads in flight before issuing the next 16), so every
+// wave's weight stream nearly drained once per stage, all waves at about the same time.
+#ifndef CG_TAIL_PIN_REFILL
+#define CG_TAIL_PIN_REFILL 1
+#endif
+__device__ __forceinline__ void pin_refill() {
+  if (CG_TAIL_PIN_REFILL) __builtin_amdgcn_sched_barrier(0);
+}
+
 // acc[i][j] += (W fragment j) x (panel rows 16 i + li)^T over all 256 k: the product of
 // stage_mma (fragment.h) with the operands swapped, so the result tile is transposed
 // (lane (li, lg) holds row 16 i + li, columns 4 lg .. +3 of the 16-column fragment j).
@@ -122,6 +133,7 @@ __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned
 #pragma unroll
         for (int j = 0; j < FN; ++j) w[ks][j] = wload16(next.w, base[j] + 1024 * ks);
       }
+      pin_refill();
     }
   } else {
     uint4 af[2][FM];
@@ -141,6 +153,7 @@ __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned
 #pragma unroll
         for (int j = 0; j < FN; ++j) w[ks][j] = wload16(next.w, base[j] + 1024 * ks);
       }
+      pin_refill();
     }
   }
 }
@@ -360,6 +373,18 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
       arow[k] = bload16(ra, (uint32_t(m0_ + c / cpr) * d + 8 * (c % cpr)) * 2);
     }
   }
+  // The residual rows the out-projection adds (the lane's own transposed tiles) are read
+  // here too, so their latency overlaps the attention rows' instead of following it.
+  f32x4 xr[FM][FN];
+  if (POST) {
+    const Rsrc rs = rsrc(a.x_src, xbytes);
+    const int li = lane & 15, lg = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        xr[i][j] = bload4f(rs, (uint32_t(m0_ + 16 * i + li) * d + cw + 16 * j + 4 * lg) * 4);
+  }
   constexpr int NB_UP = (4 * PANEL + THREADS - 1) / THREADS;
   float v_up[NB_UP], v_vec[5];
   int v_tok[3];
@@ -492,17 +517,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     const Slice nx = stage_slice(a, p, refill ? s + RING : s, cw);
     uint4(&cur)[KS][FN] = wbuf[s % RING];
     if (kind == ST_OUT) {
-      // ---- out-proj + residual (x1, kept), then LN(ln_mlp) -> panel
-      const Rsrc rs = rsrc(opaque_ptr(a.x_src), xbytes);
-      f32x4 xr[FM][FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          xr[i][j] = bload4f(rs, (uint32_t(m0 + 16 * i + li) * d + cw + 16 * j + 4 * lg) * 4);
-      // Issue the residual loads ahead of this stage's weight refills: loads complete in
-      // order, so the epilogue then waits only for them, not for the next stage's weights.
-      __builtin_amdgcn_sched_barrier(0);
+      // ---- out-proj + residual (x1, kept; xr was read in the prologue), then LN(ln_mlp) -> panel
       zero<FM>(acc);
       stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
 #pragma unroll
