@@ -116,6 +116,17 @@ __device__ __forceinline__ void load_slice(uint4 (&buf)[KS][FN], const Slice &s,
   }
 }
 
+// Keeps k-step ks's refill loads where they are written, right after the MFMAs that read
+// the registers.  Left to itself the scheduler sinks a stage's refills below most of its
+// MFMAs (the wave waited down to 3 loads in flight before issuing the next 16), so every
+// wave's weight stream nearly drained once per stage, all waves at about the same time.
+#ifndef CG_PIN_REFILL
+#define CG_PIN_REFILL 1
+#endif
+__device__ __forceinline__ void pin_refill() {
+  if (CG_PIN_REFILL) __builtin_amdgcn_sched_barrier(0);
+}
+
 // acc[i][j] += panel rows (16 i + l % 16) x W fragment j over all 256 k (panel columns
 // past a stage's width are zero, and output columns past the matrix are discarded by the
 // epilogue, so no step needs a guard).  Each fragment register is refilled with the next
@@ -146,6 +157,7 @@ __device__ __forceinline__ void stage_mma(f32x4 (&acc)[FM][FN], const unsigned c
 #pragma unroll
         for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
       }
+      pin_refill();
     }
   } else {
     // Taller blocks: the A fragments of k-step ks + 1 are read while ks multiplies (all of
@@ -167,6 +179,7 @@ __device__ __forceinline__ void stage_mma(f32x4 (&acc)[FM][FN], const unsigned c
 #pragma unroll
         for (int j = 0; j < FN; ++j) w[ks][j] = bload16(next.w, base[j] + 1024 * ks);
       }
+      pin_refill();
     }
   }
 }

@@ -96,17 +96,6 @@ __device__ __forceinline__ void load_wslice(uint4 (&buf)[KS][FN], const Slice &s
   }
 }
 
-// Keeps k-step ks's refill loads where they are written, right after the MFMAs that read
-// the registers.  Left to itself the scheduler sinks a stage's refills below most of its
-// MFMAs (the wave waited down to 3 loads in flight before issuing the next 16), so every
-// wave's weight stream nearly drained once per stage, all waves at about the same time.
-#ifndef CG_TAIL_PIN_REFILL
-#define CG_TAIL_PIN_REFILL 1
-#endif
-__device__ __forceinline__ void pin_refill() {
-  if (CG_TAIL_PIN_REFILL) __builtin_amdgcn_sched_barrier(0);
-}
-
 // acc[i][j] += (W fragment j) x (panel rows 16 i + li)^T over all 256 k: the product of
 // stage_mma (fragment.h) with the operands swapped, so the result tile is transposed
 // (lane (li, lg) holds row 16 i + li, columns 4 lg .. +3 of the 16-column fragment j).
