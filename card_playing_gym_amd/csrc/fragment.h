@@ -64,9 +64,9 @@ __device__ __forceinline__ void lds_barrier() {
   __asm__ volatile("" ::: "memory");
 }
 
-// Returns v unchanged but opaque to the optimiser.  Row and lane indices are passed
-// through it at the top of every stage so per-lane offsets are formed where they are used
-// instead of being hoisted out of the stage loop (where they exhaust registers).
+// Returns v unchanged but opaque to the optimiser: a kernel short of registers passes row
+// and lane indices through it so per-lane offsets are formed where they are used instead of
+// being hoisted out of its stage loop.
 __device__ __forceinline__ int opaque(int v) {
   __asm__ volatile("" : "+s"(v));
   return v;

@@ -497,8 +497,10 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 
 #pragma clang loop unroll(full)
   for (int s = 0; s < S; ++s) {
-    const int m0 = opaque(blk * BM);
-    const int lane_o = opaque_lane(lane);
+    // Row and lane offsets are formed once and kept (172 VGPRs at 16 rows): re-forming them
+    // in every stage through opaque() cost ~130 VALU instructions per wave and 1.8 %.
+    const int m0 = blk * BM;
+    const int lane_o = lane;
     const int li = lane_o & 15, lg = lane_o >> 4;
     int c;
     const int kind = stage_kind(p, s, c);
