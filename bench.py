@@ -169,15 +169,16 @@ class Bench:
         return sum(self.plans[s].n_tokens for s in range(first, first + count))
 
 
-def traffic_record(workload: str, steps: int, warmup: int, bytes_per_launch: float):
+def traffic_record(workload: str, steps: int, warmup: int, bytes_per_launch: float, kernel: str):
     """HBM bytes per decode-attention launch from the committed counter passes
     (FETCH_SIZE / WRITE_SIZE, calibrated on a plain copy) for this exact run: same workload,
-    step count and warm-up, and the same algorithmic bytes."""
+    step count and warm-up, the same kernel and the same algorithmic bytes."""
 
     if not TRAFFIC_FILE.exists():
         return None
     for record in json.loads(TRAFFIC_FILE.read_text()).get("records", []):
-        if (record.get("workload"), record.get("steps"), record.get("warmup")) != (workload, steps, warmup):
+        if (record.get("workload"), record.get("steps"), record.get("warmup"), record.get("kernel")) != (
+                workload, steps, warmup, kernel):
             continue
         if abs(record.get("algorithmic_bytes_per_launch", 0) - bytes_per_launch) <= 0.001 * bytes_per_launch:
             return record.get("bytes_per_launch")
@@ -190,7 +191,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     (packed chunks through the packed entry point, as the step launches them)."""
 
     from card_playing_gym_amd.nn.decode import (
-        attention_into, attention_order, attention_packed_into, attention_packed_order)
+        attention_into, attention_packed_into, attention_packed_order)
     from card_playing_gym_amd.synthetic import kv_bytes
 
     cfg = bench.config
@@ -204,18 +205,14 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     out = torch.empty((tokens, H, D), device=dev, dtype=torch.bfloat16)
     key_lengths = torch.empty(games, dtype=torch.int64, device=dev)
     rows = torch.empty(games, dtype=torch.int64, device=dev)
-    # The trunk computes each step's unit order once, before the layers (decode steps: for the
-    # persistent kernel; packed chunks: longest units first): here before the timed launches.
+    # Packed chunks: the trunk computes each step's unit order once, before the layers
+    # (longest units first): here before the timed launches.  Decode steps run unordered.
     orders = {}
-    for step in range(first, first + count):
-        if bench.chunks:
+    if bench.chunks:
+        for step in range(first, first + count):
             orders[step] = attention_packed_order(
                 bench.cache.k[0], bench.rows_all[step], bench.positions_all[step], bench.seq_starts[step],
                 bench.plans[step].n_tokens, H, bench.max_len)
-        else:
-            orders[step] = attention_order(
-                bench.cache.k[0], bench.rows_all[step] if bench.gathered else None, bench.positions_all[step] + 1,
-                games, H, 1, bench.max_len)
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
@@ -238,7 +235,7 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
             for layer in range(cfg.n_layers):
                 attention_into(out.view(games, H, 1, D), q.view(games, H, 1, D), bench.cache.k[layer],
                                bench.cache.v[layer], rows if bench.gathered else None, key_lengths, bench.max_len,
-                               D ** -0.5, orders[step])
+                               D ** -0.5)
         ends[i].record(stream)
         kv = kv_bytes(plan, cfg.n_layers, cfg.n_kv_heads, D, itemsize)
         total_bytes += kv + cfg.n_layers * plan.n_tokens * H * D * (q.element_size() + 2)  # + q read + out write (bf16)
@@ -248,18 +245,17 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     avg_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
     achieved = bytes_per_launch / (avg_us * 1e-6) / 1e9
+    # Query tiles of 16 per (row, KV head) unit: one for a decode token's 4 heads, four for
+    # chunks of up to 16 tokens.
+    kernel = "decode_attention_tr_kernel<bf16,32,4>" if bench.chunks else "decode_attention_tr_kernel<bf16,32,1>"
     return {
-        # Query tiles of 16 per (row, KV head) unit: one for a decode token's 4 heads, four
-        # for chunks of up to 16 tokens.
-        "kernel": ("decode_attention_tr_kernel<bf16,32,4>" if bench.chunks else
-                   "decode_attention_stream_kernel<bf16,32>" if all(o is not None for o in orders.values()) else
-                   "decode_attention_tr_kernel<bf16,32,1>"),
+        "kernel": kernel,
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": traffic_record(bench.workload.name, count, first, bytes_per_launch),
+        "traffic": traffic_record(bench.workload.name, count, first, bytes_per_launch, kernel),
         "avg_launch_us": round(avg_us, 2),
         "algorithmic_bytes_per_launch": int(bytes_per_launch),
         "launches": launches,

@@ -1378,12 +1378,13 @@ void launch_kv(const AttnArgs &a, hipStream_t s) {
 
 }  // namespace
 
-// Spans from which the persistent kernel is taken.  Measured on MI355X (bf16 pool, head_dim
-// 32, 4 query heads per KV head): with up to 8-9 tiles per unit (config 3, span 538) both
-// kernels stream at the same rate (50.2 / 50.4 us per launch) and the order costs a launch
-// per step; with rows of up to 32 tiles and a wide spread of lengths (config 4, span 2048:
-// restarted games beside long ones) the split kernel's longest blocks finish last, and the
-// sorted deal takes 87.4 -> 80.8 us per launch (2.09 -> 1.98 ms per step).
+// Spans from which an ordered decode call takes the persistent kernel.  Measured on MI355X
+// (bf16 pool, head_dim 32, 4 query heads per KV head): with up to 8-9 tiles per unit
+// (config 3, span 538) both kernels stream at the same rate and the order costs a launch per
+// step.  With the split kernel's earlier 64-key tiles and barrier merges, rows of up to 32
+// tiles and a wide spread of lengths (config 4, span 2048) favoured the sorted deal (87.4 ->
+// 80.8 us per launch); with 32-key tiles and the last-wave merge the split kernel matches
+// it there (82.7 against 82.6-84.7 us), so the trunk step no longer orders decode waves.
 #ifndef STREAM_MIN_SPAN
 #define STREAM_MIN_SPAN 1024
 #endif

@@ -401,15 +401,18 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
                                                 w.tok_out, hidden, d);
     CG_LAUNCHED();
   }
-  // Decode runs with long possible rows take the persistent attention kernel, and packed
-  // chunks on a 16-bit pool deal their units longest first; either way the unit order (by
-  // work) is the same for every layer of the step: computed once here.
+  // Packed chunks on a 16-bit pool deal their units longest first: the unit order (by work)
+  // is the same for every layer of the step, computed once here.  One-token decode runs take
+  // the split kernel in unit order: with 32-key tiles and the last-wave merge it streams as
+  // fast as the persistent kernel of the ordered entry points at spans of 2048-16384 keys
+  // (324.9 / 342.1 / 353.3 / 370.4 against 330.1 / 335.1 / 351.6 / 387.0 us per launch for
+  // 8192 x 2048 ... 1024 x 16384 rows of random lengths) without the order's 10-26 us launch
+  // per step (config 4: 1.855-1.887 -> 1.837 ms per step).
 #ifndef CG_PACKED_ORDER
 #define CG_PACKED_ORDER 1
 #endif
-  const bool streams = attention_streams(attn_args(0));
-  const bool ordered = streams || (CG_PACKED_ORDER && r.seq_start && (cache[0].dtype == CG_BF16 || cache[0].dtype == CG_F16) &&
-                                   (D == 32 || D == 64));
+  const bool ordered = CG_PACKED_ORDER && r.seq_start && (cache[0].dtype == CG_BF16 || cache[0].dtype == CG_F16) &&
+                       (D == 32 || D == 64);
   if (ordered) launch_attention_order(attn_args(0), w.order, s);
   auto attention = [&](int l) {
     AttnArgs a = attn_args(l);

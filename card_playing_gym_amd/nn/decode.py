@@ -48,8 +48,9 @@ def attention_into(
 ) -> None:
     """Writes attention of q [B, H, T, D] (any strides, unit last stride) into out
     [B, H, T, D] (contiguous).  ``order`` (from :func:`attention_order` for the same rows,
-    key lengths, T and span) makes decode runs take the persistent kernel, as the trunk
-    step does."""
+    key lengths, T and span) makes decode runs take the persistent kernel instead of the
+    split kernel the trunk step uses (the two stream at the same rate; results agree to
+    rounding)."""
 
     import ctypes
 

@@ -140,8 +140,9 @@ int cg_decode_attention(const void *q, int32_t q_dtype, int64_t q_sb, int64_t q_
                         int32_t B, int32_t n_heads, int32_t T, int32_t span, float scale, void *out,
                         int32_t out_dtype, void *stream);
 
-/* cg_decode_attention with a work order, as the trunk step launches it for decode waves
- * (same op and meaning, cardgym/nn/cuda_decode.py:188-202).  cg_decode_attention_order
+/* cg_decode_attention with a work order, through the persistent kernel (same op and
+ * meaning, cardgym/nn/cuda_decode.py:188-202; the trunk step itself runs decode waves
+ * through the split kernel, which streams as fast without the order).  cg_decode_attention_order
  * writes order (int32 [B * kv_heads]: the (row, KV head) units sorted by their number of
  * 64-key tiles, longest first) for these rows, key lengths, T and span, and sets *streams
  * (if not NULL) to 1 when the persistent kernel applies (16-bit pool, head_dim 32 or 64,

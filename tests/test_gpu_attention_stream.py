@@ -1,6 +1,6 @@
 """The persistent decode-attention kernel (cg_decode_attention_ordered with the order of
-cg_decode_attention_order): the kernel the trunk step launches for decode waves on a
-16-bit pool whose span reaches 1024 keys.  Checked against the oracle's grouped attention
+cg_decode_attention_order): the kernel the ordered entry points launch for decode runs on
+a 16-bit pool whose span reaches 1024 keys.  Checked against the oracle's grouped attention
 (cardgym/nn/trunk.py:225-256 restated) in float64 and with the reference's rounding, at the
 bf16 bar (2e-2), and against the split kernel (cg_decode_attention without an order) on the
 same inputs.
