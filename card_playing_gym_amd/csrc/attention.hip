@@ -564,7 +564,10 @@ __global__ __launch_bounds__(256) void decode_attention_mfma_kernel(AttnArgs a) 
 // scaled and rounded to the cache type.
 // Waves per SIMD the split kernel is built for: multi-tile forms at head_dim 32 keep two.
 template <int NQT, int D>
-constexpr int tr_waves_per_eu() { return D == 32 ? (NQT == 1 ? TR_WAVES_PER_EU : 2) : 1; }
+#ifndef TR_MQ_WAVES_PER_EU
+#define TR_MQ_WAVES_PER_EU 2
+#endif
+constexpr int tr_waves_per_eu() { return D == 32 ? (NQT == 1 ? TR_WAVES_PER_EU : TR_MQ_WAVES_PER_EU) : 1; }
 
 template <typename TKV, int D, int NQT, int SPLIT, int KT, int DEPTH, bool QRAW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(tr_waves_per_eu<NQT, D>())))
@@ -1276,6 +1279,12 @@ __global__ __launch_bounds__(1024) void attention_order_kernel(const AttnArgs a,
 #ifndef TR_ONE_WAVE_ITEMS
 #define TR_ONE_WAVE_ITEMS 2048
 #endif
+// Keys per tile when one wave takes a whole multi-token item: 32-key tiles take the form
+// from 202 to 143 VGPRs (three waves per SIMD instead of two) and measured 76.3 -> 74.6 us
+// per launch at config 5, 33.5 -> 30.6 us at prefill.
+#ifndef TR_MQ_KT
+#define TR_MQ_KT 32
+#endif
 
 // The 16-bit-pool kernels for one query form (QRAW: queries stored in the cache type).
 template <typename TKV, int D, bool QRAW>
@@ -1296,7 +1305,7 @@ void launch_tr(const AttnArgs &a, int queries, hipStream_t s) {
     // split its key tiles and merge.
     const dim3 grid_q(1, unsigned(std::min<int64_t>((int64_t(queries) + 63) / 64, 65535)));
     if (a.span <= 64 || int64_t(units) * grid_q.y >= TR_ONE_WAVE_ITEMS) {
-      decode_attention_tr_kernel<TKV, D, 4, 1, 64, TR_MQ_DEPTH, QRAW><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
+      decode_attention_tr_kernel<TKV, D, 4, 1, TR_MQ_KT, TR_MQ_DEPTH, QRAW><<<dim3((units + 3) / 4, grid_q.y), 256, 0, s>>>(a);
     } else {
       decode_attention_tr_kernel<TKV, D, 4, TR_SPLIT, 64, 1, QRAW><<<dim3(tr_grid, grid_q.y), 256, 0, s>>>(a);
     }
