@@ -131,8 +131,8 @@ void launch_tail(const TailArgs &a, hipStream_t s) {
   const int nc = (a.d_ff + PANEL - 1) / PANEL, nq = (a.n_qkv + PANEL - 1) / PANEL;
   const int mode = !a.do_post ? 0 : (a.final_ln ? 2 : 1);
   auto go = [&](auto k16, auto k32, auto k48, auto k64) {
-    // Params (layer_dev.h): d_ff + 5 PANEL floats, the QKV column map, token slots and rows.
-    const size_t dyn = (size_t(a.d_ff) + 5 * PANEL) * 4 + (3 * PANEL / 4) * 8 + size_t(bm) * (8 + 4);
+    // Params (layer_dev.h): (nc + 5) PANEL floats, the QKV column map, token slots and rows.
+    const size_t dyn = (size_t(nc) + 5) * PANEL * 4 + (3 * PANEL / 4) * 8 + size_t(bm) * (8 + 4);
     const unsigned grid = unsigned((a.M + bm - 1) / bm);
     if (bm == 64) k64<<<grid, THREADS, dyn, s>>>(a);
     else if (bm == 48) k48<<<grid, THREADS, dyn, s>>>(a);

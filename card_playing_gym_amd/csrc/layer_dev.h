@@ -253,7 +253,7 @@ __device__ __forceinline__ void row_stats_t(const f32x4 (&v)[BM / 16][FN], int c
 // Per-layer vectors, the QKV column map and the block's token slots, staged in LDS by the
 // kernel prologue (layout: params_floats / params_bytes below).
 struct Params {
-  float *b_up, *b_down, *ln2_w, *ln2_b, *ln_w, *ln_b;  // [d_ff] and [PANEL] each
+  float *b_up, *b_down, *ln2_w, *ln2_b, *ln_w, *ln_b;  // [NC PANEL] (0 past d_ff) and [PANEL] each
   int2 *qkv_map;     // [3 PANEL / 4]: per run of four QKV columns {role (0 q, 1 k, 2 v, -1 none),
                      // offset (q: column; k / v: element offset inside a pool slot row)}
   int64_t *tok_slot;  // [BM]: element offset of the token's pool slot (head 0), -1: no write
@@ -322,7 +322,7 @@ __device__ __forceinline__ void next_prologue(const TailArgs &a, const Params &p
 // a compile-time constant, so the fully unrolled stage loop folds every stage's kind and
 // the weight registers flow from stage to stage without merges.
 // Row block `blk` of one layer tail.  LDS: panel [BM rows of ROWB bytes], hbuf two or four more,
-// red 2 * WAVES * BM + 2 * BM floats, dyn the Params (d_ff + 5 PANEL floats, then 3 BM ints).
+// red 2 * WAVES * BM + 2 * BM floats, dyn the Params ((NC + 5) PANEL floats, the QKV map, then 3 BM ints).
 template <int BM, int MODE, int NC, int NQ>
 __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned char *panel,
                                           unsigned char (*hbuf)[BM * ROWB], float *red, float *dyn) {
@@ -418,7 +418,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 
   Params prm;
   prm.b_up = dyn;
-  prm.b_down = dyn + a.d_ff;
+  prm.b_down = dyn + NC * PANEL;  // b_up holds NC full chunks, zero past d_ff
   prm.ln2_w = prm.b_down + PANEL;
   prm.ln2_b = prm.ln2_w + PANEL;
   prm.ln_w = prm.ln2_b + PANEL;
@@ -437,7 +437,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 #pragma unroll
   for (int k = 0; k < NB_UP; ++k) {
     const int i = tid + k * THREADS;
-    if (i < a.d_ff) prm.b_up[i] = v_up[k];
+    if (i < NC * PANEL) prm.b_up[i] = v_up[k];  // v_up is 0 past d_ff
   }
   if (tid < PANEL) {
     prm.b_down[tid] = v_vec[0];
@@ -533,15 +533,14 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
       for (int j = 0; j < FN; ++j) {
         const int col = cw + 16 * j + 4 * lg;
         // Columns past d_ff (a partial last chunk) must stay exactly 0: the down projection's
-        // fragments for those k are not zero.  Uniform per (wave, j): a multiply, no branch.
-        const bool ok = PANEL * c + cw + 16 * j < a.d_ff;
-        const float keep = ok ? 1.f : 0.f;
-        const f32x4 bias = lds4(prm.b_up + (ok ? PANEL * c + col : 0));
+        // fragments for those k are not zero.  Their weight loads read past the buffer (0), so
+        // the product is 0, and the staged bias is 0 there: GELU(0) = 0 with no guard.
+        const f32x4 bias = lds4(prm.b_up + PANEL * c + col);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
           f32x4 g;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) g[r] = gelu_fast(acc[i][j][r] + bias[r]) * keep;
+          for (int r = 0; r < 4; ++r) g[r] = gelu_fast(acc[i][j][r] + bias[r]);
           *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + col * 2) = pack_bf16x4(g);
         }
       }
