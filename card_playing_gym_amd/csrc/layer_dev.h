@@ -508,23 +508,35 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     const Slice nx = stage_slice(a, p, refill ? s + RING : s, cw);
     uint4(&cur)[KS][FN] = wbuf[s % RING];
     if (kind == ST_OUT) {
-      // ---- out-proj + residual (x1, kept; xr was read in the prologue), then LN(ln_mlp) -> panel
-      zero<FM>(acc);
+      // ---- out-proj + residual (x1, kept; xr was read in the prologue and seeds the
+      //      accumulators), then LN(ln_mlp) -> panel
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = xr[i][j];
       stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const bool ok = m0 + 16 * i + li < a.M && cw + 16 * j < d;
-          accd[i][j] = ok ? acc[i][j] + xr[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
+          accd[i][j] = ok ? acc[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
       float mean[FM], rstd[FM];
       row_stats_t<BM>(accd, cw, d, a.eps, mean, rstd, red, wave, li, lg);
       ln_to_panel<BM>(accd, mean, rstd, prm.ln2_w, prm.ln2_b, panel, cw, d, li, lg);
       lds_barrier();
     } else if (kind == ST_UP) {
-      // ---- up chunk c + GELU -> hbuf[c] (or hbuf[c & 1] when interleaved)
-      zero<FM>(acc);
+      // ---- up chunk c (the bias seeds the accumulators) + GELU -> hbuf[c] (or hbuf[c & 1]
+      //      when interleaved).  Columns past d_ff (a partial last chunk) must stay exactly 0:
+      //      the down projection's fragments for those k are not zero.  Their weight loads
+      //      read past the buffer (0) and the staged bias is 0 there, so GELU(0) = 0.
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const f32x4 bias = lds4(prm.b_up + PANEL * c + cw + 16 * j + 4 * lg);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) acc[i][j] = bias;
+      }
       stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
       unsigned char *hb = hbuf[p.ups_first ? c : (c % HB)];
       // One GELU buffer: every wave has finished down chunk c - 1's reads of it.
@@ -532,15 +544,11 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = cw + 16 * j + 4 * lg;
-        // Columns past d_ff (a partial last chunk) must stay exactly 0: the down projection's
-        // fragments for those k are not zero.  Their weight loads read past the buffer (0), so
-        // the product is 0, and the staged bias is 0 there: GELU(0) = 0 with no guard.
-        const f32x4 bias = lds4(prm.b_up + PANEL * c + col);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
           f32x4 g;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) g[r] = gelu_fast(acc[i][j][r] + bias[r]);
+          for (int r = 0; r < 4; ++r) g[r] = gelu_fast(acc[i][j][r]);
           *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + col * 2) = pack_bf16x4(g);
         }
       }
