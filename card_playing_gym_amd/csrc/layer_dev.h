@@ -173,6 +173,16 @@ __device__ __forceinline__ u32x2 pack16x4(f32x4 v) {
   return u32x2{uint32_t(e0.bits) | uint32_t(e1.bits) << 16, uint32_t(e2.bits) | uint32_t(e3.bits) << 16};
 }
 
+// The same bits as pack16x4<bf16> with two v_cvt_pk_bf16_f32: the instruction rounds to
+// nearest even exactly as Tensor.to does (checked on MI355X over a million random and edge
+// patterns) but keeps a NaN's payload, so NaN inputs are first replaced by the quiet NaN
+// whose conversion is torch's 0x7fc0.
+__device__ __forceinline__ f32x4 canonical_nan(f32x4 v) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = v[r] != v[r] ? __uint_as_float(0x7fc00000u) : v[r];
+  return v;
+}
+
 __device__ __forceinline__ void st_nt(float *p, f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p)); }
 __device__ __forceinline__ void st_nt(void *p, u32x2 v) { __builtin_nontemporal_store(v, reinterpret_cast<u32x2 *>(p)); }
 
@@ -183,7 +193,7 @@ __device__ __forceinline__ f32x4 lds4(const float *p) { return *reinterpret_cast
 
 // Four consecutive values of `dtype` (fp32, bf16 or fp16) stored at p (aligned to their size).
 __device__ __forceinline__ void store4(void *p, int dtype, f32x4 v) {
-  if (dtype == CG_BF16) st_nt(p, pack16x4<bf16>(v));
+  if (dtype == CG_BF16) st_nt(p, pack_bf16x4(canonical_nan(v)));
   else if (dtype == CG_F16) st_nt(p, pack16x4<f16>(v));
   else st_nt(static_cast<float *>(p), v);
 }
@@ -515,12 +525,14 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = xr[i][j];
       stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
+      // Rows past M are exactly 0 already (their residual and attention rows read past the
+      // buffers); columns past d read a neighbouring row's residual and are cleared (uniform).
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const bool ok = m0 + 16 * i + li < a.M && cw + 16 * j < d;
-          accd[i][j] = ok ? acc[i][j] : f32x4{0.f, 0.f, 0.f, 0.f};
+          accd[i][j] = acc[i][j];
+          if (cw + 16 * j >= d) accd[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
       float mean[FM], rstd[FM];
       row_stats_t<BM>(accd, cw, d, a.eps, mean, rstd, red, wave, li, lg);
