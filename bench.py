@@ -72,6 +72,11 @@ def parse() -> argparse.Namespace:
         "and exit (for rocprofv3 counter and trace passes over the step's kernels)",
     )
     p.add_argument(
+        "--compaction-probe", action="store_true",
+        help="run only the KV-compaction measurement on the workload's pool, print it and exit "
+        "(for rocprofv3 trace passes over the copy kernels)",
+    )
+    p.add_argument(
         "--train-probe", action="store_true",
         help="run only the fp32 training step (our path, no reference) and print its timings, then exit "
         "(for a rocprofv3 kernel trace of the training kernels)",
@@ -915,6 +920,10 @@ def main() -> int:
         return 0
     if args.train_probe:
         print(json.dumps({"probe": "train_step", **train_step_time(bench, with_reference=False)}), flush=True)
+        return 0
+    if args.compaction_probe:
+        with torch.no_grad():
+            print(json.dumps({"probe": "compaction", **compaction_time(bench)}), flush=True)
         return 0
     with torch.no_grad():
         bench.load(0)
