@@ -13,6 +13,7 @@
 
 #include "attention.h"
 #include "common.h"
+#include "fragment.h"
 #include "gemm.h"
 #include "layer.h"
 
@@ -157,6 +158,43 @@ __global__ void rmsnorm_rows_kernel(const XT *__restrict__ x, const float *__res
   }
   const float r = rsqrtf(wave_sum(s) / float(d) + eps);
   for (int k = lane; k < d; k += 64) out[k] = to_f32(from_f32<XT>(to_f32(in[k]) * r)) * gain[k];
+}
+
+// The embedding form above for d = 64 Q with 16-byte aligned rows: four rows per wave, 16
+// lanes per row, Q float4 per lane, so the id -> row -> sum chains of four rows overlap
+// (one row per wave left the launch waiting on those latencies).
+template <int Q>
+__global__ void embed_rmsnorm_rows4_kernel(const float *__restrict__ table, int32_t vocab,
+                                           const int64_t *__restrict__ ids, const float *__restrict__ gain,
+                                           float eps, float *__restrict__ y, int32_t n, int32_t *__restrict__ flag) {
+  constexpr int D = 64 * Q;
+  const int lane = threadIdx.x & 63, l16 = lane & 15;
+  const int row = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const bool live = row < n;
+  const int64_t id = live ? ids[row] : 0;
+  const bool ok = live && id >= 0 && id < vocab;
+  if (live && !ok && l16 == 0 && flag) flag[0] = 1;
+  const float4 *in = reinterpret_cast<const float4 *>(table + (ok ? id : 0) * D);
+  float4 v[Q];
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    v[q] = ok ? in[l16 + 16 * q] : float4{0.f, 0.f, 0.f, 0.f};
+    s = fmaf(v[q].x, v[q].x, s);
+    s = fmaf(v[q].y, v[q].y, s);
+    s = fmaf(v[q].z, v[q].z, s);
+    s = fmaf(v[q].w, v[q].w, s);
+  }
+  const float r = rsqrtf(sum16(s) / float(D) + eps);
+  if (!live) return;
+  const float4 *g4 = reinterpret_cast<const float4 *>(gain);
+  float4 *out = reinterpret_cast<float4 *>(y + int64_t(row) * D);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const float4 g = g4[l16 + 16 * q];  // a row with a bad id is written as zeros
+    out[l16 + 16 * q] = ok ? float4{v[q].x * r * g.x, v[q].y * r * g.y, v[q].z * r * g.z, v[q].w * r * g.w}
+                           : float4{0.f, 0.f, 0.f, 0.f};
+  }
 }
 
 // fp32 -> bf16 (round to nearest even) weight copies.
@@ -679,8 +717,14 @@ int cg_embed_rmsnorm(const float *table, int32_t vocab, const int64_t *ids, cons
     CG_REQUIRE(table && ids && gain && y, CG_ERR_INVALID, "table, ids, gain and y are required");
     CG_REQUIRE(n >= 0 && d > 0 && vocab > 0, CG_ERR_INVALID, "bad sizes");
     if (n == 0) return;
-    rmsnorm_rows_kernel<float><<<rows_grid(n, 4), 256, 0, as_stream(stream)>>>(
-        nullptr, table, vocab, ids, gain, eps, y, n, d, flag);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(gain) |
+                           reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+    const unsigned grid4 = unsigned((int64_t(n) + 15) / 16);  // four waves of four rows
+    hipStream_t s = as_stream(stream);
+    if (aligned && d == 256) embed_rmsnorm_rows4_kernel<4><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
+    else if (aligned && d == 128) embed_rmsnorm_rows4_kernel<2><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
+    else if (aligned && d == 64) embed_rmsnorm_rows4_kernel<1><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
+    else rmsnorm_rows_kernel<float><<<rows_grid(n, 4), 256, 0, s>>>(nullptr, table, vocab, ids, gain, eps, y, n, d, flag);
     CG_LAUNCHED();
   });
 }

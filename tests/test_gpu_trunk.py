@@ -444,3 +444,38 @@ def test_forward_with_grad_enabled_is_differentiable(device):
     with torch.no_grad():
         plain = trunk(*trunk.condition(x, None, None))
     torch.testing.assert_close(out.detach(), plain, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("d", [64, 96, 128, 256])
+@pytest.mark.parametrize("n", [1, 5, 16, 17, 333])
+def test_embed_rmsnorm_matches_fp64_reference(device, d, n):
+    """RMSNorm(table[ids]) * gain (the trunk's input norm, trunk.py's embedding then
+    input_norm) against a float64 restatement, for the four-rows-per-wave form (d = 64, 128,
+    256) and the one-row-per-wave form (d = 96), with row counts that leave partial waves and
+    blocks.  An id outside the table gives a zero row and raises the flag."""
+
+    from card_playing_gym_amd import _native as nat
+    from card_playing_gym_amd.nn import ops
+    from card_playing_gym_amd.nn.kv_cache import stream_handle
+
+    gen = torch.Generator().manual_seed(1000 * d + n)
+    vocab, eps = 97, 1e-5
+    table = torch.randn(vocab, d, generator=gen).to(device)
+    gain = (torch.rand(d, generator=gen) + 0.5).to(device)
+    ids = torch.randint(0, vocab, (n,), generator=gen).to(device)
+    out = ops.embed_rmsnorm(table, ids, gain, eps)
+    x = table.double()[ids.long()]
+    ref = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * gain.double()
+    assert (out.double() - ref).abs().max().item() <= 1e-5 * max(1.0, ref.abs().max().item())
+
+    bad = ids.clone()
+    bad[n // 2] = vocab
+    y = torch.full((n, d), float("nan"), device=device)
+    flag = torch.zeros(1, dtype=torch.int32, device=device)
+    nat.call("cg_embed_rmsnorm", table.data_ptr(), vocab, bad.data_ptr(), gain.data_ptr(), eps, y.data_ptr(), n, d,
+             flag.data_ptr(), stream_handle(device))
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+    assert torch.equal(y[n // 2], torch.zeros(d, device=device))
+    keep = torch.arange(n, device=device) != n // 2
+    assert torch.equal(y[keep], out[keep])
