@@ -140,11 +140,17 @@ __device__ __forceinline__ int unit_tiles(const AttnArgs &a, int u) {
   return int(min<int64_t>(ORDER_BUCKETS - 1, (kend + STREAM_KT - 1) / STREAM_KT * qtiles));
 }
 
+// Units whose bucket the first pass keeps in LDS for the second (one byte each); units
+// past it are measured again from their lengths.
+constexpr int ORDER_CACHE = 32768;
+
 // order = the units sorted by descending work: a counting sort by one whole block
 // (any size; ties land in any order, which changes only which wave computes a unit, not its
 // result).  Called by every thread of the block.
 __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restrict__ order) {
+  static_assert(ORDER_BUCKETS <= 256, "buckets are kept as bytes");
   __shared__ int hist[ORDER_BUCKETS], scan[2][ORDER_BUCKETS];
+  __shared__ uint8_t bucket[ORDER_CACHE];
   const int tid = threadIdx.x, nt = blockDim.x;
   const int U = a.n_seqs * a.kv_heads;
   for (int i = tid; i < ORDER_BUCKETS; i += nt) hist[i] = 0;
@@ -158,6 +164,7 @@ __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restri
     for (int k = 0; k < PER; ++k) {
       const int u = base + tid + k * nt;
       w[k] = u < U ? unit_tiles(a, u) : -1;
+      if (u < U && u < ORDER_CACHE) bucket[u] = uint8_t(w[k]);
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k)
@@ -182,7 +189,7 @@ __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restri
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int u = base + tid + k * nt;
-      w[k] = u < U ? unit_tiles(a, u) : -1;
+      w[k] = u >= U ? -1 : u < ORDER_CACHE ? int(bucket[u]) : unit_tiles(a, u);
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k)

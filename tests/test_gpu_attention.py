@@ -211,3 +211,31 @@ def test_packed_order_is_a_work_sort_and_keeps_results(device, dtype, D, heads, 
     torch.cuda.synchronize()
     assert torch.equal(plain.view(torch.int16 if dtype != torch.float32 else torch.int32),
                        ordered.view(torch.int16 if dtype != torch.float32 else torch.int32))
+
+
+@pytest.mark.parametrize("B, distinct", [(3000, 1), (3000, 3), (20000, 5)])
+def test_packed_order_with_shared_work_and_many_units(device, B, distinct):
+    """The unit sort when most units share a few work values (games of one length: whole
+    waves fall into one bucket) and, at 20000 rows x 2 KV heads, more units than the sort
+    keeps in LDS between its passes: still a permutation with non-increasing work."""
+
+    from card_playing_gym_amd.nn.decode import attention_packed_order
+
+    gen = torch.Generator().manual_seed(B + distinct)
+    capacity, max_len, kv_heads, heads, D = 64, 256, 2, 8, 32
+    k_cache = torch.zeros(capacity, kv_heads, max_len, D, dtype=torch.bfloat16, device=device)
+    rows = torch.randint(0, capacity, (B,), generator=gen)
+    rows[::97] = capacity  # outside the pool: work 0
+    levels = torch.tensor([7, 70, 200, 130, 1])[:distinct]
+    positions = levels[torch.randint(0, distinct, (B,), generator=gen)]
+    counts = torch.full((B,), 4, dtype=torch.int64)
+    seq_start = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(counts, 0)])
+    n, span = int(seq_start[-1]), max_len
+    order = attention_packed_order(k_cache, rows.to(device), positions.to(device), seq_start.to(device), n, heads,
+                                   span).cpu()
+    assert torch.equal(order.sort().values, torch.arange(B * kv_heads, dtype=order.dtype))
+    kend = torch.clamp(positions + counts, max=span)
+    work = (kend + 63) // 64 * ((heads // kv_heads * counts + 15) // 16)
+    work[rows >= capacity] = 0
+    seq = work.repeat_interleave(kv_heads)[order.long()]
+    assert bool((seq[:-1] >= seq[1:]).all())
