@@ -23,6 +23,11 @@ struct cg_heads {
   size_t wp_bytes = 0, w1_bytes = 0;
 };
 
+// One block per (16 rows, stage) rather than per 16 rows (see heads_kernel).
+#ifndef CG_HEADS_SPLIT
+#define CG_HEADS_SPLIT 1
+#endif
+
 namespace cg {
 namespace {
 
@@ -36,12 +41,17 @@ struct HeadArgs {
 
 __device__ __forceinline__ float round_bf16(float v) { return to_f32(from_f32<bf16>(v)); }
 
-template <int NP>
+// SPLIT: the block's stage is blockIdx.y (policy chunk y < NP, else the value MLP), so the
+// grid holds NP + 1 blocks per 16 rows; each reads its rows and one stage's weights.
+// Otherwise one block runs every stage of its rows, the next stage's weights loading during
+// the current one's MFMAs.
+template <int NP, bool SPLIT>
 __global__ __launch_bounds__(THREADS) void heads_kernel(const HeadArgs a) {
   constexpr int BM = 16;
   constexpr int S = NP + 1;  // NP policy chunks, then the value MLP's first layer
   __shared__ __align__(16) unsigned char panel[BM * ROWB];
   __shared__ __align__(16) unsigned char mid[BM * ROWB];
+  __shared__ float w2s[16 * PANEL + 16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, lg = lane >> 4;
@@ -65,8 +75,19 @@ __global__ __launch_bounds__(THREADS) void heads_kernel(const HeadArgs a) {
     return Slice{rsrc(opaque_ptr(a.w1), uint32_t(a.d_mid) * kd * 64), kd, cw / 16, 0};
   };
   uint4 wbuf[2][KS][FN];
-  load_slice(wbuf[0], slice(0), lane);
-  if (S > 1) load_slice(wbuf[1], slice(1), lane);
+  load_slice(wbuf[0], slice(SPLIT ? int(blockIdx.y) : 0), lane);
+  if (!SPLIT && S > 1) load_slice(wbuf[1], slice(1), lane);
+  // The value MLP's second layer (W2 then b2, at most 16 x PANEL + 16 floats) is requested
+  // now and parked in LDS after the first layer, so no global round trip follows the barrier.
+  constexpr int W2R = (16 * PANEL + 16 + THREADS - 1) / THREADS;
+  const bool value_block = !SPLIT || int(blockIdx.y) == NP;
+  const int nw2 = a.n_value * a.d_mid;
+  float w2r[W2R];
+#pragma unroll
+  for (int q = 0; q < W2R; ++q) {
+    const int i = tid + q * THREADS;
+    w2r[q] = !value_block ? 0.f : i < nw2 ? a.w2[i] : i < nw2 + a.n_value ? a.b2[i - nw2] : 0.f;
+  }
 
   // Zero both panels (k >= d and mid columns >= d_mid stay zero), then the hidden rows.
   for (int o = tid * 16; o < BM * ROWB; o += THREADS * 16) {
@@ -86,41 +107,61 @@ __global__ __launch_bounds__(THREADS) void heads_kernel(const HeadArgs a) {
   }
   lds_barrier();
 
-  f32x4 acc[1][FN];
-#pragma clang loop unroll(full)
-  for (int s = 0; s < S; ++s) {
-    const bool refill = s + 2 < S;
-    const Slice nx = slice(refill ? s + 2 : s);
-    uint4(&cur)[KS][FN] = wbuf[s & 1];
-    zero<1>(acc);
-    stage_mma<1>(acc, panel, cur, nx, refill, opaque_lane(lane));
-    if (s < NP) {
-      // ---- policy chunk s: logits (bias and output rounded like the bf16 Linear)
+  // ---- policy chunk s: logits (bias and output rounded like the bf16 Linear)
+  auto policy_out = [&](const f32x4 (&acc)[1][FN], int s) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = PANEL * s + cw + 16 * j + li;
-        if (n >= a.n_policy) continue;
-        const float bias = round_bf16(a.bp[n]);
+    for (int j = 0; j < FN; ++j) {
+      const int n = PANEL * s + cw + 16 * j + li;
+      if (n >= a.n_policy) continue;
+      const float bias = round_bf16(a.bp[n]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + 4 * lg + r;
-          if (m < a.M) gst(a.logits + int64_t(m) * a.n_policy + n, round_bf16(acc[0][j][r] + bias));
-        }
-      }
-    } else {
-      // ---- value MLP, first layer: GELU of the rounded pre-activation -> mid panel
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = cw + 16 * j + li;
-        if (n >= a.d_mid) continue;
-        const float bias = round_bf16(a.b1[n]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float g = gelu_fast(round_bf16(acc[0][j][r] + bias));
-          *reinterpret_cast<bf16 *>(mid + (4 * lg + r) * ROWB + n * 2) = from_f32<bf16>(g);
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 4 * lg + r;
+        if (m < a.M) gst(a.logits + int64_t(m) * a.n_policy + n, round_bf16(acc[0][j][r] + bias));
       }
     }
+  };
+  // ---- value MLP, first layer: GELU of the rounded pre-activation -> mid panel
+  auto value_mid = [&](const f32x4 (&acc)[1][FN]) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = cw + 16 * j + li;
+      if (n >= a.d_mid) continue;
+      const float bias = round_bf16(a.b1[n]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float g = gelu_fast(round_bf16(acc[0][j][r] + bias));
+        *reinterpret_cast<bf16 *>(mid + (4 * lg + r) * ROWB + n * 2) = from_f32<bf16>(g);
+      }
+    }
+  };
+
+  f32x4 acc[1][FN];
+  if constexpr (SPLIT) {
+    const int s = int(blockIdx.y);
+    zero<1>(acc);
+    stage_mma<1>(acc, panel, wbuf[0], slice(s), false, opaque_lane(lane));
+    if (s < NP) {
+      policy_out(acc, s);
+      return;
+    }
+    value_mid(acc);
+  } else {
+#pragma clang loop unroll(full)
+    for (int s = 0; s < S; ++s) {
+      const bool refill = s + 2 < S;
+      const Slice nx = slice(refill ? s + 2 : s);
+      uint4(&cur)[KS][FN] = wbuf[s & 1];
+      zero<1>(acc);
+      stage_mma<1>(acc, panel, cur, nx, refill, opaque_lane(lane));
+      if (s < NP) policy_out(acc, s);
+      else value_mid(acc);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < W2R; ++q) {
+    const int i = tid + q * THREADS;
+    if (i < nw2 + a.n_value) w2s[i] = round_bf16(w2r[q]);
   }
   lds_barrier();
 
@@ -130,10 +171,10 @@ __global__ __launch_bounds__(THREADS) void heads_kernel(const HeadArgs a) {
     const int row = idx / a.n_value, o = idx % a.n_value;
     float sum = 0.f;
     for (int k = p; k < a.d_mid; k += 16)
-      sum = fmaf(to_f32(*reinterpret_cast<const bf16 *>(mid + row * ROWB + k * 2)), round_bf16(a.w2[o * a.d_mid + k]), sum);
+      sum = fmaf(to_f32(*reinterpret_cast<const bf16 *>(mid + row * ROWB + k * 2)), w2s[o * a.d_mid + k], sum);
     sum = sum16(sum);
     const int m = m0 + row;
-    if (p == 0 && m < a.M) gst(a.values + int64_t(m) * a.n_value + o, round_bf16(sum + round_bf16(a.b2[o])));
+    if (p == 0 && m < a.M) gst(a.values + int64_t(m) * a.n_value + o, round_bf16(sum + w2s[nw2 + o]));
   }
 }
 
@@ -227,20 +268,22 @@ int cg_heads_forward(const cg_heads *heads, const float *hidden, int32_t m, floa
     a.b2 = heads->b2;
     a.logits = logits;
     a.values = values;
-    const unsigned grid = unsigned((int64_t(m) + 15) / 16);
+    const unsigned blocks = unsigned((int64_t(m) + 15) / 16);
+    const int np = (c.n_policy + PANEL - 1) / PANEL;
+    const dim3 grid(blocks, CG_HEADS_SPLIT ? unsigned(np + 1) : 1u);
     hipStream_t s = as_stream(stream);
-    switch ((c.n_policy + PANEL - 1) / PANEL) {
+    switch (np) {
       case 1:
-        heads_kernel<1><<<grid, THREADS, 0, s>>>(a);
+        heads_kernel<1, CG_HEADS_SPLIT><<<grid, THREADS, 0, s>>>(a);
         break;
       case 2:
-        heads_kernel<2><<<grid, THREADS, 0, s>>>(a);
+        heads_kernel<2, CG_HEADS_SPLIT><<<grid, THREADS, 0, s>>>(a);
         break;
       case 3:
-        heads_kernel<3><<<grid, THREADS, 0, s>>>(a);
+        heads_kernel<3, CG_HEADS_SPLIT><<<grid, THREADS, 0, s>>>(a);
         break;
       default:
-        heads_kernel<4><<<grid, THREADS, 0, s>>>(a);
+        heads_kernel<4, CG_HEADS_SPLIT><<<grid, THREADS, 0, s>>>(a);
     }
     CG_LAUNCHED();
   });
