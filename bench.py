@@ -118,11 +118,23 @@ class Bench:
         for k, v in zip(self.cache.k, self.cache.v):
             k.normal_(generator=gen)
             v.normal_(generator=gen)
-        self.tok_buf = torch.zeros((games, 1, 1), dtype=torch.int64, device=dev)
-        self.pos_buf = torch.zeros(games, dtype=torch.int64, device=dev)
-        self.rows_buf = torch.arange(games, dtype=torch.int64, device=dev)
-        self.readout = torch.zeros(games, dtype=torch.int64, device=dev)
         self.gathered = w.mode == "continuous"
+        # The graph reads a step's inputs from one [parts, games] buffer (tokens, positions
+        # and, for gathered rows, the rows) that one copy per step fills.
+        self.inputs_all = None
+        if self.chunks:
+            self.in_buf = torch.zeros((1, games), dtype=torch.int64, device=dev)
+            self.tok_buf = torch.zeros((games, 1, 1), dtype=torch.int64, device=dev)
+        else:
+            parts = [self.tokens.reshape(total, games), self.positions_all]
+            if self.gathered:
+                parts.append(self.rows_all)
+            self.inputs_all = torch.stack(parts, 1).contiguous()
+            self.in_buf = torch.zeros((len(parts), games), dtype=torch.int64, device=dev)
+            self.tok_buf = self.in_buf[0].view(games, 1, 1)
+        self.pos_buf = self.in_buf[1] if not self.chunks else self.in_buf[0]
+        self.rows_buf = self.in_buf[2] if self.gathered else torch.arange(games, dtype=torch.int64, device=dev)
+        self.readout = torch.zeros(games, dtype=torch.int64, device=dev)
         self.graph = None
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
@@ -139,11 +151,10 @@ class Bench:
             return self.model.heads(hidden)
 
     def load(self, step: int) -> None:
-        if not self.chunks:
-            self.tok_buf.view(-1).copy_(self.tokens[step], non_blocking=True)
-        self.pos_buf.copy_(self.positions_all[step], non_blocking=True)
-        if self.gathered:
-            self.rows_buf.copy_(self.rows_all[step], non_blocking=True)
+        if self.chunks:
+            self.pos_buf.copy_(self.positions_all[step], non_blocking=True)
+        else:
+            self.in_buf.copy_(self.inputs_all[step], non_blocking=True)
 
     def capture(self, steps=(0,)) -> None:
         """One graph of the whole step (every step shares it), or for packed chunks one per
