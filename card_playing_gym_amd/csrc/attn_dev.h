@@ -143,6 +143,9 @@ __device__ __forceinline__ int unit_tiles(const AttnArgs &a, int u) {
 // Units whose bucket the first pass keeps in LDS for the second (one byte each); units
 // past it are measured again from their lengths.
 constexpr int ORDER_CACHE = 32768;
+// Up to this many units the order is assembled in LDS and written out in unit order
+// (coalesced) instead of one scattered store per unit.
+constexpr int ORDER_STAGE = 8192;
 
 // order = the units sorted by descending work: a counting sort by one whole block
 // (any size; ties land in any order, which changes only which wave computes a unit, not its
@@ -151,6 +154,7 @@ __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restri
   static_assert(ORDER_BUCKETS <= 256, "buckets are kept as bytes");
   __shared__ int hist[ORDER_BUCKETS], scan[2][ORDER_BUCKETS];
   __shared__ uint8_t bucket[ORDER_CACHE];
+  __shared__ int32_t staged[ORDER_STAGE];
   const int tid = threadIdx.x, nt = blockDim.x;
   const int U = a.n_seqs * a.kv_heads;
   for (int i = tid; i < ORDER_BUCKETS; i += nt) hist[i] = 0;
@@ -193,7 +197,15 @@ __device__ __forceinline__ void order_units(const AttnArgs &a, int32_t *__restri
     }
 #pragma unroll
     for (int k = 0; k < PER; ++k)
-      if (w[k] >= 0) order[atomicAdd(&hist[w[k]], 1)] = base + tid + k * nt;
+      if (w[k] >= 0) {
+        const int slot = atomicAdd(&hist[w[k]], 1);
+        if (U <= ORDER_STAGE) staged[slot] = base + tid + k * nt;
+        else order[slot] = base + tid + k * nt;
+      }
+  }
+  if (U <= ORDER_STAGE) {
+    __syncthreads();
+    for (int i = tid; i < U; i += nt) order[i] = staged[i];
   }
 }
 
