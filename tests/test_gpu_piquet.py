@@ -184,3 +184,30 @@ def test_embedder_refuses_autograd(device):
         module.requires_grad_(False)
         x, _, _ = module(tokens)  # frozen parameters: nothing to differentiate
     assert not x.requires_grad
+
+
+def test_graph_replays_match_eager(device):
+    """Captured in a graph, every replay of the embedder (new tokens copied in, eager calls of
+    the same embedder between replays) matches the eager call bit for bit."""
+
+    config = PiquetModelConfig(d_model=256, card_hidden=64, card_layers=2, card_kernel=3)
+    module, _ = twins(config, 1024, 512, device, seed=5)
+    n = 100
+    static = random_tokens(n, seed=1).to(device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        embed(module, static, device)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph), torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        outs = module(static)
+        kept = module.kept
+    for seed in (2, 3, 4):
+        tokens = random_tokens(n, seed=seed).to(device)
+        x, ple, values, cards = (t.clone() for t in embed(module, tokens, device))
+        static.copy_(tokens)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, g, w in zip(("x", "ple", "values", "cards"), (*outs, kept), (x, ple, values, cards)):
+            assert torch.equal(g, w), (name, seed)
