@@ -152,6 +152,7 @@ class Ragged(ctypes.Structure):
         ("positions", c_void_p),
         ("rows", c_void_p),
         ("readout", c_void_p),
+        ("status", c_void_p),
     ]
 
 

@@ -55,6 +55,34 @@ __device__ __forceinline__ f16 from_f32<f16>(float v) {
   return r;
 }
 
+// Four values at once, the one conversion every 16-bit store of K / V into the pool and of
+// stored queries goes through (the trunk step's fused append and cg_kv_write_step /
+// cg_kv_write_range): 8 bytes, element 0 in the low half.  bf16: NaN inputs are first
+// replaced by the quiet NaN 0x7fc00000, then two v_cvt_pk_bf16_f32 round to nearest even
+// (subnormals kept), so the bits are from_f32<bf16>'s, NaN -> 0x7fc0 included; f16: nearest
+// even per element (v_cvt_f16_f32), as from_f32<f16>.
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+
+__device__ __forceinline__ f32x4 canonical_nan(f32x4 v) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = v[r] != v[r] ? __uint_as_float(0x7fc00000u) : v[r];
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ u32x2 cvt4(f32x4 v);
+template <>
+__device__ __forceinline__ u32x2 cvt4<bf16>(f32x4 v) {
+  return __builtin_bit_cast(u32x2, __builtin_convertvector(canonical_nan(v), bf16x4));
+}
+template <>
+__device__ __forceinline__ u32x2 cvt4<f16>(f32x4 v) {
+  const f16 e0 = from_f32<f16>(v[0]), e1 = from_f32<f16>(v[1]), e2 = from_f32<f16>(v[2]), e3 = from_f32<f16>(v[3]);
+  return u32x2{uint32_t(e0.bits) | uint32_t(e1.bits) << 16, uint32_t(e2.bits) | uint32_t(e3.bits) << 16};
+}
+
 // Bit-preserving conversion between storage types (same type: copy).
 template <typename TO, typename TI>
 __device__ __forceinline__ TO convert(TI v) {

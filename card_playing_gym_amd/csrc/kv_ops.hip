@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <climits>
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -20,20 +21,40 @@ void set_last_error(const std::string &message) { g_last_error = message; }
 
 namespace {
 
-// One thread per (b, t, head, element).  Each thread moves one element: the write is a
-// scatter of 64-128 byte rows, so the launch is bound by the number of rows, not bytes.
-template <typename TC, typename TS>
+// Four consecutive elements of a pool row from fp32 values: the 16-bit types through cvt4,
+// the conversion the trunk step's fused append stores with.
+template <typename TC>
+__device__ __forceinline__ void put4(TC *dst, f32x4 v);
+template <>
+__device__ __forceinline__ void put4<float>(float *dst, f32x4 v) {
+  *reinterpret_cast<f32x4 *>(dst) = v;
+}
+template <>
+__device__ __forceinline__ void put4<bf16>(bf16 *dst, f32x4 v) {
+  *reinterpret_cast<u32x2 *>(dst) = cvt4<bf16>(v);
+}
+template <>
+__device__ __forceinline__ void put4<f16>(f16 *dst, f32x4 v) {
+  *reinterpret_cast<u32x2 *>(dst) = cvt4<f16>(v);
+}
+
+// One thread per (b, t, head, run of VEC elements): VEC 4 when head_dim is a multiple of 4
+// (every head_dim the trunk takes), 1 otherwise.  The write is a scatter of 64-128 byte rows,
+// so the launch is bound by the number of rows, not bytes.  A source of the pool's own type
+// is copied bit for bit (Tensor.to to the same dtype is the identity).
+template <typename TC, typename TS, int VEC>
 __global__ void kv_write_kernel(TC *__restrict__ kc, TC *__restrict__ vc, const TS *__restrict__ ks,
                                 const TS *__restrict__ vs, int64_t ks_b, int64_t ks_h, int64_t ks_t,
                                 int64_t vs_b, int64_t vs_h, int64_t vs_t,
                                 const int64_t *__restrict__ rows, const int64_t *__restrict__ positions,
                                 int32_t start, int32_t B, int32_t T, int32_t KVH, int32_t L,
                                 int32_t D, int32_t capacity) {
-  const int64_t total = int64_t(B) * T * KVH * D;
+  const int runs = D / VEC;
+  const int64_t total = int64_t(B) * T * KVH * runs;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += int64_t(gridDim.x) * blockDim.x) {
-    const int d = int(i % D);
-    int64_t r = i / D;
+    const int d = int(i % runs) * VEC;
+    int64_t r = i / runs;
     const int h = int(r % KVH);
     r /= KVH;
     const int t = int(r % T);
@@ -42,8 +63,18 @@ __global__ void kv_write_kernel(TC *__restrict__ kc, TC *__restrict__ vc, const 
     const int64_t pos = positions ? positions[int64_t(b) * T + t] : int64_t(start) + t;
     if (row < 0 || row >= capacity || pos < 0 || pos >= L) continue;
     const int64_t dst = ((row * KVH + h) * L + pos) * D + d;
-    kc[dst] = convert<TC>(ks[b * ks_b + h * ks_h + t * ks_t + d]);
-    vc[dst] = convert<TC>(vs[b * vs_b + h * vs_h + t * vs_t + d]);
+    const TS *k = ks + b * ks_b + h * ks_h + t * ks_t + d;
+    const TS *v = vs + b * vs_b + h * vs_h + t * vs_t + d;
+    if constexpr (VEC == 1 || std::is_same<TC, TS>::value) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        kc[dst + e] = convert<TC>(k[e]);
+        vc[dst + e] = convert<TC>(v[e]);
+      }
+    } else {
+      put4(kc + dst, f32x4{to_f32(k[0]), to_f32(k[1]), to_f32(k[2]), to_f32(k[3])});
+      put4(vc + dst, f32x4{to_f32(v[0]), to_f32(v[1]), to_f32(v[2]), to_f32(v[3])});
+    }
   }
 }
 
@@ -120,13 +151,18 @@ template <typename TC, typename TS>
 void launch_write(const cg_kv_layer &L, const int64_t *rows, const int64_t *positions, int32_t start,
                   const cg_kv_source &k, const cg_kv_source &v, int32_t B, int32_t T,
                   hipStream_t s) {
-  const int64_t total = int64_t(B) * T * L.kv_heads * L.head_dim;
+  const bool vec = L.head_dim % 4 == 0;
+  const int64_t total = int64_t(B) * T * L.kv_heads * (vec ? L.head_dim / 4 : L.head_dim);
   if (total == 0) return;
-  kv_write_kernel<TC, TS><<<grid_for(total, 256), 256, 0, s>>>(
-      static_cast<TC *>(L.k), static_cast<TC *>(L.v), static_cast<const TS *>(k.data),
-      static_cast<const TS *>(v.data), k.stride_b, k.stride_h, k.stride_t, v.stride_b, v.stride_h,
-      v.stride_t, rows, positions, start, B, T, L.kv_heads, L.max_len, L.head_dim, L.capacity);
-  CG_LAUNCHED();
+  auto go = [&](auto kernel) {
+    kernel<<<grid_for(total, 256), 256, 0, s>>>(
+        static_cast<TC *>(L.k), static_cast<TC *>(L.v), static_cast<const TS *>(k.data),
+        static_cast<const TS *>(v.data), k.stride_b, k.stride_h, k.stride_t, v.stride_b, v.stride_h,
+        v.stride_t, rows, positions, start, B, T, L.kv_heads, L.max_len, L.head_dim, L.capacity);
+    CG_LAUNCHED();
+  };
+  if (vec) go(kv_write_kernel<TC, TS, 4>);
+  else go(kv_write_kernel<TC, TS, 1>);
 }
 
 template <typename TC>

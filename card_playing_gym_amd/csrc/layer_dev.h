@@ -156,31 +156,11 @@ __device__ __forceinline__ float lane_groups_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
-typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
-
 // Four values rounded to bf16 (nearest even; two v_cvt_pk_bf16_f32) as 8 bytes.  For the
 // LDS panels only: a NaN keeps whatever quiet-NaN pattern the instruction gives.
 __device__ __forceinline__ u32x2 pack_bf16x4(f32x4 v) {
   const bf16x4 h = __builtin_convertvector(v, bf16x4);
   return __builtin_bit_cast(u32x2, h);
-}
-// The same with Tensor.to's rounding exactly (NaN -> 0x7fc0; fp16 nearest even), for what
-// is stored in the pool or as the queries.
-template <typename T>
-__device__ __forceinline__ u32x2 pack16x4(f32x4 v) {
-  const T e0 = from_f32<T>(v[0]), e1 = from_f32<T>(v[1]), e2 = from_f32<T>(v[2]), e3 = from_f32<T>(v[3]);
-  return u32x2{uint32_t(e0.bits) | uint32_t(e1.bits) << 16, uint32_t(e2.bits) | uint32_t(e3.bits) << 16};
-}
-
-// The same bits as pack16x4<bf16> with two v_cvt_pk_bf16_f32: the instruction rounds to
-// nearest even exactly as Tensor.to does (checked on MI355X over a million random and edge
-// patterns) but keeps a NaN's payload, so NaN inputs are first replaced by the quiet NaN
-// whose conversion is torch's 0x7fc0.
-__device__ __forceinline__ f32x4 canonical_nan(f32x4 v) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = v[r] != v[r] ? __uint_as_float(0x7fc00000u) : v[r];
-  return v;
 }
 
 __device__ __forceinline__ void st_nt(float *p, f32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p)); }
@@ -191,10 +171,11 @@ __device__ __forceinline__ f32x4 bload4f(Rsrc r, uint32_t off) {
 }
 __device__ __forceinline__ f32x4 lds4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
 
-// Four consecutive values of `dtype` (fp32, bf16 or fp16) stored at p (aligned to their size).
+// Four consecutive values of `dtype` (fp32, bf16 or fp16) stored at p (aligned to their size):
+// the 16-bit types through cvt4, the conversion cg_kv_write_step's stores use as well.
 __device__ __forceinline__ void store4(void *p, int dtype, f32x4 v) {
-  if (dtype == CG_BF16) st_nt(p, pack_bf16x4(canonical_nan(v)));
-  else if (dtype == CG_F16) st_nt(p, pack16x4<f16>(v));
+  if (dtype == CG_BF16) st_nt(p, cvt4<bf16>(v));
+  else if (dtype == CG_F16) st_nt(p, cvt4<f16>(v));
   else st_nt(static_cast<float *>(p), v);
 }
 

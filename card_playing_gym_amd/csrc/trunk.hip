@@ -77,17 +77,27 @@ Workspace carve(const cg_trunk &t, int32_t n_tokens, int32_t n_seqs, char *base)
   return w;
 }
 
+// A readout offset as torch indexing reads it (trunk.py:429, x[batch, readout_offsets]):
+// negative offsets count from the end of the sequence's len tokens; -1 when outside.
+__device__ __forceinline__ int64_t readout_offset(int64_t o, int64_t len) {
+  if (o < 0) o += len;
+  return o >= 0 && o < len ? o : -1;
+}
+
 // Per-token cache slot (row, clamped write position), per-sequence readout token, and
 // per-token output row (tok_out: the sequence whose readout the token is, or -1; every
-// token is its own output row when readout is NULL).  Sequences whose readout offset is
-// outside their chunk get a zero hidden row.
+// token is its own output row when readout is NULL).  Tokens whose row is outside the pool
+// or whose position is negative are neither written nor attended, and sequences whose
+// readout offset is outside their chunk get a zero hidden row; each case sets its status
+// word (plain stores of 1: every writer stores the same value).
 // Padded mode (seq_start NULL): token i belongs to sequence i / T.
 __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t *__restrict__ positions,
                             const int64_t *__restrict__ rows, const int64_t *__restrict__ readout,
                             int32_t n_seqs, int32_t n_tokens, int32_t T, int32_t max_len,
                             int32_t capacity, int32_t *__restrict__ tok_row,
                             int32_t *__restrict__ tok_pos, int32_t *__restrict__ readout_tok,
-                            int32_t *__restrict__ tok_out, float *__restrict__ hidden, int32_t d) {
+                            int32_t *__restrict__ tok_out, float *__restrict__ hidden, int32_t d,
+                            int32_t *__restrict__ status) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n_tokens) {
     int b, t;
@@ -105,19 +115,30 @@ __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t
       t = i % T;
     }
     const int64_t row = rows ? rows[b] : int64_t(b);
-    int64_t pos = positions[b] + t;
+    const int64_t p0 = positions[b];
+    int64_t pos = p0 + t;
     if (pos > max_len - 1) pos = max_len - 1;
-    const bool ok = row >= 0 && row < capacity && pos >= 0;
+    const bool row_ok = row >= 0 && row < capacity, pos_ok = p0 >= 0;
+    const bool ok = row_ok && pos_ok;
     tok_row[i] = ok ? int32_t(row) : -1;
     tok_pos[i] = ok ? int32_t(pos) : 0;
-    tok_out[i] = readout ? (readout[b] == t ? b : -1) : i;
+    if (status && !row_ok) status[0] = 1;
+    if (status && !pos_ok) status[1] = 1;
+    if (readout) {
+      const int64_t len = seq_start ? seq_start[b + 1] - seq_start[b] : int64_t(T);
+      tok_out[i] = readout_offset(readout[b], len) == t ? b : -1;
+    } else {
+      tok_out[i] = i;
+    }
   }
   if (readout && i < n_seqs) {
     const int64_t start = seq_start ? seq_start[i] : int64_t(i) * T;
     const int64_t stop = seq_start ? seq_start[i + 1] : start + T;
-    int64_t r = start + readout[i];
-    if (r < start || r >= stop) {
+    const int64_t o = readout_offset(readout[i], stop - start);
+    int64_t r = start + o;
+    if (o < 0) {
       r = -1;
+      if (status) status[2] = 1;
       if (hidden)
         for (int k = 0; k < d; ++k) hidden[int64_t(i) * d + k] = 0.f;
     }
@@ -436,7 +457,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
     const int n = N > r.n_seqs ? N : r.n_seqs;
     plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout, r.n_seqs, N, r.T,
                                                 max_len, cache[0].capacity, w.tok_row, w.tok_pos, w.readout_tok,
-                                                w.tok_out, hidden, d);
+                                                w.tok_out, hidden, d, r.status);
     CG_LAUNCHED();
   }
   // Packed chunks on a 16-bit pool deal their units longest first: the unit order (by work)

@@ -18,10 +18,16 @@ version counters moved), on the current stream of the handle's device:
 * every eager call that uses the handle, and ``refresh_native()`` on demand (after an
   in-place edit outside an optimiser, e.g. ``with torch.no_grad(): p.mul_(0.5)``).
 
-A handle whose parameters moved (``module.to(other_device)``, a replaced Parameter) is
-retired, not destroyed: a graph captured earlier may still replay against it, and freeing
-its device memory would turn that replay into a memory fault.  Retired handles keep their
-parameters alive, are still refreshed, and are released with their module.
+A handle whose parameters moved (``module.to(other_device)``, ``.double()``, a replaced
+Parameter) is retired, not destroyed: a graph captured earlier may still replay against it,
+and freeing its device memory would turn that replay into a memory fault.  The native
+handles also hold raw pointers into the fp32 parameters themselves (LayerNorm gains and
+biases the kernels read directly, the sources of every refresh), and ``Module._apply``
+swaps ``param.data`` onto new storage inside the same Parameter objects, so each handle
+keeps a detached view of every parameter as it was built: the storage its pointers name
+stays allocated until the handle is released with its module.  A handle whose parameters
+no longer live where its pointers point is never refreshed again: its copies keep the
+weights of the moment the parameters moved.
 """
 
 from __future__ import annotations
@@ -45,6 +51,9 @@ class DerivedCopies:
         self.params = list(params)
         self.device = device
         self.signature = tuple(p.data_ptr() for p in self.params)
+        # Detached views share the parameters' current storage and keep it alive after
+        # param.data is swapped onto new storage (the native handle points into it).
+        self._storage = [p.detach() for p in self.params]
         self.versions = tuple(p._version for p in self.params)
         _LIVE.add(self)
         _install_optimizer_hook()
@@ -75,13 +84,21 @@ class DerivedCopies:
             and all(a is b for a, b in zip(params, self.params))
         )
 
-    def refresh_now(self, stream: int | None = None) -> None:
+    def moved(self) -> bool:
+        """Whether any parameter's data now lives elsewhere than the handle's pointers name."""
+
+        return tuple(p.data_ptr() for p in self.params) != self.signature
+
+    def refresh_now(self, stream: int | None = None) -> bool:
+        if self.moved():
+            return False
         self._refresh(self.current_stream() if stream is None else stream)
         self.versions = tuple(p._version for p in self.params)
+        return True
 
     def refresh_if_changed(self, stream: int | None = None) -> bool:
         versions = tuple(p._version for p in self.params)
-        if versions == self.versions:
+        if versions == self.versions or self.moved():
             return False
         self._refresh(self.current_stream() if stream is None else stream)
         self.versions = versions

@@ -8,9 +8,13 @@ so each (row, KV head) prefix is one contiguous segment that the attention kerne
 with full-width coalesced loads.
 
 The pool must live on a ROCm device; the methods raise on CPU tensors (there is no CPU
-path).  Kernels skip out-of-range rows and positions instead of faulting; set
-``CARDGYM_HIP_CHECK=1`` to have every write validate its indices on the device and raise
-``IndexError`` (this reads a flag back, so it synchronises).
+path).  Kernels skip out-of-range rows and positions instead of faulting.  The trunk step
+records what it skipped in the pool's device ``status`` words (a row outside the pool, a
+negative position, a readout offset outside its sequence) without reading anything back;
+``check()`` reads them (one small copy, which waits for the stream), raises ``IndexError``
+naming what was wrong, and clears them -- a collector can call it right after it copies a
+wave's outputs to the host.  Set ``CARDGYM_HIP_CHECK=1`` to check after every eager step and
+to have every write validate its indices on the device (both synchronise).
 """
 
 from __future__ import annotations
@@ -58,8 +62,15 @@ def index_tensor(values, device: torch.device) -> torch.Tensor:
     return tensor.to(device, non_blocking=True).contiguous()
 
 
-def _check_enabled() -> bool:
+def check_enabled() -> bool:
     return os.environ.get("CARDGYM_HIP_CHECK", "0") not in ("", "0")
+
+
+STATUS_MESSAGES = (
+    "cache row outside [0, capacity)",
+    "negative cache position",
+    "readout offset outside its sequence",
+)
 
 
 class KVCache:
@@ -104,6 +115,25 @@ class KVCache:
             self.k = [torch.zeros((capacity, *self._row_shape), device=self.device, dtype=dtype) for _ in range(n_layers)]
             self.v = [torch.zeros_like(k) for k in self.k]
         self._layers: list[nat.KVLayer] | None = None
+        # Set by trunk steps over this pool (cg_ragged.status): see check().
+        self.status = torch.zeros(3, device=self.device, dtype=torch.int32)
+
+    def step_errors(self, clear: bool = True) -> list[str]:
+        """What the trunk steps over this pool skipped since the last clear (reads the
+        device status words: waits for the current stream)."""
+
+        words = self.status.tolist()
+        if clear and any(words):
+            self.status.zero_()
+        return [message for message, word in zip(STATUS_MESSAGES, words) if word]
+
+    def check(self) -> None:
+        """Raises ``IndexError`` if a trunk step over this pool met an index the reference's
+        indexing would refuse (cardgym/nn/kv_cache.py:98-105, trunk.py:429); clears the words."""
+
+        errors = self.step_errors()
+        if errors:
+            raise IndexError("trunk step: " + "; ".join(errors))
 
     @staticmethod
     def bytes_per_row(n_layers: int, kv_heads: int, head_dim: int, max_len: int, dtype: torch.dtype) -> int:
@@ -146,7 +176,7 @@ class KVCache:
         return stream_handle(self.device)
 
     def _validate(self, layer: int, rows: torch.Tensor | None, positions: torch.Tensor | None) -> None:
-        if not _check_enabled():
+        if not check_enabled():
             return
         flag = torch.zeros(1, dtype=torch.int32, device=self.device)
         nat.call(

@@ -173,13 +173,14 @@ def _(x, weight, lookup, scale, compute):
 # -- the trunk step ----------------------------------------------------------------------
 
 
-@torch.library.custom_op("cardgym_hip::trunk_step", mutates_args=("k", "v"))
+@torch.library.custom_op("cardgym_hip::trunk_step", mutates_args=("k", "v", "status"))
 def trunk_step(
     x: Tensor,
     ple: Optional[Tensor],
     values: Optional[Tensor],
     k: List[Tensor],
     v: List[Tensor],
+    status: Optional[Tensor],
     positions: Tensor,
     seq_start: Optional[Tensor],
     rows: Optional[Tensor],
@@ -194,7 +195,9 @@ def trunk_step(
     ``k`` / ``v`` (``KVCache.pools()``, mutated) and returns the final-norm hidden rows, fp32 [n_seqs, d] at
     the readout tokens (or [n_tokens, d] without ``readout``).  ``x`` [n_tokens, d],
     ``ple`` [n_tokens, n_layers * per_layer_dim], ``values`` [n_tokens, value_width]
-    (fp32, contiguous); index tensors int64 as ``cg_ragged_step`` takes them."""
+    (fp32, contiguous); index tensors int64 as ``cg_ragged`` takes them.  ``status`` (int32
+    [3] on the device, ``KVCache.status``) gets a 1 in word 0 / 1 / 2 when some row is outside
+    the pool, some position is negative, some readout offset is outside its sequence."""
 
     module = lookup(trunk)
     device = x.device
@@ -203,8 +206,10 @@ def trunk_step(
     hidden = torch.empty((n_seqs if readout is not None else n_tokens, d), device=device, dtype=torch.float32)
     size = nat.lib().cg_trunk_workspace_size(native.handle, n_tokens, n_seqs)
     workspace = torch.empty(max(size, 1), device=device, dtype=torch.uint8)
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 3 or not status.is_contiguous()):
+        raise ValueError("status must be a contiguous int32 tensor of 3 words")
     step = nat.Ragged(
-        n_seqs, n_tokens, T, span, _ptr(seq_start), positions.data_ptr(), _ptr(rows), _ptr(readout),
+        n_seqs, n_tokens, T, span, _ptr(seq_start), positions.data_ptr(), _ptr(rows), _ptr(readout), _ptr(status),
     )
     nat.call(
         "cg_trunk_forward", native.handle, kv_layers(k, v), x.data_ptr(), _ptr(ple), _ptr(values), ctypes.byref(step),
@@ -214,7 +219,7 @@ def trunk_step(
 
 
 @trunk_step.register_fake
-def _(x, ple, values, k, v, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
+def _(x, ple, values, k, v, status, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
     return x.new_empty((n_seqs if readout is not None else x.shape[0], x.shape[1]))
 
 

@@ -28,7 +28,7 @@ from torch import nn
 from .. import _native as nat
 from . import ops
 from .derived import DerivedCopies, HandleCache, after_load_hook
-from .kv_cache import KVCache, index_tensor, require_device, stream_handle
+from .kv_cache import KVCache, check_enabled, index_tensor, require_device, stream_handle
 
 ValueEmbeddingMode = Literal["off", "alternating", "all"]
 
@@ -146,10 +146,21 @@ def _param(tensor: torch.Tensor) -> torch.Tensor:
 
 
 def compute_dtype_code(device: torch.device) -> int:
-    """bf16 projections under bf16 autocast on the device, fp32 otherwise."""
+    """bf16 projections under bf16 autocast on the device, fp32 without autocast.
 
-    if torch.is_autocast_enabled(device.type) and torch.get_autocast_dtype(device.type) == torch.bfloat16:
-        return nat.CG_BF16
+    fp16 autocast (the reference's ``precision = "fp16"``) is refused rather than run in
+    another precision: the kernels have no fp16 projection path.  An fp16 KV pool is
+    supported under either precision."""
+
+    if torch.is_autocast_enabled(device.type):
+        dtype = torch.get_autocast_dtype(device.type)
+        if dtype == torch.bfloat16:
+            return nat.CG_BF16
+        if dtype == torch.float16:
+            raise RuntimeError(
+                "fp16 autocast is not supported by the HIP trunk: run under bf16 autocast or fp32 "
+                "(an fp16 KV cache works with either)"
+            )
     return nat.CG_F32
 
 
@@ -368,10 +379,13 @@ class Trunk(ops.Registered, nn.Module):
         # One opaque op per step (torch.ops.cardgym_hip.trunk_step): eager, compiled and
         # captured calls all launch the same cg_trunk_forward.
         k_pools, v_pools = cache.pools()
-        return ops.trunk_step(
-            flat, ple_flat, values_flat, k_pools, v_pools, positions, seq_start, rows, readout, self.op_key,
-            compute_dtype_code(device), n_seqs, T, 0 if span is None else int(span),
+        hidden = ops.trunk_step(
+            flat, ple_flat, values_flat, k_pools, v_pools, cache.status, positions, seq_start, rows, readout,
+            self.op_key, compute_dtype_code(device), n_seqs, T, 0 if span is None else int(span),
         )
+        if check_enabled() and not torch.compiler.is_compiling() and not torch.cuda.is_current_stream_capturing():
+            cache.check()
+        return hidden
 
     def forward_ragged(
         self,

@@ -34,10 +34,11 @@ VOCAB = 512
 class SyntheticModel(ops.Registered, SequenceModel):
     """Embedding -> trunk -> (policy logits, seat values).
 
-    Besides :meth:`heads` it answers the actor interface the reference's decode graphs
-    call (cardgym/games/base.py:25-58: ``policy_heads``, ``graphable_heads``,
-    ``pop_context``, ``policy_logits``, ``player_values``), so
-    ``card_playing_gym_amd.rl.graphs.DecodeGraphs`` runs it as it runs a game's actor."""
+    Besides :meth:`heads` it answers the actor interface a rollout collector calls at each
+    wave's readout (cardgym/games/base.py:25-58: ``policy_heads``, ``graphable_heads``,
+    ``pop_context``, ``policy_logits``, ``player_values``), so the reference's own decode
+    graphs run it as they run a game's actor; :meth:`readout_heads` gives
+    ``card_playing_gym_amd.rl.wave_graphs.WaveGraphs`` every head in one launch."""
 
     graphable_heads = True
     policy_heads = ("policy",)
@@ -97,6 +98,18 @@ class SyntheticModel(ops.Registered, SequenceModel):
 
     def player_values(self, hidden: torch.Tensor) -> torch.Tensor:
         return self.heads(hidden)[1]
+
+    def readout_heads(self, hidden: torch.Tensor, heads: tuple[str, ...], values: bool) -> dict[str, torch.Tensor]:
+        """``heads``' logits (and the seat values) from one fused heads launch."""
+
+        for head in heads:
+            if head not in self.policy_heads:
+                raise ValueError(f"Unknown policy head {head!r}.")
+        logits, seat_values = self.heads(hidden)
+        out = {head: logits for head in heads}
+        if values:
+            out["values"] = seat_values
+        return out
 
     def _run_heads(self, h: torch.Tensor, compute: int) -> tuple[torch.Tensor, torch.Tensor]:
         """The launches behind ``torch.ops.cardgym_hip.synthetic_heads``."""

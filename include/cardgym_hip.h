@@ -254,6 +254,14 @@ typedef struct cg_ragged {
   const int64_t *positions;  /* int64 [n_seqs] */
   const int64_t *rows;       /* int64 [n_seqs] or NULL */
   const int64_t *readout;    /* int64 [n_seqs] or NULL */
+  int32_t *status;           /* int32 [3] device words or NULL: the step sets status[0] = 1
+                                when some rows[b] is outside [0, capacity), status[1] = 1 when
+                                some positions[b] is negative (those tokens are neither written
+                                nor attended: where the reference's index_put would raise,
+                                kv_cache.py:98-105), status[2] = 1 when some readout[b] is
+                                outside [-len_b, len_b) of its sequence (a zero hidden row;
+                                negative offsets count from the sequence's end, as torch
+                                indexing does, trunk.py:429).  Never cleared by the step. */
 } cg_ragged;
 
 /* Workspace bytes cg_trunk_forward needs for n_tokens tokens and n_seqs sequences. */

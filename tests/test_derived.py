@@ -94,10 +94,22 @@ def test_moved_parameters_retire_the_handle_without_destroying_it():
     second = owner.native()
     assert second is not first and first in owner._handles.retired
     assert not [e for e in log if e[0] == "close"]
+    # The storage `first` points into outlives the swap of param.data: a graph captured
+    # before the move still reads it.
+    assert [t.data_ptr() for t in first._storage] == list(first.signature)
+    assert first.moved() and not second.moved()
+    # The moved parameters are no longer what `first` points into: updates to them never
+    # refresh it (no eager call, no optimiser step, no refresh_all).
+    before = refreshes(log)
     with torch.no_grad():
-        first.params[0].add_(1)  # a graph captured before the move still reads `first`
+        first.params[0].add_(1)
     derived.refresh_all()
-    assert ("refresh", id(first)) in log
+    first.params[0].grad = torch.ones_like(first.params[0])
+    torch.optim.SGD([first.params[0]], lr=0.1).step()
+    assert ("refresh", id(first)) not in log
+    assert not first.refresh_now() and not first.refresh_if_changed()
+    # `second` owns the moved parameters: refresh_all after the in-place edit, then the step.
+    assert log[-2:] == [("refresh", id(second))] * 2 and refreshes(log) == before + 2
     owner._handles.close()
     assert {("close", id(first)), ("close", id(second))} <= set(log)
 

@@ -1,13 +1,17 @@
-"""The reference's rollout caller on the custom ops: ``DecodeGraphs``
-(card_playing_gym_amd/rl/graphs.py, the interface of cardgym/rl/graphs.py:63-151) compiles
-the wave body with ``torch.compile(dynamic=True)``, warms it up on a side stream, captures
-it into a HIP graph and replays it.  Checked against the same waves run eagerly (no
-compile, no graph) on a twin pool.
+"""Decode waves as HIP graphs, two ways, checked against the same waves run eagerly (no
+compile, no graph) on a twin pool:
 
-Bar: bit-equal outputs and pools -- the compiled, captured and eager paths launch the same
-kernels on the same inputs.  Also: the body compiles as one graph (``fullgraph=True``), the
-compiled body appends to the pool in place (functionalisation makes no copy of it), replays
-follow in-place weight updates, and ``torch.library.opcheck`` passes on each op.
+* ``WaveGraphs`` (card_playing_gym_amd/rl/wave_graphs.py): eager first wave per shape,
+  capture without a second append, pinned staging reused per shape, least-recently-used
+  shapes released;
+* the reference's caller pattern (tests/caller.py: ``torch.compile(dynamic=True,
+  fullgraph=True)`` of the wave body over the ``cardgym_hip`` ops, side-stream warm-up,
+  capture, replay), which the reference's collectors run unchanged over this model.
+
+Bar: bit-equal outputs and pools -- every path launches the same kernels on the same
+inputs.  Also: the compiled body appends to the pool in place (functionalisation makes no
+copy of it), replays follow weight updates (``load_state_dict``), and
+``torch.library.opcheck`` passes on each op.
 """
 
 from __future__ import annotations
@@ -17,8 +21,9 @@ import pytest
 import torch
 
 from card_playing_gym_amd.nn import ops
-from card_playing_gym_amd.rl.graphs import DecodeGraphs, graphs_enabled
+from card_playing_gym_amd.rl.wave_graphs import DecodeGraphs, WaveGraphs
 from card_playing_gym_amd.synthetic import build_model, trunk_config
+from tests.caller import CapturedWave, compiled, random_wave, to_device, wave_body
 
 pytestmark = pytest.mark.gpu
 
@@ -37,19 +42,10 @@ def setup(device, layers: int, capacity: int, max_len: int, seed: int = 3):
     return model, cache, twin
 
 
-def random_wave(rng, capacity: int, rows: int, run: int, max_pos: int):
-    cache_rows = rng.permutation(capacity)[:rows]
-    positions = rng.integers(0, max_pos, size=rows)
-    tokens = rng.integers(0, 512, size=(rows, run, 1))
-    offsets = rng.integers(0, run, size=rows)
-    return tokens, positions, offsets, cache_rows
-
-
 def eager_wave(model, cache, tokens, positions, offsets, cache_rows, span):
-    dev = cache.device
-    up = lambda a: torch.from_numpy(np.asarray(a, dtype=np.int64)).to(dev)  # noqa: E731
+    tokens, positions, offsets, cache_rows = to_device(cache.device, tokens, positions, offsets, cache_rows)
     with torch.autocast("cuda", dtype=torch.bfloat16, cache_enabled=False):
-        hidden = model.forward_ragged(up(tokens), up(positions), cache, up(offsets), span=span, rows=up(cache_rows))
+        hidden = model.forward_ragged(tokens, positions, cache, offsets, span=span, rows=cache_rows)
         logits, values = model.heads(hidden)
     return torch.cat([logits, values], dim=-1)
 
@@ -58,13 +54,15 @@ def pools_equal(a, b) -> bool:
     return all(torch.equal(x, y) for x, y in zip(a.k + a.v, b.k + b.v))
 
 
-def test_decode_graphs_match_eager(device):
+def test_wave_graphs_match_eager(device):
     capacity, max_len = 96, 128
     model, cache, twin = setup(device, 4, capacity, max_len)
-    assert graphs_enabled(model, device)
-    graphs = DecodeGraphs(model, cache, precision="bf16", values=True)
+    assert DecodeGraphs is WaveGraphs
+    graphs = WaveGraphs(model, cache, precision="bf16", values=True, max_graphs=2)
     rng = np.random.default_rng(7)
-    shapes = [(64, 1), (64, 1), (32, 3), (64, 1), (32, 3), (17, 2), (17, 2)]
+    # (rows, run): repeats replay; a third shape releases the least recently used one.
+    shapes = [(64, 1), (64, 1), (32, 3), (64, 1), (32, 3), (17, 2), (17, 2), (64, 1), (32, 3)]
+    held = []
     with torch.no_grad():
         for index, (rows, run) in enumerate(shapes):
             wave = random_wave(rng, capacity, rows, run, 100)
@@ -74,18 +72,49 @@ def test_decode_graphs_match_eager(device):
             torch.cuda.synchronize()
             assert torch.equal(got, want), f"wave {index}"
             assert pools_equal(cache, twin), f"wave {index}"
-        assert len(graphs) == 3
+            held.append(sorted(k[:2] for k in graphs._shapes))
+        assert held[5] == [(17, 2), (32, 3)] and held[7] == [(17, 2), (64, 1)]
+        assert len(graphs) == 2
         assert graphs.columns == {"policy": slice(0, 512), "values": slice(512, 514)}
         # New weights in place (as a trainer update lands): the captured graphs follow.
         fresh = build_model(trunk_config(4), seed=11, device=device)
         model.load_state_dict(fresh.state_dict())
-        wave = random_wave(rng, capacity, 64, 1, 100)
-        got = graphs.run(*wave, span=max_len).clone()
-        want = eager_wave(model, twin, *wave, max_len)
-        torch.cuda.synchronize()
-        assert torch.equal(got, want)
-        assert pools_equal(cache, twin)
-        assert len(graphs) == 3
+        for rows, run in [(64, 1), (32, 3)]:
+            wave = random_wave(rng, capacity, rows, run, 100)
+            got = graphs.run(*wave, span=max_len).clone()
+            want = eager_wave(model, twin, *wave, max_len)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want)
+            assert pools_equal(cache, twin)
+        graphs.clear()
+        assert len(graphs) == 0
+
+
+def test_reference_caller_pattern(device):
+    """Compiled body, side-stream warm-up, capture, replays with new inputs, replay after
+    ``load_state_dict``: bit-equal to eager waves."""
+
+    capacity, max_len = 96, 128
+    model, cache, twin = setup(device, 4, capacity, max_len, seed=4)
+    body = compiled(wave_body(model, cache, torch.bfloat16))
+    rng = np.random.default_rng(8)
+    rows, run = 48, 2
+    with torch.no_grad():
+        first = random_wave(rng, capacity, rows, run, 100)
+        print("capture", flush=True)
+        captured = CapturedWave(body, *to_device(device, *first), max_len)
+        eager_wave(model, twin, *first, max_len)  # the warm-up's append
+        for index in range(4):
+            if index == 3:
+                fresh = build_model(trunk_config(4), seed=12, device=device)
+                model.load_state_dict(fresh.state_dict())
+            wave = first if index == 0 else random_wave(rng, capacity, rows, run, 100)
+            print(f"replay {index}", flush=True)
+            got = captured.replay(*to_device(device, *wave)).clone()
+            want = eager_wave(model, twin, *wave, max_len)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"replay {index}"
+            assert pools_equal(cache, twin), f"replay {index}"
 
 
 def test_wave_compiles_as_one_graph_and_appends_in_place(device):
@@ -96,22 +125,20 @@ def test_wave_compiles_as_one_graph_and_appends_in_place(device):
     capacity, max_len = 256, 512
     model, cache, twin = setup(device, 4, capacity, max_len, seed=5)
     pool_bytes = sum(t.numel() * t.element_size() for t in cache.k + cache.v)
-    graphs = DecodeGraphs(model, cache, precision="bf16", values=True)
-    body = torch.compile(graphs._outputs, dynamic=True, fullgraph=True)
+    body = compiled(wave_body(model, cache, torch.bfloat16))
     rng = np.random.default_rng(9)
     with torch.no_grad():
         for index, (rows, run) in enumerate([(128, 1), (96, 2), (128, 1)]):
-            tokens, positions, offsets, cache_rows = random_wave(rng, capacity, rows, run, 400)
-            packed = np.concatenate([a.reshape(-1) for a in (tokens, positions, offsets, cache_rows)]).astype(np.int64)
-            inputs = torch.from_numpy(packed).to(device)
+            wave = random_wave(rng, capacity, rows, run, 400)
+            inputs = to_device(device, *wave)
             print(f"compiled call {index}: rows {rows} run {run}", flush=True)
             torch.cuda.synchronize()
             torch.cuda.reset_peak_memory_stats(device)
             base = torch.cuda.memory_allocated(device)
-            out = torch.cat(body(inputs, rows, run, 1, max_len), dim=-1)
+            out = body(*inputs, max_len)
             torch.cuda.synchronize()
             extra = torch.cuda.max_memory_allocated(device) - base
-            want = eager_wave(model, twin, tokens, positions, offsets, cache_rows, max_len)
+            want = eager_wave(model, twin, *wave, max_len)
             torch.cuda.synchronize()
             assert torch.equal(out, want), f"call {index}"
             assert pools_equal(cache, twin), f"call {index}"
@@ -134,8 +161,8 @@ def test_opcheck(device):
     with torch.no_grad():
         torch.library.opcheck(
             torch.ops.cardgym_hip.trunk_step.default,
-            (x, None, None, k_pools, v_pools, positions, None, cache_rows, readout, model.trunk.op_key, 1, rows, 1,
-             max_len),
+            (x, None, None, k_pools, v_pools, cache.status, positions, None, cache_rows, readout, model.trunk.op_key, 1,
+             rows, 1, max_len),
         )
         hidden = torch.randn(rows, 256, device=device)
         for compute in (0, 1):

@@ -29,8 +29,8 @@ def test_ops_are_registered():
         assert hasattr(torch.ops.cardgym_hip, name), name
     schema = str(torch.ops.cardgym_hip.trunk_step.default._schema)
     # The pools are declared mutated (so functionalisation orders them), nothing else is.
-    assert "Tensor(a3!)[] k" in schema and "Tensor(a4!)[] v" in schema, schema
-    assert schema.count("!") == 2, schema
+    assert "Tensor(a3!)[] k" in schema and "Tensor(a4!)[] v" in schema and "Tensor(a5!)? status" in schema, schema
+    assert schema.count("!") == 3, schema
 
 
 @pytest.mark.parametrize("chunks", [False, True])
@@ -87,7 +87,7 @@ def test_keys_follow_copies_and_die_with_modules():
 
 @pytest.mark.parametrize("stacked", [True, False])
 def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
-    """Inductor (CPU codegen here) compiles the decode body of DecodeGraphs with dynamic
+    """Inductor (CPU codegen here) compiles the reference caller's decode body (tests/caller.py) with dynamic
     shapes and ``fullgraph=True``; the trunk-step op must receive the pool's own storage
     tensors -- no functional clone around the call (which, over per-layer views of one
     stacked tensor, read past the pool's end) -- and its appends must land in the pool.
@@ -95,7 +95,7 @@ def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
 
     import card_playing_gym_amd.nn.trunk as trunk_module
     import card_playing_gym_amd.synthetic as synthetic_module
-    from card_playing_gym_amd.rl import graphs as graphs_module
+    from tests.caller import wave_body
 
     for module in (trunk_module, synthetic_module):
         monkeypatch.setattr(module, "require_device", lambda *tensors: None)
@@ -109,7 +109,7 @@ def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
     storage = [t.data_ptr() for t in cache.pools()[0]]
     seen = []
 
-    def trunk_cpu(x, ple, values, k, v, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
+    def trunk_cpu(x, ple, values, k, v, status, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
         seen.append([t.data_ptr() for t in k])
         layers = list(k[0].unbind(0)) if k[0].dim() == 5 else list(k)
         for b in range(int(n_seqs)):
@@ -118,18 +118,13 @@ def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
                     layer[int(rows[b]), :, min(int(positions[b]) + t, layer.shape[2] - 1)] = 1.0
         return x.new_zeros((int(n_seqs), x.shape[1]))
 
-    class Body(graphs_module.DecodeGraphs):
-        def __init__(self):  # the body alone: no graph pool, no capture
-            self.model, self.cache, self.precision, self.values = model, cache, "fp32", True
-            self.heads = tuple(model.policy_heads)
-
     torch._dynamo.reset()
     with torch.library._scoped_library("cardgym_hip", "IMPL") as lib:
         lib.impl("trunk_step", trunk_cpu, "CPU")
         lib.impl("embed_rmsnorm", lambda table, ids, w, eps: table.new_zeros((ids.numel(), table.shape[1])), "CPU")
         lib.impl("synthetic_heads", lambda h, m, c, p, n: (h.new_zeros((h.shape[0], p)), h.new_zeros((h.shape[0], n))),
                  "CPU")
-        body = torch.compile(Body()._outputs, dynamic=True, fullgraph=True)
+        body = torch.compile(wave_body(model, cache, None), dynamic=True, fullgraph=True)
         rng = np.random.default_rng(3)
         written = 0
         with torch.no_grad():
@@ -138,9 +133,9 @@ def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
                 positions = rng.integers(0, 50, size=rows)
                 tokens = rng.integers(0, 512, size=(rows, run, 1))
                 offsets = rng.integers(0, run, size=rows)
-                packed = np.concatenate([a.reshape(-1) for a in (tokens, positions, offsets, cache_rows)])
-                out = body(torch.from_numpy(packed.astype(np.int64)), rows, run, 1, 64)
-                assert [tuple(o.shape) for o in out] == [(rows, model.vocab), (rows, 2)]
+                out = body(*[torch.from_numpy(np.asarray(a, dtype=np.int64)) for a in
+                             (tokens, positions, offsets, cache_rows)], 64)
+                assert tuple(out.shape) == (rows, model.vocab + 2)
                 assert seen[-1] == storage
                 written = max(written, int(sum(t.float().sum().item() for t in cache.k)))
     torch._dynamo.reset()
