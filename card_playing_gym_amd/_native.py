@@ -206,6 +206,7 @@ _SIGNATURES = {
     "cg_trunk_forward_static": (
         c_int32, [c_void_p, P(KVLayer), c_void_p, c_void_p, c_void_p, P(Ragged), c_void_p, c_void_p],
     ),
+    "cg_gelu_bf16": (c_int32, [c_void_p, c_void_p, c_int64, c_void_p]),
     "cg_rmsnorm": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_int32, c_void_p]),
     "cg_embed_rmsnorm": (
         c_int32,

@@ -226,6 +226,20 @@ __device__ __forceinline__ float gelu_fast(float x) {
   return x * (0.5f + __builtin_copysignf(h, x));
 }
 
+// GELU of four bf16 values (packed two per word, low half first) -> four bf16 values: the
+// MLP's GELU under autocast, whose input is the bf16 output of mlp[0] (trunk.py:135).
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2_t;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_t;
+__device__ __forceinline__ u32x2_t gelu_bf16x4(u32x2_t x) {
+  f32x4 y;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    y[2 * r] = gelu_fast(__uint_as_float(x[r] << 16));
+    y[2 * r + 1] = gelu_fast(__uint_as_float(x[r] & 0xffff0000u));
+  }
+  return __builtin_bit_cast(u32x2_t, __builtin_convertvector(y, bf16x4_t));
+}
+
 
 }  // namespace
 }  // namespace cg

@@ -62,6 +62,9 @@ void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_
 // output columns stays inside one head); bf16 projections.
 bool tail_supported(int d, int d_ff, int n_qkv, int head_dim);
 
+// The fused layer kernel's GELU (bf16 in, bf16 out) over n values (a multiple of 4).
+void launch_gelu_apply(const void *x, void *y, int64_t n, hipStream_t stream);
+
 void launch_tail(const TailArgs &a, hipStream_t stream);
 
 }  // namespace cg

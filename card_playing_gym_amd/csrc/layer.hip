@@ -72,6 +72,29 @@ void launch_pack_fragments(const float *src, void *dst, int N, int K, hipStream_
   CG_LAUNCHED();
 }
 
+namespace {
+// The fused kernel's GELU (gelu_bf16x4) over an array of bf16 values, four per thread.
+__global__ __launch_bounds__(256) void gelu_apply_kernel(const uint2 *__restrict__ x, uint2 *__restrict__ y, int64_t n4) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += int64_t(gridDim.x) * blockDim.x) {
+    const uint2 v = x[i];
+    const u32x2_t g = gelu_bf16x4(u32x2_t{v.x, v.y});
+    y[i] = uint2{g[0], g[1]};
+  }
+}
+}  // namespace
+
+void launch_gelu_apply(const void *x, void *y, int64_t n, hipStream_t s) {
+  CG_REQUIRE(n % 4 == 0, CG_ERR_UNSUPPORTED, "GELU: a multiple of 4 values");
+  CG_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7) == 0, CG_ERR_UNSUPPORTED,
+             "GELU: 8-byte aligned arrays");
+  const int64_t n4 = n / 4;
+  if (n4 == 0) return;
+  int64_t blocks = (n4 + 255) / 256;
+  if (blocks > 1024) blocks = 1024;
+  gelu_apply_kernel<<<unsigned(blocks), 256, 0, s>>>(static_cast<const uint2 *>(x), static_cast<uint2 *>(y), n4);
+  CG_LAUNCHED();
+}
+
 bool tail_supported(int d, int d_ff, int n_qkv, int head_dim) {
   return d > 0 && d <= PANEL && d % 16 == 0 && d_ff > 0 && d_ff % 16 == 0 && d_ff <= 4 * PANEL &&
          n_qkv > 0 && n_qkv % 16 == 0 && n_qkv <= 3 * PANEL && head_dim > 0 && head_dim % 4 == 0;

@@ -534,16 +534,14 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
       unsigned char *hb = hbuf[p.ups_first ? c : (c % HB)];
       // One GELU buffer: every wave has finished down chunk c - 1's reads of it.
       if (HB == 1 && c > 0) lds_barrier();
+      // GELU of the bf16 Linear output (rounded to nearest even first, as autocast's Linear
+      // returns it), rounded to bf16 again for the down projection's panel.
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int col = cw + 16 * j + 4 * lg;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          f32x4 g;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) g[r] = gelu_fast(acc[i][j][r]);
-          *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + col * 2) = pack_bf16x4(g);
-        }
+        for (int i = 0; i < FM; ++i)
+          *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + col * 2) = gelu_bf16x4(pack_bf16x4(acc[i][j]));
       }
       // Down chunk c reads every wave's columns of GELU chunk c.
       if (!p.ups_first || c == p.nc - 1) lds_barrier();

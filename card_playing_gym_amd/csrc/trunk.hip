@@ -715,6 +715,15 @@ int cg_trunk_forward_static(const cg_trunk *trunk, const cg_kv_layer *cache, con
   });
 }
 
+int cg_gelu_bf16(const void *x, void *y, int64_t n, void *stream) {
+  return guarded([&] {
+    CG_REQUIRE(n >= 0, CG_ERR_INVALID, "n must be non-negative");
+    if (n == 0) return;
+    CG_REQUIRE(x && y, CG_ERR_INVALID, "x and y are required");
+    launch_gelu_apply(x, y, n, as_stream(stream));
+  });
+}
+
 int cg_rmsnorm(const void *x, int32_t x_dtype, const float *gain, float eps, float *y, int32_t n, int32_t d,
                void *stream) {
   return guarded([&] {

@@ -295,6 +295,13 @@ int cg_trunk_forward_static(const cg_trunk *trunk, const cg_kv_layer *cache, con
                             const float *ple, const float *values, const cg_ragged *step, float *hidden,
                             void *stream);
 
+/* GELU of the fused bf16 layer kernel (the MLP's nn.GELU, cardgym/nn/trunk.py:135, under
+ * autocast: the bf16 output of mlp[0] in, bf16 out), exposed so that callers and tests can
+ * check it: n bf16 values (n a multiple of 4, 8-byte aligned arrays) through the kernel's
+ * GELU, x * Phi(x) with Phi from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), rounded
+ * to bf16 (nearest even). */
+int cg_gelu_bf16(const void *x, void *y, int64_t n, void *stream);
+
 /* ---- conditioning, embedding and heads ------------------------------------------ */
 
 /* RMSNorm (cardgym/nn/trunk.py:104-115): y = rms_norm(x, eps).to(x.dtype) * gain, rows of
