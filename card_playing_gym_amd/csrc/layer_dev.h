@@ -32,13 +32,19 @@ constexpr int ring_of() { return BM > 48 ? 1 : TAIL_RING; }
 
 enum StageKind { ST_OUT, ST_UP, ST_DOWN, ST_QKV };
 
-// MLP stage order.  Blocks of up to 32 rows run every up chunk first (each GELU output to
+// MLP stage order.  Blocks of up to 48 rows run every up chunk first (each GELU output to
 // its own LDS buffer), one barrier, then every down chunk: one block-wide wait for the MLP
-// instead of one per chunk.  48- and 64-row blocks interleave up c, down c through two
-// buffers (four would not fit in LDS beside the panel); a taller block would use one, with
-// a barrier before each GELU chunk overwrites the one the last down chunk read.
+// instead of one per chunk; from 32 rows each chunk's GELU runs inside the next up chunk's
+// k-steps, beside its MFMAs.  64-row blocks interleave up c, down c through two buffers (four would
+// not fit in LDS beside the panel); a taller block would use one, with a barrier before each
+// GELU chunk overwrites the one the last down chunk read.
 template <int BM>
-constexpr bool ups_first() { return BM <= 32; }
+constexpr bool ups_first() { return BM <= 48; }
+// The previous up chunk's GELU inside the next one's k-steps: measured faster at 32 rows
+// (config 4: 1.787 -> 1.731 ms per step) and 48 (config 5: 2.805 -> 2.788), slower at 16
+// (config 3: 1.140 -> 1.168), where a stage has two MFMAs per k-step to hide work behind.
+template <int BM>
+constexpr bool gelu_pipelined() { return ups_first<BM>() && BM >= 32; }
 template <int BM>
 constexpr int hbufs_of() { return ups_first<BM>() ? 4 : (BM <= 64 ? 2 : 1); }
 
@@ -100,9 +106,15 @@ __device__ __forceinline__ void load_wslice(uint4 (&buf)[KS][FN], const Slice &s
 // stage_mma (fragment.h) with the operands swapped, so the result tile is transposed
 // (lane (li, lg) holds row 16 i + li, columns 4 lg .. +3 of the 16-column fragment j).
 // The weight registers are refilled with the next stage's fragments as in stage_mma.
-template <int FM>
+// `between(ks)` runs after k-step ks's MFMAs and refills are issued: independent VALU work
+// (the previous up chunk's GELU) placed there executes while the matrix core multiplies.
+struct NoWork {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+template <int FM, typename Between = NoWork>
 __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned char *lds,
-                                            uint4 (&w)[KS][FN], const Slice &next, bool refill, int lane) {
+                                            uint4 (&w)[KS][FN], const Slice &next, bool refill, int lane,
+                                            Between between = NoWork{}) {
   const int li = lane & 15, lg = lane >> 4;
   uint32_t base[FN];
 #pragma unroll
@@ -123,6 +135,7 @@ __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned
         for (int j = 0; j < FN; ++j) w[ks][j] = wload16(next.w, base[j] + 1024 * ks);
       }
       pin_refill();
+      between(ks);
     }
   } else {
     uint4 af[2][FM];
@@ -143,6 +156,7 @@ __device__ __forceinline__ void stage_mma_t(f32x4 (&acc)[FM][FN], const unsigned
         for (int j = 0; j < FN; ++j) w[ks][j] = wload16(next.w, base[j] + 1024 * ks);
       }
       pin_refill();
+      between(ks);
     }
   }
 }
@@ -449,6 +463,7 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   // chunks accumulate onto it (accd starts as x1), so it is never written to or read back
   // from memory and needs no registers of its own.
   f32x4 acc[FM][FN], accd[FM][FN];
+  f32x4 prev[FM][FN];  // the previous up chunk's accumulators, before its GELU
   zero<FM>(accd);
   {
     const int m0 = blk * BM;
@@ -530,21 +545,41 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
 #pragma unroll
         for (int i = 0; i < FM; ++i) acc[i][j] = bias;
       }
-      stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
-      unsigned char *hb = hbuf[p.ups_first ? c : (c % HB)];
-      // One GELU buffer: every wave has finished down chunk c - 1's reads of it.
-      if (HB == 1 && c > 0) lds_barrier();
       // GELU of the bf16 Linear output (rounded to nearest even first, as autocast's Linear
-      // returns it), rounded to bf16 again for the down projection's panel.
+      // returns it), rounded to bf16 again for the down projection's panel: one (row tile,
+      // column tile) group of four values per lane.
+      auto gelu_group = [&](const f32x4 (&v)[FM][FN], unsigned char *hb, int g) {
+        const int i = g / FN, j = g % FN;
+        *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + (cw + 16 * j + 4 * lg) * 2) =
+            gelu_bf16x4(pack_bf16x4(v[i][j]));
+      };
+      constexpr int G = FM * FN;
+      constexpr bool PIPE = gelu_pipelined<BM>();
+      if (PIPE && c > 0) {
+        // Up chunks run back to back: chunk c - 1's GELU is spread over chunk c's k-steps.
+        unsigned char *hp = hbuf[c - 1];
+        stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o, [&](int ks) {
 #pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int col = cw + 16 * j + 4 * lg;
+          for (int g = 0; g < G; ++g)
+            if (g * KS / G == ks) gelu_group(prev, hp, g);
+        });
+      } else {
+        stage_mma_t<FM>(acc, panel, cur, nx, refill, lane_o);
+      }
+      unsigned char *hb = hbuf[p.ups_first ? c : (c % HB)];
+      if (PIPE && c < p.nc - 1) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
-          *reinterpret_cast<u32x2 *>(hb + (16 * i + li) * ROWB + col * 2) = gelu_bf16x4(pack_bf16x4(acc[i][j]));
+#pragma unroll
+          for (int j = 0; j < FN; ++j) prev[i][j] = acc[i][j];
+      } else {
+        // One GELU buffer: every wave has finished down chunk c - 1's reads of it.
+        if (HB == 1 && c > 0) lds_barrier();
+#pragma unroll
+        for (int g = 0; g < G; ++g) gelu_group(acc, hb, g);
+        // Down chunk c reads every wave's columns of GELU chunk c.
+        if (!p.ups_first || c == p.nc - 1) lds_barrier();
       }
-      // Down chunk c reads every wave's columns of GELU chunk c.
-      if (!p.ups_first || c == p.nc - 1) lds_barrier();
     } else if (kind == ST_DOWN) {
       // ---- down chunk c (accumulates); after the last: residual (+PLE), next prologue
       const bool last = c == p.nc - 1;
