@@ -203,6 +203,11 @@ _SIGNATURES = {
         c_int32,
         [c_void_p, P(KVLayer), c_void_p, c_void_p, c_void_p, P(Ragged), c_void_p, c_void_p, c_size_t, c_void_p],
     ),
+    "cg_trunk_forward_tokens": (
+        c_int32,
+        [c_void_p, P(KVLayer), c_void_p, c_int32, c_void_p, c_void_p, c_float, c_void_p, c_void_p, P(Ragged),
+         c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
     "cg_trunk_forward_static": (
         c_int32, [c_void_p, P(KVLayer), c_void_p, c_void_p, c_void_p, P(Ragged), c_void_p, c_void_p],
     ),

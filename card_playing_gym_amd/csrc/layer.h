@@ -50,6 +50,22 @@ struct TailArgs {
   float *hidden;     // final_ln: [rows, d]
   int32_t hidden_vec;  // hidden is 16-byte aligned (rows written as float4 runs)
   const int32_t *tok_out;
+
+  // MODE 0 only.  plan != 0: the launch forms the step's plan itself from its descriptors
+  // (cg_ragged): per token its cache row, clamped write position and output row, written to
+  // plan_row / plan_pos / plan_out (the tok_* arrays of the later launches); per sequence a
+  // zero hidden row when its readout offset is outside its chunk; the status words.
+  int32_t plan;
+  const int64_t *seq_start, *positions, *rows, *readout;
+  int32_t n_seqs, T, capacity;
+  int32_t *plan_row, *plan_pos, *plan_out, *status;
+  // embed_table != NULL: the input rows are formed here from token ids, x = rms_norm(
+  // embed_table[ids]) * in_gain (eps in_eps; a row of an id outside [0, vocab) is zero).
+  const float *embed_table;
+  int32_t vocab;
+  const int64_t *ids;
+  const float *in_gain;
+  float in_eps;
 };
 
 // The fused kernel reads its four weight matrices in MFMA fragment order: W [N, K] (fp32,

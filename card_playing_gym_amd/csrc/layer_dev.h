@@ -322,6 +322,47 @@ __device__ __forceinline__ void next_prologue(const TailArgs &a, const Params &p
   }
 }
 
+// A readout offset as torch indexing reads it (trunk.py:429): negative offsets count from
+// the end of the sequence's len tokens; -1 when outside.
+__device__ __forceinline__ int64_t readout_index(int64_t o, int64_t len) {
+  if (o < 0) o += len;
+  return o >= 0 && o < len ? o : -1;
+}
+// Token i of the step: (cache row or -1, clamped write position, output row or -1), as the
+// reference writes it (trunk.py:417-420, kv_cache.py:84-105).  Rows outside the pool and
+// negative positions are neither written nor attended and set their status word.
+__device__ __forceinline__ void plan_token(const TailArgs &a, int i, int &row_out, int &pos_out, int &out_row) {
+  int b, t;
+  if (a.seq_start) {
+    int lo = 0, hi = a.n_seqs - 1;  // last b with seq_start[b] <= i
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.seq_start[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    b = lo;
+    t = int(i - a.seq_start[b]);
+  } else {
+    b = a.T == 1 ? i : i / a.T;
+    t = i - b * a.T;
+  }
+  const int64_t row = a.rows ? a.rows[b] : int64_t(b);
+  const int64_t p0 = a.positions[b];
+  int64_t pos = p0 + t;
+  if (pos > a.max_len - 1) pos = a.max_len - 1;
+  const bool row_ok = row >= 0 && row < a.capacity, pos_ok = p0 >= 0;
+  row_out = row_ok && pos_ok ? int(row) : -1;
+  pos_out = row_ok && pos_ok ? int(pos) : 0;
+  if (a.status && !row_ok) a.status[0] = 1;
+  if (a.status && !pos_ok) a.status[1] = 1;
+  if (a.readout) {
+    const int64_t len = a.seq_start ? a.seq_start[b + 1] - a.seq_start[b] : int64_t(a.T);
+    out_row = readout_index(a.readout[b], len) == t ? b : -1;
+  } else {
+    out_row = i;
+  }
+}
+
 // MODE: 0 = first block's prologue (x = x_src, LN + QKV), 1 = post + next QKV, 2 = post +
 // final norm.  NC / NQ: 256-wide chunks of d_ff / of the QKV width.  The stage sequence is
 // a compile-time constant, so the fully unrolled stage loop folds every stage's kind and
@@ -369,15 +410,45 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
   }
   // The residual rows the out-projection adds (the lane's own transposed tiles) are read
   // here too, so their latency overlaps the attention rows' instead of following it.
+  // The first block's input rows (its embedding rows, or the conditioned rows) are read here
+  // as well.
   f32x4 xr[FM][FN];
-  if (POST) {
-    const Rsrc rs = rsrc(a.x_src, xbytes);
+  bool id_ok[FM];
+  {
     const int li = lane & 15, lg = lane >> 4;
+    if (POST) {
+      const Rsrc rs = rsrc(a.x_src, xbytes);
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        xr[i][j] = bload4f(rs, (uint32_t(m0_ + 16 * i + li) * d + cw + 16 * j + 4 * lg) * 4);
+        for (int j = 0; j < FN; ++j)
+          xr[i][j] = bload4f(rs, (uint32_t(m0_ + 16 * i + li) * d + cw + 16 * j + 4 * lg) * 4);
+    } else if (a.embed_table) {
+      const Rsrc rt = rsrc(a.embed_table, uint32_t(a.vocab) * uint32_t(d) * 4);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = m0_ + 16 * i + li;
+        const int64_t id = m < a.M ? a.ids[m] : 0;
+        id_ok[i] = m < a.M && id >= 0 && id < a.vocab;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          xr[i][j] = bload4f(rt, uint32_t((id_ok[i] ? id : 0) * d + cw + 16 * j + 4 * lg) * 4);
+      }
+    } else {
+      const Rsrc rs = rsrc(a.x_src, xbytes);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const uint32_t off = (uint32_t(m0_ + 16 * i + li) * d + cw + 16 * j + 4 * lg) * 4;
+          if (a.x_src_vec) {
+            xr[i][j] = bload4f(rs, off);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xr[i][j][r] = bloadf(rs, off + 4 * r);
+          }
+        }
+    }
   }
   constexpr int NB_UP = (4 * PANEL + THREADS - 1) / THREADS;
   float v_up[NB_UP], v_vec[5];
@@ -396,9 +467,34 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
     v_vec[3] = in ? a.ln_w[tid] : 0.f;
     v_vec[4] = in ? a.ln_b[tid] : 0.f;
     const bool tin = tid < BM && m0_ + tid < a.M;
-    v_tok[0] = tin && !a.final_ln ? a.tok_row[m0_ + tid] : -1;
-    v_tok[1] = tin && !a.final_ln ? a.tok_pos[m0_ + tid] : 0;
-    v_tok[2] = tin && a.final_ln ? a.tok_out[m0_ + tid] : -1;
+    if (!POST && a.plan) {
+      // The step's plan, formed here for this block's tokens and sequences.
+      v_tok[0] = -1;
+      v_tok[1] = 0;
+      v_tok[2] = -1;
+      if (tin) {
+        const int i = m0_ + tid;
+        plan_token(a, i, v_tok[0], v_tok[1], v_tok[2]);
+        a.plan_row[i] = v_tok[0];
+        a.plan_pos[i] = v_tok[1];
+        a.plan_out[i] = v_tok[2];
+        if (a.final_ln) v_tok[0] = -1;
+      }
+      const int sq = m0_ + tid;
+      if (tid < BM && a.readout && sq < a.n_seqs) {
+        const int64_t start = a.seq_start ? a.seq_start[sq] : int64_t(sq) * a.T;
+        const int64_t stop = a.seq_start ? a.seq_start[sq + 1] : start + a.T;
+        if (readout_index(a.readout[sq], stop - start) < 0) {
+          if (a.status) a.status[2] = 1;
+          if (a.hidden)
+            for (int k = 0; k < d; ++k) a.hidden[int64_t(sq) * d + k] = 0.f;
+        }
+      }
+    } else {
+      v_tok[0] = tin && !a.final_ln ? a.tok_row[m0_ + tid] : -1;
+      v_tok[1] = tin && !a.final_ln ? a.tok_pos[m0_ + tid] : 0;
+      v_tok[2] = tin && a.final_ln ? a.tok_out[m0_ + tid] : -1;
+    }
     // QKV column runs: role and offset of columns 4 tid .. +3 (head_dim is a multiple of 4).
     const int n = 4 * tid, kvw = a.kv_heads * a.head_dim;
     if (!a.final_ln && n < a.n_qkv) {
@@ -478,25 +574,63 @@ __device__ __forceinline__ void tail_body(const TailArgs &a, int blk, unsigned c
       lds_barrier();
     } else {
       // First block's prologue: the conditioned input is the residual stream.
-      const Rsrc rs = rsrc(a.x_src, xbytes);
+      if (a.embed_table) {
+        // ... formed here: the token's embedding row (read in the prologue) through the input
+        // RMSNorm (trunk.py:104-115, rms_norm(x.float(), eps) * weight; fp32 rows, no rounding).
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i) {
+          const int m = m0 + 16 * i + li;
+          if (m < a.M && !id_ok[i] && a.status) a.status[3] = 1;
+          float sq = 0.f;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int m = m0 + 16 * i + li, c0 = cw + 16 * j + 4 * lg;
-          const uint32_t off = (uint32_t(m) * d + c0) * 4;
-          f32x4 v;
-          if (a.x_src_vec) {
-            v = bload4f(rs, off);
-          } else {
+          for (int j = 0; j < FN; ++j) {
+            f32x4 v = xr[i][j];
+            if (!(id_ok[i] && cw + 16 * j < d)) v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = bloadf(rs, off + 4 * r);
+            for (int r = 0; r < 4; ++r) sq = fmaf(v[r], v[r], sq);
+            acc[i][j] = v;
           }
-          const bool ok = m < a.M && cw + 16 * j < d;
-          if (!ok) v = f32x4{0.f, 0.f, 0.f, 0.f};
-          if (ok && a.x != a.x_src) st_nt(a.x + int64_t(m) * d + c0, v);
-          acc[i][j] = v;
+          sq = lane_groups_sum(sq);
+          if (lg == 0) red[wave * BM + 16 * i + li] = sq;
         }
+        lds_barrier();
+        float *rms = red + 2 * WAVES * BM;
+        if (tid < BM) {
+          float total = 0.f;
+#pragma unroll
+          for (int w = 0; w < WAVES; ++w) total += red[w * BM + tid];
+          rms[tid] = rsqrtf(total / float(d) + a.in_eps);
+        }
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int m = m0 + 16 * i + li;
+          const float r = rms[16 * i + li];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int c0 = cw + 16 * j + 4 * lg;
+            if (cw + 16 * j >= d) continue;
+            const f32x4 g = *reinterpret_cast<const f32x4 *>(a.in_gain + c0);
+            f32x4 x;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[q] = acc[i][j][q] * r * g[q];
+            acc[i][j] = x;
+            if (m < a.M) st_nt(a.x + int64_t(m) * d + c0, x);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const int m = m0 + 16 * i + li, c0 = cw + 16 * j + 4 * lg;
+            f32x4 v = xr[i][j];
+            const bool ok = m < a.M && cw + 16 * j < d;
+            if (!ok) v = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (ok && a.x != a.x_src) st_nt(a.x + int64_t(m) * d + c0, v);
+            acc[i][j] = v;
+          }
+      }
       next_prologue<BM>(a, prm, acc, panel, red, cw, wave, li, lg);
     }
   }

@@ -229,6 +229,20 @@ unsigned rows_grid(int32_t n, int waves_per_block) {
   return unsigned((n + waves_per_block - 1) / waves_per_block);
 }
 
+// RMSNorm(table[ids]) * gain -> y [n, d] fp32: four rows per wave for the usual widths
+// (16-byte aligned rows), one row per wave otherwise.  flag (may be NULL) = 1 on a bad id.
+void launch_embed_rmsnorm(const float *table, int32_t vocab, const int64_t *ids, const float *gain, float eps,
+                          float *y, int32_t n, int32_t d, int32_t *flag, hipStream_t s) {
+  const bool aligned = ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(gain) |
+                         reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  const unsigned grid4 = unsigned((int64_t(n) + 15) / 16);  // four waves of four rows
+  if (aligned && d == 256) embed_rmsnorm_rows4_kernel<4><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
+  else if (aligned && d == 128) embed_rmsnorm_rows4_kernel<2><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
+  else if (aligned && d == 64) embed_rmsnorm_rows4_kernel<1><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
+  else rmsnorm_rows_kernel<float><<<rows_grid(n, 4), 256, 0, s>>>(nullptr, table, vocab, ids, gain, eps, y, n, d, flag);
+  CG_LAUNCHED();
+}
+
 void convert_weights(cg_trunk &t, hipStream_t s) {
   if (t.compute != CG_BF16) return;
   const int d = t.cfg.d_model, hd = t.cfg.n_heads * t.head_dim, ff = t.cfg.d_ff;
@@ -369,11 +383,23 @@ namespace cg {
 namespace {
 
 // The step on a given workspace: cg_trunk_forward and cg_trunk_forward_static.
+// Token ids instead of conditioned rows (cg_trunk_forward_tokens): x = rms_norm(table[ids]) * gain.
+struct Embed {
+  const float *table = nullptr;
+  int32_t vocab = 0;
+  const int64_t *ids = nullptr;
+  const float *gain = nullptr;
+  float eps = 0.f;
+};
+
 void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x, const float *ple,
                    const float *values, const cg_ragged *step, float *hidden, void *workspace,
-                   size_t workspace_size, void *stream) {
-  CG_REQUIRE(trunk && cache && x && step && hidden, CG_ERR_INVALID,
-             "trunk, cache, x, step and hidden are required");
+                   size_t workspace_size, void *stream, const Embed &embed = Embed{}) {
+  CG_REQUIRE(trunk && cache && step && hidden, CG_ERR_INVALID, "trunk, cache, step and hidden are required");
+  CG_REQUIRE((x != nullptr) != (embed.table != nullptr), CG_ERR_INVALID,
+             "exactly one of the input rows and the embedding table is required");
+  CG_REQUIRE(!embed.table || (embed.ids && embed.gain && embed.vocab > 0), CG_ERR_INVALID,
+             "token ids, the input norm gain and a positive vocabulary are required with the table");
   const cg_trunk &t = *trunk;
   const cg_trunk_config &c = t.cfg;
   const cg_ragged &r = *step;
@@ -453,12 +479,21 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
     a.scale_log2 = 1.4426950408889634f / sqrtf(float(D));
     return a;
   };
-  {
+  // The fused path's first launch forms the plan of padded runs itself; packed runs keep a
+  // launch for it (each token's sequence is a search over the chunk bounds, a chain of
+  // dependent loads that measured 14 us longer per step inside the first launch at config 5).
+  const bool plan_in_first = t.fused && !r.seq_start;
+  if (!plan_in_first) {
     const int n = N > r.n_seqs ? N : r.n_seqs;
     plan_kernel<<<(n + 255) / 256, 256, 0, s>>>(r.seq_start, r.positions, r.rows, r.readout, r.n_seqs, N, r.T,
                                                 max_len, cache[0].capacity, w.tok_row, w.tok_pos, w.readout_tok,
                                                 w.tok_out, hidden, d, r.status);
     CG_LAUNCHED();
+  }
+  if (!t.fused && embed.table) {
+    launch_embed_rmsnorm(embed.table, embed.vocab, embed.ids, embed.gain, embed.eps, w.x, N, d,
+                         r.status ? r.status + 3 : nullptr, s);
+    x = w.x;
   }
   // Packed chunks on a 16-bit pool deal their units longest first: the unit order (by work)
   // is the same for every layer of the step, computed once here.  One-token decode runs take
@@ -529,6 +564,28 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
       ta.x_src = x;
       ta.x_src_vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
       ta.x = w.x;
+      ta.plan = plan_in_first ? 1 : 0;
+      ta.seq_start = r.seq_start;
+      ta.positions = r.positions;
+      ta.rows = r.rows;
+      ta.readout = r.readout;
+      ta.n_seqs = r.n_seqs;
+      ta.T = r.T;
+      ta.capacity = cache[0].capacity;
+      ta.plan_row = w.tok_row;
+      ta.plan_pos = w.tok_pos;
+      ta.plan_out = w.tok_out;
+      ta.status = r.status;
+      if (embed.table) {
+        CG_REQUIRE(((reinterpret_cast<uintptr_t>(embed.table) | reinterpret_cast<uintptr_t>(embed.gain)) & 15) == 0,
+                   CG_ERR_UNSUPPORTED, "embedding table and gain must be 16-byte aligned");
+        ta.x_src = nullptr;
+        ta.embed_table = embed.table;
+        ta.vocab = embed.vocab;
+        ta.ids = embed.ids;
+        ta.in_gain = embed.gain;
+        ta.in_eps = embed.eps;
+      }
       set_next(ta, 0);
       launch_tail(ta, s);
     }
@@ -566,7 +623,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
     return;
   }
 
-  CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
+  if (x != w.x) CG_HIP(hipMemcpyAsync(w.x, x, size_t(N) * d * 4, hipMemcpyDeviceToDevice, s));
   launch_layernorm_rows(w.x, nullptr, t.layers[0].ln_attn_w, t.layers[0].ln_attn_b, c.eps, w.xn,
                         act_dtype, N, d, s);
   // Whole-row residual tiles fuse the next LayerNorm into the residual epilogue.
@@ -695,6 +752,22 @@ void *device_scratch() {
 
 extern "C" {
 
+int cg_trunk_forward_tokens(const cg_trunk *trunk, const cg_kv_layer *cache, const float *table, int32_t vocab,
+                            const int64_t *ids, const float *gain, float eps, const float *ple, const float *values,
+                            const cg_ragged *step, float *hidden, void *workspace, size_t workspace_size,
+                            void *stream) {
+  return guarded([&] {
+    CG_REQUIRE(table != nullptr, CG_ERR_INVALID, "table is NULL");
+    Embed e;
+    e.table = table;
+    e.vocab = vocab;
+    e.ids = ids;
+    e.gain = gain;
+    e.eps = eps;
+    trunk_forward(trunk, cache, nullptr, ple, values, step, hidden, workspace, workspace_size, stream, e);
+  });
+}
+
 int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
                      const float *ple, const float *values, const cg_ragged *step, float *hidden,
                      void *workspace, size_t workspace_size, void *stream) {
@@ -747,15 +820,7 @@ int cg_embed_rmsnorm(const float *table, int32_t vocab, const int64_t *ids, cons
     CG_REQUIRE(table && ids && gain && y, CG_ERR_INVALID, "table, ids, gain and y are required");
     CG_REQUIRE(n >= 0 && d > 0 && vocab > 0, CG_ERR_INVALID, "bad sizes");
     if (n == 0) return;
-    const bool aligned = ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(gain) |
-                           reinterpret_cast<uintptr_t>(y)) & 15) == 0;
-    const unsigned grid4 = unsigned((int64_t(n) + 15) / 16);  // four waves of four rows
-    hipStream_t s = as_stream(stream);
-    if (aligned && d == 256) embed_rmsnorm_rows4_kernel<4><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
-    else if (aligned && d == 128) embed_rmsnorm_rows4_kernel<2><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
-    else if (aligned && d == 64) embed_rmsnorm_rows4_kernel<1><<<grid4, 256, 0, s>>>(table, vocab, ids, gain, eps, y, n, flag);
-    else rmsnorm_rows_kernel<float><<<rows_grid(n, 4), 256, 0, s>>>(nullptr, table, vocab, ids, gain, eps, y, n, d, flag);
-    CG_LAUNCHED();
+    launch_embed_rmsnorm(table, vocab, ids, gain, eps, y, n, d, flag, as_stream(stream));
   });
 }
 

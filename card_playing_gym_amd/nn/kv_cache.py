@@ -10,7 +10,8 @@ with full-width coalesced loads.
 The pool must live on a ROCm device; the methods raise on CPU tensors (there is no CPU
 path).  Kernels skip out-of-range rows and positions instead of faulting.  The trunk step
 records what it skipped in the pool's device ``status`` words (a row outside the pool, a
-negative position, a readout offset outside its sequence) without reading anything back;
+negative position, a readout offset outside its sequence, a token id outside the embedding
+table) without reading anything back;
 ``check()`` reads them (one small copy, which waits for the stream), raises ``IndexError``
 naming what was wrong, and clears them -- a collector can call it right after it copies a
 wave's outputs to the host.  Set ``CARDGYM_HIP_CHECK=1`` to check after every eager step and
@@ -70,6 +71,7 @@ STATUS_MESSAGES = (
     "cache row outside [0, capacity)",
     "negative cache position",
     "readout offset outside its sequence",
+    "token id outside the embedding table",
 )
 
 
@@ -116,7 +118,7 @@ class KVCache:
             self.v = [torch.zeros_like(k) for k in self.k]
         self._layers: list[nat.KVLayer] | None = None
         # Set by trunk steps over this pool (cg_ragged.status): see check().
-        self.status = torch.zeros(3, device=self.device, dtype=torch.int32)
+        self.status = torch.zeros(len(STATUS_MESSAGES), device=self.device, dtype=torch.int32)
 
     def step_errors(self, clear: bool = True) -> list[str]:
         """What the trunk steps over this pool skipped since the last clear (reads the

@@ -27,7 +27,7 @@ import torch
 from torch import Tensor
 
 from .. import _native as nat
-from .kv_cache import dtype_code, stream_handle
+from .kv_cache import dtype_code, require_device, stream_handle
 
 # -- module registry --------------------------------------------------------------------
 
@@ -206,11 +206,7 @@ def trunk_step(
     hidden = torch.empty((n_seqs if readout is not None else n_tokens, d), device=device, dtype=torch.float32)
     size = nat.lib().cg_trunk_workspace_size(native.handle, n_tokens, n_seqs)
     workspace = torch.empty(max(size, 1), device=device, dtype=torch.uint8)
-    if status is not None and (status.dtype != torch.int32 or status.numel() < 3 or not status.is_contiguous()):
-        raise ValueError("status must be a contiguous int32 tensor of 3 words")
-    step = nat.Ragged(
-        n_seqs, n_tokens, T, span, _ptr(seq_start), positions.data_ptr(), _ptr(rows), _ptr(readout), _ptr(status),
-    )
+    step = _ragged(status, n_seqs, n_tokens, T, span, seq_start, positions, rows, readout)
     nat.call(
         "cg_trunk_forward", native.handle, kv_layers(k, v), x.data_ptr(), _ptr(ple), _ptr(values), ctypes.byref(step),
         hidden.data_ptr(), workspace.data_ptr(), size, stream_handle(device),
@@ -218,9 +214,64 @@ def trunk_step(
     return hidden
 
 
+def _ragged(status, n_seqs, n_tokens, T, span, seq_start, positions, rows, readout) -> "nat.Ragged":
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 4 or not status.is_contiguous()):
+        raise ValueError("status must be a contiguous int32 tensor of 4 words")
+    return nat.Ragged(
+        n_seqs, n_tokens, T, span, _ptr(seq_start), positions.data_ptr(), _ptr(rows), _ptr(readout), _ptr(status),
+    )
+
+
 @trunk_step.register_fake
 def _(x, ple, values, k, v, status, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
     return x.new_empty((n_seqs if readout is not None else x.shape[0], x.shape[1]))
+
+
+@torch.library.custom_op("cardgym_hip::trunk_step_tokens", mutates_args=("k", "v", "status"))
+def trunk_step_tokens(
+    ids: Tensor,
+    table: Tensor,
+    gain: Tensor,
+    eps: float,
+    k: List[Tensor],
+    v: List[Tensor],
+    status: Optional[Tensor],
+    positions: Tensor,
+    seq_start: Optional[Tensor],
+    rows: Optional[Tensor],
+    readout: Optional[Tensor],
+    trunk: int,
+    compute: int,
+    n_seqs: int,
+    T: int,
+    span: int,
+) -> Tensor:
+    """``trunk_step`` of the rows rms_norm(table[ids], eps) * gain (``cg_trunk_forward_tokens``):
+    a single-field token embedder and the trunk's input RMSNorm folded into the step.  ``ids``
+    int64 [n_tokens]; ``table`` fp32 [vocab, d]; ``gain`` fp32 [d]."""
+
+    require_device(ids, table, gain)
+    if table.device != ids.device or gain.device != ids.device:
+        raise RuntimeError("token ids, embedding table and gain must be on one device")
+    module = lookup(trunk)
+    device = ids.device
+    native = module.native(device, compute)
+    n_tokens, d = ids.numel(), table.shape[1]
+    hidden = torch.empty((n_seqs if readout is not None else n_tokens, d), device=device, dtype=torch.float32)
+    size = nat.lib().cg_trunk_workspace_size(native.handle, n_tokens, n_seqs)
+    workspace = torch.empty(max(size, 1), device=device, dtype=torch.uint8)
+    step = _ragged(status, n_seqs, n_tokens, T, span, seq_start, positions, rows, readout)
+    nat.call(
+        "cg_trunk_forward_tokens", native.handle, kv_layers(k, v), _param(table).data_ptr(), table.shape[0],
+        ids.data_ptr(), _param(gain).data_ptr(), float(eps), None, None, ctypes.byref(step), hidden.data_ptr(),
+        workspace.data_ptr(), size, stream_handle(device),
+    )
+    return hidden
+
+
+@trunk_step_tokens.register_fake
+def _(ids, table, gain, eps, k, v, status, positions, seq_start, rows, readout, trunk, compute, n_seqs, T, span):
+    return ids.new_empty((n_seqs if readout is not None else ids.numel(), table.shape[1]), dtype=torch.float32)
 
 
 # -- heads and game embedders -----------------------------------------------------------

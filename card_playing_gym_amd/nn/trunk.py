@@ -346,7 +346,7 @@ class Trunk(ops.Registered, nn.Module):
 
     def _run(
         self,
-        x: torch.Tensor,
+        x: torch.Tensor | None,
         ple: torch.Tensor | None,
         values: torch.Tensor | None,
         cache: KVCache,
@@ -358,15 +358,29 @@ class Trunk(ops.Registered, nn.Module):
         rows: torch.Tensor | None,
         readout: torch.Tensor | None,
         span: int | None,
+        tokens: tuple[torch.Tensor, torch.Tensor] | None = None,
     ) -> torch.Tensor:
         # (The pool is named by its storage tensors only, never by its per-layer views:
         # see KVCache.pools.)
-        require_device(x)
         if cache.device.type != "cuda":
             raise RuntimeError("the KV pool must live on the GPU")
         config = self.config
         if cache.n_layers != config.n_layers or cache.kv_heads != config.n_kv_heads or cache.head_dim != config.head_dim:
             raise ValueError("cache layout does not match the trunk")
+        k_pools, v_pools = cache.pools()
+        if tokens is not None:
+            # Token ids through a single-field embedding table and the input norm, in the step.
+            ids, table = tokens
+            require_device(ids)
+            norm = self.input_norm
+            hidden = ops.trunk_step_tokens(
+                ids, table, norm.weight, float(norm.eps), k_pools, v_pools, cache.status, positions, seq_start, rows,
+                readout, self.op_key, compute_dtype_code(ids.device), n_seqs, T, 0 if span is None else int(span),
+            )
+            if check_enabled() and not torch.compiler.is_compiling() and not torch.cuda.is_current_stream_capturing():
+                cache.check()
+            return hidden
+        require_device(x)
         device = x.device
         n_tokens = x.numel() // config.d_model
         flat = x.reshape(n_tokens, config.d_model).float().contiguous()
@@ -378,7 +392,6 @@ class Trunk(ops.Registered, nn.Module):
             raise ValueError("This trunk expects a value-embedding lookup.")
         # One opaque op per step (torch.ops.cardgym_hip.trunk_step): eager, compiled and
         # captured calls all launch the same cg_trunk_forward.
-        k_pools, v_pools = cache.pools()
         hidden = ops.trunk_step(
             flat, ple_flat, values_flat, k_pools, v_pools, cache.status, positions, seq_start, rows, readout,
             self.op_key, compute_dtype_code(device), n_seqs, T, 0 if span is None else int(span),
@@ -438,6 +451,56 @@ class Trunk(ops.Registered, nn.Module):
             x, ple, values, cache, n_seqs=starts.numel() - 1, T=0, seq_start=starts,
             positions=index_tensor(positions, device), rows=None if rows is None else index_tensor(rows, device),
             readout=None if readout_offsets is None else index_tensor(readout_offsets, device), span=span,
+        )
+
+    def tokens_fold(self, width: int) -> bool:
+        """Whether a single-field embedder's token ids (``width`` 1) can go into the step itself
+        (``cg_trunk_forward_tokens``): an input norm, no per-layer or value embeddings, and
+        no autograd recording."""
+
+        return (
+            width == 1 and self.input_norm is not None and not self.config.per_layer_dim
+            and not self._value_index and not self._recording()
+        )
+
+    def forward_ragged_tokens(self, ids, table, cache, positions, readout_offsets, span=None, rows=None):
+        """``forward_ragged`` of the rows rms_norm(table[ids]) * input_norm.weight: ids int64
+        [B, T] (padded runs), table the embedder's fp32 [vocab, d_model] weight."""
+
+        device = ids.device
+        batch, length = ids.shape
+        return self._run(
+            None, None, None, cache, n_seqs=batch, T=length, seq_start=None,
+            positions=index_tensor(positions, device), rows=None if rows is None else index_tensor(rows, device),
+            readout=index_tensor(readout_offsets, device), span=span,
+            tokens=(ids.reshape(-1).to(torch.int64).contiguous(), table),
+        )
+
+    def forward_packed_tokens(self, ids, table, cache, positions, seq_start, readout_offsets, rows=None, span=None):
+        """``forward_packed`` of token ids [N] (int64) through ``table`` and the input norm."""
+
+        device = ids.device
+        starts = index_tensor(seq_start, device)
+        return self._run(
+            None, None, None, cache, n_seqs=starts.numel() - 1, T=0, seq_start=starts,
+            positions=index_tensor(positions, device), rows=None if rows is None else index_tensor(rows, device),
+            readout=None if readout_offsets is None else index_tensor(readout_offsets, device), span=span,
+            tokens=(ids.reshape(-1).to(torch.int64).contiguous(), table),
+        )
+
+    def forward_prefill_tokens(self, ids, table, cache, rows):
+        """``forward_prefill`` of token ids [B, T] (int64) through ``table`` and the input norm."""
+
+        batch, length = ids.shape
+        if length > cache.max_len:
+            raise IndexError("prefill longer than the pool's max_len")
+        device = ids.device
+        return self._run(
+            None, None, None, cache, n_seqs=batch, T=length, seq_start=None,
+            positions=torch.zeros(batch, dtype=torch.int64, device=device),
+            rows=None if rows is None else index_tensor(rows, device),
+            readout=torch.full((batch,), length - 1, dtype=torch.int64, device=device), span=length,
+            tokens=(ids.reshape(-1).to(torch.int64).contiguous(), table),
         )
 
     def forward_prefill(

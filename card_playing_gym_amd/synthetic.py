@@ -71,6 +71,25 @@ class SyntheticModel(ops.Registered, SequenceModel):
         out = ops.embed_rmsnorm(self.embedding.weight, ids, trunk.input_norm.weight, float(trunk.input_norm.eps))
         return out.view(*tokens.shape[:-1], d), None, None
 
+    # The step from token ids: the embedding lookup and the input norm run inside the trunk
+    # step (cg_trunk_forward_tokens) instead of as a launch of their own before it.
+    def forward_ragged(self, tokens, positions, cache, readout_offsets, span=None, rows=None):
+        if not self.trunk.tokens_fold(tokens.shape[-1]) or self.trunk._recording(self.embedding.weight):
+            return super().forward_ragged(tokens, positions, cache, readout_offsets, span, rows)
+        return self.trunk.forward_ragged_tokens(tokens[..., 0], self.embedding.weight, cache, positions,
+                                                readout_offsets, span, rows)
+
+    def forward_packed(self, tokens, seq_start, positions, cache, readout_offsets, rows=None, span=None):
+        if not self.trunk.tokens_fold(tokens.shape[-1]) or self.trunk._recording(self.embedding.weight):
+            return super().forward_packed(tokens, seq_start, positions, cache, readout_offsets, rows, span)
+        return self.trunk.forward_packed_tokens(tokens[..., 0], self.embedding.weight, cache, positions, seq_start,
+                                                readout_offsets, rows, span)
+
+    def forward_prefill(self, tokens, cache, rows):
+        if not self.trunk.tokens_fold(tokens.shape[-1]) or self.trunk._recording(self.embedding.weight):
+            return super().forward_prefill(tokens, cache, rows)
+        return self.trunk.forward_prefill_tokens(tokens[..., 0], self.embedding.weight, cache, rows)
+
     def heads(self, hidden: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Policy logits [B, vocab] and seat values [B, seats], fp32.
 

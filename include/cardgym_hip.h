@@ -254,14 +254,17 @@ typedef struct cg_ragged {
   const int64_t *positions;  /* int64 [n_seqs] */
   const int64_t *rows;       /* int64 [n_seqs] or NULL */
   const int64_t *readout;    /* int64 [n_seqs] or NULL */
-  int32_t *status;           /* int32 [3] device words or NULL: the step sets status[0] = 1
+  int32_t *status;           /* int32 [4] device words or NULL: the step sets status[0] = 1
                                 when some rows[b] is outside [0, capacity), status[1] = 1 when
                                 some positions[b] is negative (those tokens are neither written
                                 nor attended: where the reference's index_put would raise,
                                 kv_cache.py:98-105), status[2] = 1 when some readout[b] is
                                 outside [-len_b, len_b) of its sequence (a zero hidden row;
                                 negative offsets count from the sequence's end, as torch
-                                indexing does, trunk.py:429).  Never cleared by the step. */
+                                indexing does, trunk.py:429), status[3] = 1 when a token id of
+                                cg_trunk_forward_tokens is outside the table (a zero input
+                                row, where F.embedding would raise).  Never cleared by the
+                                step. */
 } cg_ragged;
 
 /* Workspace bytes cg_trunk_forward needs for n_tokens tokens and n_seqs sequences. */
@@ -277,6 +280,17 @@ size_t cg_trunk_workspace_size(const cg_trunk *trunk, int32_t n_tokens, int32_t 
 int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x,
                      const float *ple, const float *values, const cg_ragged *step, float *hidden,
                      void *workspace, size_t workspace_size, void *stream);
+
+/* SequenceModel.forward_ragged of a single-field token embedder (cardgym/nn/model.py:76-89:
+ * embed, Trunk.condition's input RMSNorm, Trunk.forward_ragged; trunk.py:104-115, 285-312,
+ * 391-429) from token ids: x = rms_norm(table[ids[i]], eps) * gain for the packed tokens
+ * (ids int64 [n_tokens], table fp32 [vocab, d_model], gain fp32 [d_model]), then exactly
+ * cg_trunk_forward.  With bf16 projections the rows are formed inside the first layer's
+ * launch, together with the step's per-token plan, instead of in launches of their own. */
+int cg_trunk_forward_tokens(const cg_trunk *trunk, const cg_kv_layer *cache, const float *table, int32_t vocab,
+                            const int64_t *ids, const float *gain, float eps, const float *ple, const float *values,
+                            const cg_ragged *step, float *hidden, void *workspace, size_t workspace_size,
+                            void *stream);
 
 /* No counterpart in the reference.  cg_trunk_forward for callers that cannot allocate its
  * workspace (code under HIP graph capture that must not call hipMalloc, tight serving loops,

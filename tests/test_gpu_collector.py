@@ -150,6 +150,61 @@ def test_step_status_words(device):
     assert torch.equal(got[3], torch.zeros_like(got[3]))
     assert torch.equal(got[:3], want[:3]) and torch.equal(got[4:], want[4:])
     assert cache.step_errors() == ["readout offset outside its sequence"]
+    # A token id outside the embedding table (F.embedding would raise): a zero input row.
+    bad_tokens = tokens.clone()
+    bad_tokens[2, 0, 0] = 512 + 7
+    with torch.no_grad(), autocast(device, "bf16"):
+        model.forward_ragged(bad_tokens, positions, cache, last, rows=rows)
+    assert cache.step_errors() == ["token id outside the embedding table"]
+
+
+@pytest.mark.parametrize("mode", ["padded", "packed", "prefill"])
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_token_step_matches_row_step(device, precision, mode):
+    """The step from token ids (embedding and input norm inside the step,
+    cg_trunk_forward_tokens) against the step from conditioned rows (embedding norm as
+    its own launch, then cg_trunk_forward): fp32 bit-equal (the same kernels), bf16
+    within the bf16 bar (the first layer kernel sums each row's squares in its own order)."""
+
+    config = trunk_config(4)
+    model, _ = twins(config, precision, device)
+    dtype = torch.bfloat16 if precision == "bf16" else torch.float32
+    capacity, max_len, B, T = 48, 64, 40, 3
+    caches = [model.new_cache(capacity, max_len, dtype) for _ in range(2)]
+    gen = torch.Generator().manual_seed(31)
+    tokens = torch.randint(0, 512, (B, T, 1), generator=gen).to(device)
+    positions = torch.randint(0, max_len - T, (B,), generator=gen).to(device)
+    rows = torch.randperm(capacity, generator=gen)[:B].to(device)
+    readout = torch.randint(0, T, (B,), generator=gen).to(device)
+    seq_start = torch.arange(B + 1, device=device) * T
+    trunk = model.trunk
+    out = []
+    with torch.no_grad(), autocast(device, precision):
+        for fold, cache in zip((True, False), caches):
+            if fold:
+                if mode == "padded":
+                    h = model.forward_ragged(tokens, positions, cache, readout, rows=rows)
+                elif mode == "packed":
+                    h = model.forward_packed(tokens.reshape(B * T, 1), seq_start, positions, cache, readout, rows)
+                else:
+                    h = model.forward_prefill(tokens, cache, rows)
+            else:
+                x, _, _ = model.prepare(tokens)
+                if mode == "padded":
+                    h = trunk.forward_ragged(x, None, None, cache, positions, readout, rows=rows)
+                elif mode == "packed":
+                    h = trunk.forward_packed(x.reshape(B * T, -1), None, None, cache, positions, seq_start, readout, rows)
+                else:
+                    h = trunk.forward_prefill(x, None, None, cache, rows)
+            out.append(h)
+    torch.cuda.synchronize()
+    if precision == "fp32":
+        assert torch.equal(out[0], out[1])
+        assert all(torch.equal(a, b) for a, b in zip(caches[0].k + caches[0].v, caches[1].k + caches[1].v))
+    else:
+        assert max_err(out[0], out[1]) <= BF16_TOL
+    for cache in caches:
+        cache.check()
 
 
 @pytest.mark.parametrize("mode", ["decode", "padded", "packed"])

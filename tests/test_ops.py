@@ -19,7 +19,8 @@ from card_playing_gym_amd.nn.kv_cache import KVCache
 from card_playing_gym_amd.nn.trunk import TrunkConfig
 from card_playing_gym_amd.synthetic import build_model
 
-OPS = ("rmsnorm", "embed_rmsnorm", "ple_context", "trunk_step", "synthetic_heads", "piquet_embed", "decode_attention")
+OPS = ("rmsnorm", "embed_rmsnorm", "ple_context", "trunk_step", "trunk_step_tokens", "synthetic_heads", "piquet_embed",
+       "decode_attention")
 
 
 def test_ops_are_registered():
@@ -30,6 +31,9 @@ def test_ops_are_registered():
     schema = str(torch.ops.cardgym_hip.trunk_step.default._schema)
     # The pools are declared mutated (so functionalisation orders them), nothing else is.
     assert "Tensor(a3!)[] k" in schema and "Tensor(a4!)[] v" in schema and "Tensor(a5!)? status" in schema, schema
+    assert schema.count("!") == 3, schema
+    schema = str(torch.ops.cardgym_hip.trunk_step_tokens.default._schema)
+    assert "Tensor(a4!)[] k" in schema and "Tensor(a5!)[] v" in schema and "Tensor(a6!)? status" in schema, schema
     assert schema.count("!") == 3, schema
 
 
@@ -118,9 +122,16 @@ def test_compiled_wave_hands_the_op_the_pool_itself(monkeypatch, stacked):
                     layer[int(rows[b]), :, min(int(positions[b]) + t, layer.shape[2] - 1)] = 1.0
         return x.new_zeros((int(n_seqs), x.shape[1]))
 
+    def tokens_cpu(ids, table, gain, eps, k, v, status, positions, seq_start, rows, readout, trunk, compute, n_seqs,
+                   T, span):
+        x = table.new_zeros((ids.numel(), table.shape[1]))
+        return trunk_cpu(x, None, None, k, v, status, positions, seq_start, rows, readout, trunk, compute, n_seqs, T,
+                         span)
+
     torch._dynamo.reset()
     with torch.library._scoped_library("cardgym_hip", "IMPL") as lib:
         lib.impl("trunk_step", trunk_cpu, "CPU")
+        lib.impl("trunk_step_tokens", tokens_cpu, "CPU")
         lib.impl("embed_rmsnorm", lambda table, ids, w, eps: table.new_zeros((ids.numel(), table.shape[1])), "CPU")
         lib.impl("synthetic_heads", lambda h, m, c, p, n: (h.new_zeros((h.shape[0], p)), h.new_zeros((h.shape[0], n))),
                  "CPU")
