@@ -27,6 +27,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import signal
 import sys
 import time
 from pathlib import Path
@@ -1046,15 +1047,72 @@ def main() -> int:
     return 0
 
 
-def _stop_compile_workers() -> None:
-    """The compiled reference leg starts Inductor's compile worker processes; end them so
-    that no process outlives the benchmark."""
+def _descendants() -> list[int]:
+    """PIDs of every process this one started, directly or not (from /proc)."""
 
+    parent: dict[int, int] = {}
+    for entry in os.listdir("/proc"):
+        if not entry.isdigit():
+            continue
+        try:
+            with open(f"/proc/{entry}/stat") as f:
+                fields = f.read().rsplit(")", 1)[1].split()
+            parent[int(entry)] = int(fields[1])
+        except (OSError, IndexError, ValueError):
+            continue
+    found, frontier = [], [os.getpid()]
+    while frontier:
+        pid = frontier.pop()
+        kids = [p for p, pp in parent.items() if pp == pid]
+        found.extend(kids)
+        frontier.extend(kids)
+    return found
+
+
+def _alive(pid: int) -> bool:
+    try:
+        with open(f"/proc/{pid}/stat") as f:
+            return f.read().rsplit(")", 1)[1].split()[0] != "Z"
+    except (OSError, IndexError):
+        return False
+
+
+def _stop_compile_workers() -> None:
+    """The compiled reference leg starts Inductor's compile workers (a sidecar process and
+    its pool) and multiprocessing may start a resource tracker: ask the workers to shut down,
+    then wait for every process this one started, directly or through them, and end any
+    that is still running after a grace period, so that no process outlives the benchmark.
+    The descendants are listed before the shutdown, so that pool processes whose parent
+    exits first are still waited for."""
+
+    kids = _descendants()
     try:
         from torch._inductor.async_compile import shutdown_compile_workers
     except ImportError:
-        return
-    shutdown_compile_workers()
+        shutdown_compile_workers = None
+    if shutdown_compile_workers is not None:
+        shutdown_compile_workers()
+    for sig, grace in ((None, 3.0), (signal.SIGTERM, 3.0), (signal.SIGKILL, 2.0)):
+        alive = [p for p in kids if _alive(p)]
+        if not alive:
+            break
+        if sig is not None:
+            for pid in alive:
+                try:
+                    os.kill(pid, sig)
+                except OSError:
+                    pass
+        deadline = time.monotonic() + grace
+        while time.monotonic() < deadline and any(_alive(p) for p in alive):
+            for pid in alive:
+                try:
+                    os.waitpid(pid, os.WNOHANG)  # reaps direct children
+                except ChildProcessError:
+                    pass
+            time.sleep(0.05)
+    left = [p for p in kids if _alive(p)]
+    if left:
+        log(f"bench: {len(left)} child processes still running at exit")
 
 
 if __name__ == "__main__":
