@@ -490,7 +490,13 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
                                                 w.tok_out, hidden, d, r.status);
     CG_LAUNCHED();
   }
-  if (!t.fused && embed.table) {
+  // The fused first launch reads the embedding rows through a buffer descriptor (a 32-bit
+  // byte range) as float4 runs: tables of 4 GiB or more, or unaligned ones, take the
+  // embedding norm as a launch of its own, whose rows the first launch then reads.
+  const bool embed_in_first =
+      embed.table && t.fused && int64_t(embed.vocab) * d * 4 < (int64_t(1) << 32) &&
+      ((reinterpret_cast<uintptr_t>(embed.table) | reinterpret_cast<uintptr_t>(embed.gain)) & 15) == 0;
+  if (embed.table && !embed_in_first) {
     launch_embed_rmsnorm(embed.table, embed.vocab, embed.ids, embed.gain, embed.eps, w.x, N, d,
                          r.status ? r.status + 3 : nullptr, s);
     x = w.x;
@@ -576,9 +582,7 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
       ta.plan_pos = w.tok_pos;
       ta.plan_out = w.tok_out;
       ta.status = r.status;
-      if (embed.table) {
-        CG_REQUIRE(((reinterpret_cast<uintptr_t>(embed.table) | reinterpret_cast<uintptr_t>(embed.gain)) & 15) == 0,
-                   CG_ERR_UNSUPPORTED, "embedding table and gain must be 16-byte aligned");
+      if (embed_in_first) {
         ta.x_src = nullptr;
         ta.embed_table = embed.table;
         ta.vocab = embed.vocab;

@@ -286,7 +286,9 @@ int cg_trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const floa
  * 391-429) from token ids: x = rms_norm(table[ids[i]], eps) * gain for the packed tokens
  * (ids int64 [n_tokens], table fp32 [vocab, d_model], gain fp32 [d_model]), then exactly
  * cg_trunk_forward.  With bf16 projections the rows are formed inside the first layer's
- * launch, together with the step's per-token plan, instead of in launches of their own. */
+ * launch, together with the step's per-token plan, instead of in launches of their own
+ * (when table and gain are 16-byte aligned and the table is under 4 GiB; otherwise the
+ * embedding norm runs as a launch of its own first, with the same result). */
 int cg_trunk_forward_tokens(const cg_trunk *trunk, const cg_kv_layer *cache, const float *table, int32_t vocab,
                             const int64_t *ids, const float *gain, float eps, const float *ple, const float *values,
                             const cg_ragged *step, float *hidden, void *workspace, size_t workspace_size,

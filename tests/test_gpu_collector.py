@@ -207,6 +207,39 @@ def test_token_step_matches_row_step(device, precision, mode):
         cache.check()
 
 
+def test_unaligned_table_takes_the_separate_embedding_launch(device):
+    """An embedding table the first layer launch cannot read as float4 runs (not 16-byte
+    aligned) is normed by its own launch first (cg_trunk_forward_tokens falls back instead of
+    refusing): the same step as from the aligned table, at the bf16 bar, and the status word
+    of a bad id still set."""
+
+    config = trunk_config(2)
+    model, _ = twins(config, "bf16", device)
+    capacity, max_len, B = 48, 64, 40
+    gen = torch.Generator().manual_seed(37)
+    ids = torch.randint(0, 512, (B, 1), generator=gen).to(device)
+    positions = torch.randint(0, max_len - 1, (B,), generator=gen).to(device)
+    rows = torch.randperm(capacity, generator=gen)[:B].to(device)
+    readout = torch.zeros(B, dtype=torch.int64, device=device)
+    table = model.embedding.weight.detach()
+    spare = torch.empty(table.numel() + 1, device=device, dtype=torch.float32)
+    shifted = spare[1:].view_as(table)
+    shifted.copy_(table)
+    assert shifted.data_ptr() % 16 != 0
+    caches = [model.new_cache(capacity, max_len, torch.bfloat16) for _ in range(2)]
+    out = []
+    with torch.no_grad(), autocast(device, "bf16"):
+        for t, cache in zip((table, shifted), caches):
+            out.append(model.trunk.forward_ragged_tokens(ids, t, cache, positions, readout, rows=rows))
+        bad = ids.clone()
+        bad[5, 0] = -3
+        model.trunk.forward_ragged_tokens(bad, shifted, caches[1], positions, readout, rows=rows)
+    torch.cuda.synchronize()
+    assert max_err(out[0], out[1]) <= BF16_TOL
+    caches[0].check()
+    assert caches[1].step_errors() == ["token id outside the embedding table"]
+
+
 @pytest.mark.parametrize("mode", ["decode", "padded", "packed"])
 @pytest.mark.parametrize("pool", [torch.bfloat16, torch.float16])
 def test_fused_append_converts_like_tensor_to(device, pool, mode):
