@@ -210,11 +210,11 @@ __device__ __forceinline__ float sum16(float v) {
 // approximation of Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7, far below the bf16
 // rounding the result gets): erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^{-z^2},
 // t = 1 / (1 + p z) for z = |x| / sqrt 2 >= 0.  With q = erfc(z) / 2 (the halves folded into
-// the coefficients), Phi(x) = 1 - q for x >= 0 and q for x < 0, i.e. 0.5 + copysign(0.5 - q, x):
-// 0.5 - q is one FMA, the sign one bit insert (v_bfi), so no compare or select.  The
-// subtraction adds at most ~1.5e-8 to Phi, below the approximation's own 7.5e-8.  GELU(+inf)
-// = +inf, GELU(-inf) = NaN and GELU(-0) = -0, as torch's formula gives.  Fourteen VALU
-// instructions, two of them transcendental.
+// the coefficients), Phi(x) = 1 - q for x >= 0 and q for x < 0, so with h = 0.5 - q (one FMA)
+// GELU(x) = x / 2 + |x| h for either sign: one more FMA, no compare, select or sign insert.
+// Computing h adds at most ~1.5e-8 to Phi, below the approximation's own 7.5e-8.  GELU(+inf)
+// = +inf and GELU(-inf) = NaN, as torch's formula gives; GELU(-0) is +0 (torch: -0, the same
+// value).  Thirteen VALU instructions, two of them transcendental.
 __device__ __forceinline__ float gelu_fast(float x) {
   const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, fabsf(x), 1.0f));
   float poly = fmaf(0.5f * 1.061405429f, t, 0.5f * -1.453152027f);
@@ -223,7 +223,7 @@ __device__ __forceinline__ float gelu_fast(float x) {
   poly = fmaf(poly, t, 0.5f * 0.254829592f);
   const float e = __builtin_amdgcn_exp2f((x * (-0.5f * 1.4426950408889634f)) * x);
   const float h = fmaf(-(poly * t), e, 0.5f);  // 0.5 - q
-  return x * (0.5f + __builtin_copysignf(h, x));
+  return fmaf(fabsf(x), h, 0.5f * x);
 }
 
 // GELU of four bf16 values (packed two per word, low half first) -> four bf16 values: the
