@@ -14,9 +14,9 @@ pools, on the HIP path against the oracle (cardgym/nn/trunk.py, kv_cache.py rest
 * The fused append (the QKV epilogue of the layer kernel): the bits it stores in a 16-bit
   pool are ``Tensor.to`` of the fp32 values the same step stores in an fp32 pool (nearest
   even; NaN -> 0x7fc0 in bf16).
-* fp16 pools (``kv_dtype = "fp16"`` of the reference's configs) with fp32 projections,
-  through ``forward_ragged`` (rows, resets), ``forward_packed`` and prefill; fp16 autocast
-  itself is refused.
+* fp16 pools (``kv_dtype = "fp16"`` of the reference's configs) with fp32 projections and
+  under bf16 autocast (the reference's own pairing), through ``forward_ragged`` (rows,
+  resets), ``forward_packed`` and prefill; fp16 autocast itself is refused.
 """
 
 from __future__ import annotations
@@ -286,15 +286,18 @@ FP16_WORKLOADS = {
 }
 
 
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
 @pytest.mark.parametrize("name", sorted(FP16_WORKLOADS))
-def test_fp16_pool_matches_oracle(device, name):
-    """fp16 K / V storage with fp32 projections: the reference rounds q, the scores and P
-    to the pool's type (trunk.py:222, 245, 255); bar 2e-2 on hidden states, logits and
-    values; cache slots as check_step compares them."""
+def test_fp16_pool_matches_oracle(device, name, precision):
+    """fp16 K / V storage with fp32 projections, and under bf16 autocast (the reference's
+    own configs pair ``precision = "bf16"`` with ``kv_dtype = "fp16"``, e.g.
+    configs/piquet/base.toml:12-16): the reference rounds q, the scores and P to the pool's
+    type (trunk.py:222, 245, 255); bar 2e-2 on hidden states, logits and values; cache slots
+    as check_step compares them."""
 
     workload = FP16_WORKLOADS[name]
     config = workload.trunk_config()
-    model, ref = twins(config, "fp32", device)
+    model, ref = twins(config, precision, device)
     max_len = workload.max_len(4)
     driver = Driver(workload, seed=2, max_len=max_len)
     native, oracle = cache_pair(config, workload.games, max_len, torch.float16, device)
@@ -302,8 +305,8 @@ def test_fp16_pool_matches_oracle(device, name):
     packed, rows = workload.mode == "chunks", workload.mode == "continuous"
     for step in range(4):
         plan = driver.step()
-        errs = check_step(model, ref, native, oracle, plan, device, "fp32", packed, rows, BF16_TOL)
-        print(f"{name} step {step}: {errs}", flush=True)
+        errs = check_step(model, ref, native, oracle, plan, device, precision, packed, rows, BF16_TOL)
+        print(f"{name} {precision} step {step}: {errs}", flush=True)
     native.check()
 
 
