@@ -146,6 +146,15 @@ __global__ void plan_kernel(const int64_t *__restrict__ seq_start, const int64_t
   }
 }
 
+// A step with sequences but no tokens: every readout offset is outside its (empty) chunk, so
+// every hidden row is zero and the readout status word is set, as plan_kernel does per row.
+__global__ void empty_readout_kernel(float *__restrict__ hidden, int32_t n_seqs, int32_t d,
+                                     int32_t *__restrict__ status) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < int64_t(n_seqs) * d) hidden[i] = 0.f;
+  if (i == 0 && status) status[2] = 1;
+}
+
 // One wave per row: y = rms_norm(src row) * gain; src row = table[ids[row]] or x[row].
 // XT float: fp32 rows; XT bf16: bf16 rows whose normalised value rounds to bf16 before the
 // gain (rms_norm(x.float()).to(x.dtype) * gain).
@@ -395,10 +404,14 @@ struct Embed {
 void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float *x, const float *ple,
                    const float *values, const cg_ragged *step, float *hidden, void *workspace,
                    size_t workspace_size, void *stream, const Embed &embed = Embed{}) {
-  CG_REQUIRE(trunk && cache && step && hidden, CG_ERR_INVALID, "trunk, cache, step and hidden are required");
-  CG_REQUIRE((x != nullptr) != (embed.table != nullptr), CG_ERR_INVALID,
+  CG_REQUIRE(trunk && cache && step, CG_ERR_INVALID, "trunk, cache and step are required");
+  // A step without tokens reads no rows (its empty inputs may come as NULL) and writes hidden
+  // rows only for readouts.
+  const bool no_tokens = step->n_tokens == 0;
+  CG_REQUIRE(hidden || (no_tokens && !step->readout), CG_ERR_INVALID, "hidden is required");
+  CG_REQUIRE(no_tokens || (x != nullptr) != (embed.table != nullptr), CG_ERR_INVALID,
              "exactly one of the input rows and the embedding table is required");
-  CG_REQUIRE(!embed.table || (embed.ids && embed.gain && embed.vocab > 0), CG_ERR_INVALID,
+  CG_REQUIRE(!embed.table || no_tokens || (embed.ids && embed.gain && embed.vocab > 0), CG_ERR_INVALID,
              "token ids, the input norm gain and a positive vocabulary are required with the table");
   const cg_trunk &t = *trunk;
   const cg_trunk_config &c = t.cfg;
@@ -407,9 +420,9 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
   CG_REQUIRE(r.positions != nullptr, CG_ERR_INVALID, "positions is NULL");
   CG_REQUIRE(r.seq_start || int64_t(r.n_seqs) * r.T == r.n_tokens, CG_ERR_INVALID,
              "padded step: n_tokens must equal n_seqs * T");
-  CG_REQUIRE(c.per_layer_dim == 0 || ple, CG_ERR_INVALID,
+  CG_REQUIRE(r.n_tokens == 0 || c.per_layer_dim == 0 || ple, CG_ERR_INVALID,
              "This trunk expects a per-layer embedding lookup.");
-  CG_REQUIRE(c.value_width == 0 || values, CG_ERR_INVALID,
+  CG_REQUIRE(r.n_tokens == 0 || c.value_width == 0 || values, CG_ERR_INVALID,
              "This trunk expects a value-embedding lookup.");
   for (int l = 0; l < c.n_layers; ++l) {
     const cg_kv_layer &L = cache[l];
@@ -422,7 +435,16 @@ void trunk_forward(const cg_trunk *trunk, const cg_kv_layer *cache, const float 
   }
   CG_REQUIRE(r.rows || r.n_seqs <= cache[0].capacity, CG_ERR_RANGE,
              "dense rows: more sequences than cache rows");
-  if (r.n_tokens == 0 || r.n_seqs == 0) return;
+  if (r.n_seqs == 0) return;
+  if (r.n_tokens == 0) {
+    if (r.readout) {
+      const int64_t n = int64_t(r.n_seqs) * c.d_model;
+      empty_readout_kernel<<<unsigned((n + 255) / 256), 256, 0, as_stream(stream)>>>(hidden, r.n_seqs, c.d_model,
+                                                                                    r.status);
+      CG_LAUNCHED();
+    }
+    return;
+  }
   Workspace w = carve(t, r.n_tokens, r.n_seqs, static_cast<char *>(workspace));
   CG_REQUIRE(workspace && workspace_size >= w.bytes, CG_ERR_INVALID,
              "workspace too small: need " + std::to_string(w.bytes) + " bytes");

@@ -207,6 +207,30 @@ def test_token_step_matches_row_step(device, precision, mode):
         cache.check()
 
 
+@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+def test_packed_step_without_tokens(device, precision):
+    """Packed sequences that all carry zero tokens: nothing is written, every readout is
+    outside its (empty) chunk, so every hidden row is zero and the readout status word is set
+    (the reference's indexing of the empty packed rows would raise)."""
+
+    config = trunk_config(2)
+    model, _ = twins(config, precision, device)
+    dtype = torch.bfloat16 if precision == "bf16" else torch.float32
+    cache = model.new_cache(16, 32, dtype)
+    before = [k.clone() for k in cache.k + cache.v]
+    B = 5
+    x = torch.empty((0, config.d_model), device=device)
+    seq_start = torch.zeros(B + 1, dtype=torch.int64, device=device)
+    positions = torch.arange(B, dtype=torch.int64, device=device)
+    readout = torch.zeros(B, dtype=torch.int64, device=device)
+    with torch.no_grad(), autocast(device, precision):
+        hidden = model.trunk.forward_packed(x, None, None, cache, positions, seq_start, readout)
+    torch.cuda.synchronize()
+    assert hidden.shape == (B, config.d_model) and torch.equal(hidden, torch.zeros_like(hidden))
+    assert all(torch.equal(a, b) for a, b in zip(before, cache.k + cache.v))
+    assert cache.step_errors() == ["readout offset outside its sequence"]
+
+
 def test_unaligned_table_takes_the_separate_embedding_launch(device):
     """An embedding table the first layer launch cannot read as float4 runs (not 16-byte
     aligned) is normed by its own launch first (cg_trunk_forward_tokens falls back instead of
