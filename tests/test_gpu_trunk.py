@@ -15,6 +15,7 @@ import torch
 from card_playing_gym_amd.synthetic import WORKLOADS, Driver, StepPlan, trunk_config
 from card_playing_gym_amd.nn.trunk import TrunkConfig
 from card_playing_gym_amd.nn.trunk import Trunk
+from card_playing_gym_amd.nn.kv_cache import KVCache
 from oracle.reference_path import RefCache, RefTrunk, ref_config_of
 from tests.helpers import autocast, cache_pair, fill_prefixes, max_err, random_trunk, run_native, run_oracle, twins
 
@@ -139,6 +140,63 @@ def test_ragged_decode_matches_full_forward(device):
             for row, (start, count) in enumerate(zip(cursor, counts)):
                 if count:
                     torch.testing.assert_close(hidden[row], full[row, start + count - 1], rtol=1e-5, atol=1e-5)
+            cursor = [c + n for c, n in zip(cursor, counts)]
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_conditioned_decode_matches_full_forward(device, precision):
+    """The same invariant for a trunk with per-layer embeddings and alternating value
+    embeddings (the game actors' shape; the reference checks cached policies against replay,
+    tests/piquet/test_piquet_streams.py:347-366): prefill, then ragged waves of 0-3 tokens per
+    row, each conditioned as Trunk.condition does, reproduce the full causal forward: 1e-5 in
+    fp32, the bf16 bar under bf16 autocast with a bf16 pool."""
+
+    config = TrunkConfig(d_model=64, n_layers=3, n_heads=4, n_kv_heads=2, d_ff=160, per_layer_dim=16,
+                         value_embeddings="alternating")
+    state = random_trunk(config, seed=31)
+    trunk = Trunk(config)
+    trunk.load_state_dict({k[len("trunk."):]: v for k, v in state.items()})
+    trunk = trunk.to(device)
+    rng = np.random.default_rng(3)
+    B = 6
+    lengths = [int(x) for x in rng.integers(6, 20, size=B)]
+    L = max(lengths)
+    gen = torch.Generator().manual_seed(32)
+    raw = torch.randn(B, L, config.d_model, generator=gen).to(device)
+    ple_l = torch.randn(B, L, config.ple_width, generator=gen).to(device)
+    ve_l = torch.randn(B, L, config.value_width, generator=gen).to(device)
+    tol = 1e-5 if precision == "fp32" else BF16_TOL
+    pool = torch.float32 if precision == "fp32" else torch.bfloat16
+
+    def close(got, want):
+        torch.testing.assert_close(got, want, rtol=tol, atol=tol)
+
+    with torch.no_grad(), autocast(device, precision):
+        full = trunk(*trunk.condition(raw, ple_l, ve_l)).float().cpu()
+        cache = KVCache(n_layers=config.n_layers, kv_heads=config.n_kv_heads, head_dim=config.head_dim,
+                        capacity=B, max_len=L + 1, device=device, dtype=pool)
+        x, ple, values = trunk.condition(raw[:, :4], ple_l[:, :4], ve_l[:, :4])
+        hidden = trunk.forward_prefill(x, ple, values, cache, None).cpu()
+        close(hidden, full[:, 3])
+        cursor = [4] * B
+        while any(c < n for c, n in zip(cursor, lengths)):
+            counts = [min(int(rng.integers(0, 4)), n - c) for c, n in zip(cursor, lengths)]
+            if not any(counts):
+                continue
+            run = max(counts)
+            index = torch.zeros(B, run, dtype=torch.int64)
+            offsets = torch.zeros(B, dtype=torch.int64)
+            for row, (start, count) in enumerate(zip(cursor, counts)):
+                take = [start + min(t, count - 1) for t in range(run)] if count else [0] * run
+                index[row] = torch.tensor(take)  # repeat-last padding; rows without tokens read slot 0
+                offsets[row] = max(count - 1, 0)
+            pick = lambda t: torch.gather(t, 1, index.to(device)[..., None].expand(B, run, t.shape[-1]))  # noqa: E731
+            x, ple, values = trunk.condition(pick(raw), pick(ple_l), pick(ve_l))
+            hidden = trunk.forward_ragged(x, ple, values, cache, torch.tensor(cursor, device=device),
+                                          offsets.to(device)).cpu()
+            for row, (start, count) in enumerate(zip(cursor, counts)):
+                if count:
+                    close(hidden[row], full[row, start + count - 1])
             cursor = [c + n for c, n in zip(cursor, counts)]
 
 
