@@ -353,11 +353,14 @@ SHAPES = [
     dict(d_model=240, n_layers=2, n_heads=10, n_kv_heads=2, d_ff=480, per_layer_dim=0, value_embeddings="all"),
     # full multi-head attention: three QKV chunks; a 16-wide last FF chunk; PLE repeated 4x
     dict(d_model=256, n_layers=2, n_heads=8, n_kv_heads=8, d_ff=272, per_layer_dim=64, value_embeddings="off"),
+    # head_dim 64 (the attention kernels' wide form), GQA 2 per KV head, d_ff 768 (three chunks)
+    dict(d_model=256, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=768, per_layer_dim=0, value_embeddings="alternating"),
 ]
+SHAPE_IDS = ["d64", "d240", "d256mha", "d256hd64"]
 
 
 @pytest.mark.parametrize("packed", [False, True])
-@pytest.mark.parametrize("shape", SHAPES, ids=["d64", "d240", "d256mha"])
+@pytest.mark.parametrize("shape", SHAPES, ids=SHAPE_IDS)
 def test_bf16_trunk_shapes_with_conditioning(device, shape, packed):
     """bf16 steps of trunks other than the benchmark's, with per-layer and value
     embeddings switched on, against the oracle's bf16 rounding path (2e-2)."""
@@ -414,7 +417,7 @@ def test_bf16_trunk_shapes_with_conditioning(device, shape, packed):
 
 
 @pytest.mark.parametrize("games,T", [(1024, 32), (640, 16), (384, 16)], ids=["rows64", "rows48", "rows32"])
-@pytest.mark.parametrize("shape", SHAPES, ids=["d64", "d240", "d256mha"])
+@pytest.mark.parametrize("shape", SHAPES, ids=SHAPE_IDS)
 def test_bf16_tall_prefill_with_conditioning(device, shape, games, T):
     """Prefill of 1024 rows x 32 tokens (32768 token rows: 64-row blocks of the fused layer
     kernel on 256 CUs), 640 x 16 (10240 rows: 48-row blocks) and 384 x 16 (6144 rows: 32-row
