@@ -204,8 +204,9 @@ def traffic_record(workload: str, steps: int, warmup: int, bytes_per_launch: flo
 
 def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     """Average duration and algorithmic bytes of the decode-attention launches of steps
-    first..first+count-1, replayed on their own with HIP events on the launch stream
-    (packed chunks through the packed entry point, as the step launches them)."""
+    first..first+count-1, replayed on their own (each step's launches in a HIP graph, as the
+    step runs them) between HIP events on the launch stream (packed chunks through the packed
+    entry point, as the step launches them)."""
 
     from card_playing_gym_amd.nn.decode import (
         attention_into, attention_packed_into, attention_packed_order)
@@ -220,8 +221,6 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
     q_dtype = bench.cache.dtype if bench.chunks and bench.cache.dtype != torch.float32 else torch.float32
     q = torch.randn((tokens, H, D), device=dev, dtype=torch.float32).to(q_dtype)
     out = torch.empty((tokens, H, D), device=dev, dtype=torch.bfloat16)
-    key_lengths = torch.empty(games, dtype=torch.int64, device=dev)
-    rows = torch.empty(games, dtype=torch.int64, device=dev)
     # Packed chunks: the trunk computes each step's unit order once, before the layers
     # (longest units first): here before the timed launches.  Decode steps run unordered.
     orders = {}
@@ -230,34 +229,50 @@ def attention_roofline(bench: Bench, first: int, count: int) -> dict:
             orders[step] = attention_packed_order(
                 bench.cache.k[0], bench.rows_all[step], bench.positions_all[step], bench.seq_starts[step],
                 bench.plans[step].n_tokens, H, bench.max_len)
+    # Each step's launches are captured in a HIP graph of their own (as the step runs them,
+    # inside its graph), over that step's own rows and key lengths; the graphs are then
+    # replayed back to back between two events on the launch stream.
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(count)]
     total_bytes = 0
     itemsize = bench.cache.dtype.itemsize
+    graphs, held = [], []
     for i in range(count):
         step = first + i
         plan = bench.plans[step]
-        rows.copy_(bench.rows_all[step])
+        rows_i = bench.rows_all[step].clone()
         if bench.chunks:
-            key_lengths.copy_(bench.positions_all[step])
+            lengths_i = bench.positions_all[step].clone()
             n = plan.n_tokens
-            starts[i].record(stream)
-            for layer in range(cfg.n_layers):
-                attention_packed_into(out[:n], q[:n], bench.cache.k[layer], bench.cache.v[layer], rows, key_lengths,
-                                      bench.seq_starts[step], bench.max_len, D ** -0.5, orders[step])
+
+            def launches(step=step, n=n, rows_i=rows_i, lengths_i=lengths_i):
+                for layer in range(cfg.n_layers):
+                    attention_packed_into(out[:n], q[:n], bench.cache.k[layer], bench.cache.v[layer], rows_i,
+                                          lengths_i, bench.seq_starts[step], bench.max_len, D ** -0.5, orders[step])
         else:
-            key_lengths.copy_(bench.positions_all[step] + 1)
-            starts[i].record(stream)
-            for layer in range(cfg.n_layers):
-                attention_into(out.view(games, H, 1, D), q.view(games, H, 1, D), bench.cache.k[layer],
-                               bench.cache.v[layer], rows if bench.gathered else None, key_lengths, bench.max_len,
-                               D ** -0.5)
-        ends[i].record(stream)
+            lengths_i = bench.positions_all[step] + 1
+
+            def launches(rows_i=rows_i, lengths_i=lengths_i):
+                for layer in range(cfg.n_layers):
+                    attention_into(out.view(games, H, 1, D), q.view(games, H, 1, D), bench.cache.k[layer],
+                                   bench.cache.v[layer], rows_i if bench.gathered else None, lengths_i,
+                                   bench.max_len, D ** -0.5)
+        if i == 0:
+            launches()  # once eagerly, outside any capture
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            launches()
+        graphs.append(graph)
+        held.append((rows_i, lengths_i))
         kv = kv_bytes(plan, cfg.n_layers, cfg.n_kv_heads, D, itemsize)
         total_bytes += kv + cfg.n_layers * plan.n_tokens * H * D * (q.element_size() + 2)  # + q read + out write (bf16)
     torch.cuda.synchronize()
-    ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for graph in graphs:
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
     launches = count * cfg.n_layers
     avg_us = ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
